@@ -1,0 +1,73 @@
+"""ctypes binding of libanima_hip.so (declarations mirror include/anima_hip.h).
+
+The library is the only compute path: when it cannot be loaded this module
+raises instead of falling back to any CPU implementation.
+"""
+from __future__ import annotations
+
+import ctypes as ct
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libanima_hip.so")
+
+_P = ct.c_void_p
+_I = ct.c_int
+_F = ct.c_float
+_B = ct.c_bool
+_I64P = ct.POINTER(ct.c_int64)
+
+# name -> (restype, argtypes); every symbol declared in include/anima_hip.h.
+SIGNATURES = {
+    "anima_rt_init": (_B, []),
+    "anima_rt_destroy": (None, []),
+    "anima_rt_run_sdpa_flash": (_B, [_P] * 4 + [_I] * 4 + [_F, _B]),
+    "anima_rt_run_sdpa": (_B, [_P] * 4 + [_I] * 4 + [_F, _B]),
+    "anima_rt_run_rmsnorm": (_B, [_P, _P, _P, _I, _I, _F]),
+    "anima_rt_run_rope": (_B, [_P, _P, _P, _I, _I, _I]),
+    "anima_hip_last_error": (ct.c_char_p, []),
+    "anima_hip_version": (_I, []),
+    "anima_hip_flash_f32_dev": (_B, [_P] * 4 + [_I] * 5 + [_I64P] * 4 + [_F, _B, _P]),
+    "anima_hip_qk_prologue_dev": (_B, [_P] * 4 + [_I] * 4 + [_I64P] * 2 + [_F, _I, _P]),
+    "anima_hip_attention": (_B, [_P] * 7 + [_I] * 5 + [_F, _I]),
+}
+
+
+class AnimaHipError(RuntimeError):
+    """A libanima_hip entry point returned false."""
+
+
+_lib = None
+
+
+def load() -> ct.CDLL:
+    """Load libanima_hip.so once and declare every entry point."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise AnimaHipError(
+                f"{LIB_PATH} is missing; build it with `make -C anima-on-android_amd` "
+                "(or __graft_entry__.build())")
+        lib = ct.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    msg = load().anima_hip_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(ok: bool, what: str) -> None:
+    if not ok:
+        raise AnimaHipError(f"{what} failed: {last_error()}")
+
+
+def strides(s) -> object:
+    """int64[3] {batch, head, seq} element strides, or None for contiguous."""
+    if s is None:
+        return None
+    return (ct.c_int64 * 3)(*[int(x) for x in s])

@@ -1,0 +1,159 @@
+"""Torch-free host interface of the attention path, on numpy buffers.
+
+`AnimaRT` is a drop-in for the ``rt`` object NumpyDiT calls
+(``NumpyRT`` in scripts/phone_pipeline_nd.py:46-68): the same method names,
+argument meanings and array layouts, backed by libanima_hip.so on the GPU.
+One deliberate difference: a false return from the library raises
+`AnimaHipError` (the reference's ``run_sdpa`` ignores the return value,
+phone_pipeline_nd.py:67, and would hand back zeros).
+"""
+from __future__ import annotations
+
+import ctypes as ct
+import math
+
+import numpy as np
+
+from . import _lib
+
+F32 = 0
+BF16 = 1
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def init() -> None:
+    """anima_rt_init (anima_rt/src/anima_rt.cpp:13-20)."""
+    _lib.check(_lib.load().anima_rt_init(), "anima_rt_init")
+
+
+def destroy() -> None:
+    """anima_rt_destroy (anima_rt.cpp:166-171)."""
+    _lib.load().anima_rt_destroy()
+
+
+def sdpa_flash(q, k, v, scale=None, is_causal=False) -> np.ndarray:
+    """anima_rt_run_sdpa_flash on [BH,S,D] arrays (anima_rt.cpp:147-156)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    if k.shape != (BH, Sk, D) or v.shape != (BH, Sk, D):
+        raise ValueError(f"sdpa shapes q{q.shape} k{k.shape} v{v.shape}")
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    o = np.zeros((BH, Sq, D), np.float32)
+    ok = _lib.load().anima_rt_run_sdpa_flash(_p(q), _p(k), _p(v), _p(o), BH, Sq, Sk, D,
+                                             ct.c_float(scale), ct.c_bool(is_causal))
+    _lib.check(ok, "anima_rt_run_sdpa_flash")
+    return o
+
+
+def sdpa_math(q, k, v, scale=None, is_causal=False) -> np.ndarray:
+    """anima_rt_run_sdpa (anima_rt.cpp:78-141): the reference's math entry,
+    whose effective logit scale is scale**2.  Needs init() first."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    o = np.zeros((BH, Sq, D), np.float32)
+    ok = _lib.load().anima_rt_run_sdpa(_p(q), _p(k), _p(v), _p(o), BH, Sq, Sk, D,
+                                       ct.c_float(scale), ct.c_bool(is_causal))
+    _lib.check(ok, "anima_rt_run_sdpa")
+    return o
+
+
+def rmsnorm(x, w=None, eps=1e-6) -> np.ndarray:
+    """anima_rt_run_rmsnorm over the last axis (anima_rt.cpp:45-50). Needs init()."""
+    x = _f32(x)
+    D = x.shape[-1]
+    M = x.size // D if D else 0
+    w = None if w is None else _f32(w)
+    out = np.zeros_like(x)
+    ok = _lib.load().anima_rt_run_rmsnorm(_p(x), _p(w), _p(out), M, D, ct.c_float(eps))
+    _lib.check(ok, "anima_rt_run_rmsnorm")
+    return out
+
+
+def rope(t, freqs) -> np.ndarray:
+    """anima_rt_run_rope on t [N,S,D] with freqs [S,D/2,2,2] (anima_rt.cpp:160-164)."""
+    t = _f32(t)
+    N, S, D = t.shape
+    f = _f32(freqs)
+    if f.size != S * D * 2:
+        raise ValueError(f"freqs has {f.size} values, expected S*D*2 = {S * D * 2}")
+    out = np.zeros_like(t)
+    ok = _lib.load().anima_rt_run_rope(_p(t), _p(f), _p(out), N, S, D)
+    _lib.check(ok, "anima_rt_run_rope")
+    return out
+
+
+def attention(q, k, v, q_norm_w=None, k_norm_w=None, freqs=None, eps=1e-6,
+              mode=F32) -> np.ndarray:
+    """One call for the middle of NumpyAttention.forward
+    (anima_rt/scripts/numpy_dit.py:283-294): per-head RMSNorm of q and k,
+    RoPE when `freqs` is given (self-attention), SDPA with scale 1/sqrt(D),
+    on [B,S,H,D] projections.  Returns [B,S_q,H,D] float32, i.e. the
+    [B*S_q, H*D] input of output_proj without any host transposes."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    if k.shape != (B, Sk, H, D) or v.shape != (B, Sk, H, D):
+        raise ValueError(f"attention shapes q{q.shape} k{k.shape} v{v.shape}")
+    qw = None if q_norm_w is None else _f32(q_norm_w)
+    kw = None if k_norm_w is None else _f32(k_norm_w)
+    f = None if freqs is None else _f32(freqs)
+    out = np.zeros((B, Sq, H, D), np.float32)
+    ok = _lib.load().anima_hip_attention(_p(q), _p(k), _p(v), _p(qw), _p(kw), _p(f), _p(out),
+                                         B, Sq, Sk, H, D, ct.c_float(eps), int(mode))
+    _lib.check(ok, "anima_hip_attention")
+    return out
+
+
+class AnimaRT:
+    """Drop-in for NumpyDiT's ``rt`` (NumpyRT, scripts/phone_pipeline_nd.py:46-68).
+
+    ``norm_weights`` maps '<prefix>.weight' to float32 arrays, like NumpyRT's
+    ``nw``; ``run_rmsnorm(x, key)`` looks the weight up by key prefix.
+    """
+
+    def __init__(self, norm_weights=None):
+        init()
+        self._nw = dict(norm_weights or {})
+
+    def _w(self, key):
+        w = self._nw.get(key + ".weight")
+        return None if w is None else _f32(w)
+
+    def run_rmsnorm(self, x, key, eps=1e-6):
+        x = np.asarray(x, np.float32)
+        return rmsnorm(x, self._w(key), eps)
+
+    def run_sdpa(self, q, k, v):
+        """[B,H,S,D] q/k/v -> [B,H,S_q,D], scale 1/sqrt(D), non-causal."""
+        B, H, Sq, D = q.shape
+        Sk = k.shape[2]
+        o = sdpa_flash(np.asarray(q).reshape(B * H, Sq, D), np.asarray(k).reshape(B * H, Sk, D),
+                       np.asarray(v).reshape(B * H, Sk, D), scale=1.0 / math.sqrt(D))
+        return o.reshape(B, H, Sq, D)
+
+    def run_rope(self, t, freqs):
+        """[B,S,H,D] activations with an [S,D/2,2,2] table (rotate-half)."""
+        t = np.asarray(t, np.float32)
+        B, S, H, D = t.shape
+        flat = np.ascontiguousarray(t.transpose(0, 2, 1, 3)).reshape(B * H, S, D)
+        return rope(flat, freqs).reshape(B, H, S, D).transpose(0, 2, 1, 3)
+
+    def run_attention(self, q, k, v, prefix, rope_emb=None, mode=F32):
+        """NumpyAttention.forward's norm -> RoPE -> SDPA core for block `prefix`
+        on [B,S,H,D] projections (numpy_dit.py:283-294)."""
+        freqs = None if rope_emb is None else np.asarray(rope_emb, np.float32).reshape(
+            q.shape[1], q.shape[3] // 2, 2, 2)
+        return attention(q, k, v, self._w(f"{prefix}.q_norm"), self._w(f"{prefix}.k_norm"),
+                         freqs, mode=mode)

@@ -1,0 +1,445 @@
+// C-ABI layer of libanima_hip.so: argument checking, the device context
+// (device, stream, grow-only workspace) and host<->device marshaling for the
+// anima_rt drop-in entry points.  Kernels live in the other translation units.
+#include "common.h"
+
+#include "anima_hip.h"
+
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+namespace anima_hip {
+
+namespace {
+thread_local std::string t_last_error;
+}
+
+bool fail(const std::string &msg)
+{
+    t_last_error = msg;
+    return false;
+}
+
+bool hip_ok(hipError_t e, const char *what)
+{
+    if (e == hipSuccess)
+        return true;
+    return fail(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+namespace {
+
+// Grow-only device buffer.
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    bool reserve(size_t bytes, const char *what)
+    {
+        if (bytes <= cap)
+            return true;
+        if (p) {
+            (void)hipFree(p);
+            p = nullptr;
+            cap = 0;
+        }
+        const size_t want = std::max<size_t>(bytes, 256);
+        if (!hip_ok(hipMalloc(&p, want), what))
+            return false;
+        cap = want;
+        return true;
+    }
+    void release()
+    {
+        if (p)
+            (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+struct Runtime {
+    std::recursive_mutex mu;
+    bool ready = false;        // device + stream exist
+    bool user_init = false;    // anima_rt_init() succeeded (gates rmsnorm/math sdpa)
+    int device = 0;
+    hipStream_t stream = nullptr;
+    DevBuf q, k, v, o, w0, w1, fr, q2, k2, v2;
+};
+
+Runtime &rt()
+{
+    static Runtime r;
+    return r;
+}
+
+bool ensure_ready(Runtime &r)
+{
+    if (r.ready)
+        return true;
+    int n = 0;
+    if (!hip_ok(hipGetDeviceCount(&n), "hipGetDeviceCount"))
+        return false;
+    if (n <= 0)
+        return fail("no HIP device visible");
+    if (!hip_ok(hipGetDevice(&r.device), "hipGetDevice"))
+        return false;
+    if (!hip_ok(hipStreamCreateWithFlags(&r.stream, hipStreamNonBlocking), "hipStreamCreate"))
+        return false;
+    r.ready = true;
+    return true;
+}
+
+// Device entry points run on the caller's stream; NULL is HIP's default
+// (null) stream, as in other HIP libraries.
+hipStream_t pick_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+Strides contiguous(int H, int S, int D)
+{
+    return Strides{int64_t(H) * S * D, int64_t(S) * D, int64_t(D)};
+}
+
+Strides from_array(const int64_t *a, int H, int S, int D)
+{
+    return a ? Strides{a[0], a[1], a[2]} : contiguous(H, S, D);
+}
+
+bool check_dims(int B, int H, int S_q, int S_kv, int D)
+{
+    if (B < 0 || H < 0 || S_q < 0 || S_kv < 0 || D < 0)
+        return fail("negative dimension");
+    return true;
+}
+
+size_t f32_bytes(int64_t n) { return size_t(n) * sizeof(float); }
+
+bool h2d(void *dst, const void *src, size_t n, hipStream_t st)
+{
+    return n == 0 || hip_ok(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, st), "H2D copy");
+}
+
+bool d2h(void *dst, const void *src, size_t n, hipStream_t st)
+{
+    return n == 0 || hip_ok(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, st), "D2H copy");
+}
+
+bool sync(hipStream_t st) { return hip_ok(hipStreamSynchronize(st), "hipStreamSynchronize"); }
+
+// Shared body of the two host-pointer SDPA entries.
+bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int BH, int S_q,
+               int S_kv, int D, float scale, bool causal)
+{
+    if (!check_dims(1, BH, S_q, S_kv, D))
+        return false;
+    const int64_t nq = int64_t(BH) * S_q * D, nk = int64_t(BH) * S_kv * D;
+    if (nq == 0)
+        return true;
+    if (!Q || !out || (nk > 0 && (!K || !V)))
+        return fail("sdpa: null pointer");
+    Runtime &r = rt();
+    const hipStream_t st = r.stream;
+    if (!r.q.reserve(f32_bytes(nq), "workspace Q") || !r.o.reserve(f32_bytes(nq), "workspace O") ||
+        !r.k.reserve(f32_bytes(nk), "workspace K") || !r.v.reserve(f32_bytes(nk), "workspace V"))
+        return false;
+    if (!h2d(r.q.p, Q, f32_bytes(nq), st) || !h2d(r.k.p, K, f32_bytes(nk), st) ||
+        !h2d(r.v.p, V, f32_bytes(nk), st))
+        return false;
+    FlashProblem p;
+    p.q = r.q.p;
+    p.k = r.k.p;
+    p.v = r.v.p;
+    p.o = static_cast<float *>(r.o.p);
+    p.qs = p.os = contiguous(BH, S_q, D);
+    p.ks = p.vs = contiguous(BH, S_kv, D);
+    p.B = 1;
+    p.H = BH;
+    p.S_q = S_q;
+    p.S_kv = S_kv;
+    p.D = D;
+    p.scale = scale;
+    p.causal = causal;
+    if (!launch_flash_f32(p, st))
+        return false;
+    if (!d2h(out, r.o.p, f32_bytes(nq), st))
+        return false;
+    return sync(st);
+}
+
+}  // namespace
+}  // namespace anima_hip
+
+using namespace anima_hip;
+
+extern "C" {
+
+bool anima_rt_init(void)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!ensure_ready(r))
+        return false;
+    r.user_init = true;
+    return true;
+}
+
+void anima_rt_destroy(void)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!r.ready)
+        return;
+    (void)hipStreamSynchronize(r.stream);
+    for (DevBuf *b : {&r.q, &r.k, &r.v, &r.o, &r.w0, &r.w1, &r.fr, &r.q2, &r.k2, &r.v2})
+        b->release();
+    (void)hipStreamDestroy(r.stream);
+    r.stream = nullptr;
+    r.ready = false;
+    r.user_init = false;
+}
+
+bool anima_rt_run_sdpa_flash(const float *Q, const float *K, const float *V, float *out, int BH,
+                             int S_q, int S_kv, int D, float scale, bool is_causal)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!ensure_ready(r))
+        return false;
+    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale, is_causal);
+}
+
+bool anima_rt_run_sdpa(const float *Q, const float *K, const float *V, float *out, int BH,
+                       int S_q, int S_kv, int D, float scale, bool is_causal)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!r.user_init)
+        return fail("anima_rt_run_sdpa: anima_rt_init() has not been called");
+    // The reference multiplies both Q and K by `scale`: softmax(scale^2 QK^T)V.
+    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale * scale, is_causal);
+}
+
+bool anima_rt_run_rmsnorm(const float *x, const float *w, float *out, int m, int d, float eps)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!r.user_init)
+        return fail("anima_rt_run_rmsnorm: anima_rt_init() has not been called");
+    if (m < 0 || d < 0)
+        return fail("rmsnorm: negative dimension");
+    const int64_t n = int64_t(m) * d;
+    if (n == 0)
+        return true;
+    if (!x || !out)
+        return fail("rmsnorm: null pointer");
+    const hipStream_t st = r.stream;
+    if (!r.q.reserve(f32_bytes(n), "workspace x") || !r.o.reserve(f32_bytes(n), "workspace y"))
+        return false;
+    if (w && !r.w0.reserve(f32_bytes(d), "workspace w"))
+        return false;
+    if (!h2d(r.q.p, x, f32_bytes(n), st) || (w && !h2d(r.w0.p, w, f32_bytes(d), st)))
+        return false;
+    RowProblem p;
+    p.x = static_cast<const float *>(r.q.p);
+    p.out = r.o.p;
+    p.w = w ? static_cast<const float *>(r.w0.p) : nullptr;
+    p.freqs = nullptr;
+    p.xs = p.os = Strides{0, 0, int64_t(d)};
+    p.B = 1;
+    p.S = m;
+    p.H = 1;
+    p.D = d;
+    p.eps = eps;
+    p.norm = true;
+    p.out_bf16 = false;
+    if (!launch_rows(p, st) || !d2h(out, r.o.p, f32_bytes(n), st))
+        return false;
+    return sync(st);
+}
+
+bool anima_rt_run_rope(const float *t, const float *freqs, float *out, int N, int S, int D)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!ensure_ready(r))
+        return false;
+    if (N < 0 || S < 0 || D < 0)
+        return fail("rope: negative dimension");
+    const int64_t n = int64_t(N) * S * D, nf = int64_t(S) * D * 2;
+    if (n == 0)
+        return true;
+    if (!t || !freqs || !out)
+        return fail("rope: null pointer");
+    const hipStream_t st = r.stream;
+    if (!r.q.reserve(f32_bytes(n), "workspace t") || !r.o.reserve(f32_bytes(n), "workspace out") ||
+        !r.fr.reserve(f32_bytes(nf), "workspace freqs"))
+        return false;
+    if (!h2d(r.q.p, t, f32_bytes(n), st) || !h2d(r.fr.p, freqs, f32_bytes(nf), st))
+        return false;
+    RowProblem p;
+    p.x = static_cast<const float *>(r.q.p);
+    p.out = r.o.p;
+    p.w = nullptr;
+    p.freqs = static_cast<const float *>(r.fr.p);
+    p.xs = p.os = Strides{int64_t(S) * D, 0, int64_t(D)};
+    p.B = N;
+    p.S = S;
+    p.H = 1;
+    p.D = D;
+    p.eps = 0.0f;
+    p.norm = false;
+    p.out_bf16 = false;
+    if (!launch_rows(p, st) || !d2h(out, r.o.p, f32_bytes(n), st))
+        return false;
+    return sync(st);
+}
+
+const char *anima_hip_last_error(void) { return t_last_error.c_str(); }
+
+int anima_hip_version(void) { return 100; }
+
+bool anima_hip_flash_f32_dev(const float *q, const float *k, const float *v, float *o, int B,
+                             int H, int S_q, int S_kv, int D, const int64_t *q_strides,
+                             const int64_t *k_strides, const int64_t *v_strides,
+                             const int64_t *o_strides, float scale, bool is_causal, void *stream)
+{
+    Runtime &r = rt();
+    {
+        std::lock_guard<std::recursive_mutex> g(r.mu);
+        if (!ensure_ready(r))
+            return false;
+    }
+    if (!check_dims(B, H, S_q, S_kv, D))
+        return false;
+    if (int64_t(B) * H * S_q * D > 0 && (!q || !o || (S_kv > 0 && (!k || !v))))
+        return fail("flash_f32_dev: null pointer");
+    FlashProblem p;
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.o = o;
+    p.qs = from_array(q_strides, H, S_q, D);
+    p.ks = from_array(k_strides, H, S_kv, D);
+    p.vs = from_array(v_strides, H, S_kv, D);
+    p.os = from_array(o_strides, H, S_q, D);
+    p.B = B;
+    p.H = H;
+    p.S_q = S_q;
+    p.S_kv = S_kv;
+    p.D = D;
+    p.scale = scale;
+    p.causal = is_causal;
+    return launch_flash_f32(p, pick_stream(stream));
+}
+
+bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const float *freqs,
+                               int B, int S, int H, int D, const int64_t *x_strides,
+                               const int64_t *out_strides, float eps, int flags, void *stream)
+{
+    Runtime &r = rt();
+    {
+        std::lock_guard<std::recursive_mutex> g(r.mu);
+        if (!ensure_ready(r))
+            return false;
+    }
+    if (B < 0 || S < 0 || H < 0 || D < 0)
+        return fail("qk_prologue: negative dimension");
+    if (int64_t(B) * S * H * D > 0 && (!x || !out))
+        return fail("qk_prologue: null pointer");
+    RowProblem p;
+    p.x = x;
+    p.out = out;
+    p.w = w;
+    p.freqs = freqs;
+    // x/out stride arrays describe [B, H, S, D] views, like the attention ones.
+    p.xs = from_array(x_strides, H, S, D);
+    p.os = from_array(out_strides, H, S, D);
+    p.B = B;
+    p.S = S;
+    p.H = H;
+    p.D = D;
+    p.eps = eps;
+    p.norm = (flags & 1) != 0;
+    p.out_bf16 = (flags & 2) != 0;
+    return launch_rows(p, pick_stream(stream));
+}
+
+bool anima_hip_attention(const float *q, const float *k, const float *v, const float *q_norm_w,
+                         const float *k_norm_w, const float *freqs, float *out, int B, int S_q,
+                         int S_kv, int H, int D, float eps, int mode)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!ensure_ready(r))
+        return false;
+    if (!check_dims(B, H, S_q, S_kv, D))
+        return false;
+    if (mode != ANIMA_HIP_F32)
+        return fail("anima_hip_attention: mode " + std::to_string(mode) + " is not available");
+    if (freqs && S_q != S_kv)
+        return fail("anima_hip_attention: RoPE needs S_q == S_kv (self-attention)");
+    const int64_t nq = int64_t(B) * S_q * H * D, nk = int64_t(B) * S_kv * H * D;
+    if (nq == 0)
+        return true;
+    if (!q || !out || (nk > 0 && (!k || !v)))
+        return fail("anima_hip_attention: null pointer");
+    const hipStream_t st = r.stream;
+    const int64_t nf = freqs ? int64_t(S_q) * D * 2 : 0;
+    if (!r.q.reserve(f32_bytes(nq), "workspace q") || !r.k.reserve(f32_bytes(nk), "workspace k") ||
+        !r.v.reserve(f32_bytes(nk), "workspace v") || !r.o.reserve(f32_bytes(nq), "workspace o") ||
+        !r.q2.reserve(f32_bytes(nq), "workspace q'") || !r.k2.reserve(f32_bytes(nk), "workspace k'"))
+        return false;
+    if ((q_norm_w && !r.w0.reserve(f32_bytes(D), "workspace q_norm")) ||
+        (k_norm_w && !r.w1.reserve(f32_bytes(D), "workspace k_norm")) ||
+        (nf && !r.fr.reserve(f32_bytes(nf), "workspace freqs")))
+        return false;
+    if (!h2d(r.q.p, q, f32_bytes(nq), st) || !h2d(r.k.p, k, f32_bytes(nk), st) ||
+        !h2d(r.v.p, v, f32_bytes(nk), st) ||
+        (q_norm_w && !h2d(r.w0.p, q_norm_w, f32_bytes(D), st)) ||
+        (k_norm_w && !h2d(r.w1.p, k_norm_w, f32_bytes(D), st)) ||
+        (nf && !h2d(r.fr.p, freqs, f32_bytes(nf), st)))
+        return false;
+    // [B, S, H, D] viewed as [B, H, S, D]: strides {S*H*D, D, H*D}.
+    const Strides qv{int64_t(S_q) * H * D, int64_t(D), int64_t(H) * D};
+    const Strides kv{int64_t(S_kv) * H * D, int64_t(D), int64_t(H) * D};
+    RowProblem pq;
+    pq.x = static_cast<const float *>(r.q.p);
+    pq.out = r.q2.p;
+    pq.w = q_norm_w ? static_cast<const float *>(r.w0.p) : nullptr;
+    pq.freqs = nf ? static_cast<const float *>(r.fr.p) : nullptr;
+    pq.xs = pq.os = qv;
+    pq.B = B;
+    pq.S = S_q;
+    pq.H = H;
+    pq.D = D;
+    pq.eps = eps;
+    pq.norm = true;
+    pq.out_bf16 = false;
+    RowProblem pk = pq;
+    pk.x = static_cast<const float *>(r.k.p);
+    pk.out = r.k2.p;
+    pk.w = k_norm_w ? static_cast<const float *>(r.w1.p) : nullptr;
+    pk.xs = pk.os = kv;
+    pk.S = S_kv;
+    if (!launch_rows(pq, st) || !launch_rows(pk, st))
+        return false;
+    FlashProblem p;
+    p.q = r.q2.p;
+    p.k = r.k2.p;
+    p.v = r.v.p;
+    p.o = static_cast<float *>(r.o.p);
+    p.qs = p.os = qv;
+    p.ks = p.vs = kv;
+    p.B = B;
+    p.H = H;
+    p.S_q = S_q;
+    p.S_kv = S_kv;
+    p.D = D;
+    p.scale = float(1.0 / std::sqrt(double(D)));  // as NumpyRT.run_sdpa passes it
+    p.causal = false;
+    if (!launch_flash_f32(p, st) || !d2h(out, r.o.p, f32_bytes(nq), st))
+        return false;
+    return sync(st);
+}
+
+}  // extern "C"

@@ -1,0 +1,57 @@
+// Shared declarations of libanima_hip: launch descriptors, error reporting
+// and the kernel launchers each translation unit exports to the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <string>
+
+namespace anima_hip {
+
+// Record an error message for anima_hip_last_error(); always returns false so
+// callers can `return fail(...)`.
+bool fail(const std::string &msg);
+// Check a HIP status; on error record "<what>: <hip error string>".
+bool hip_ok(hipError_t e, const char *what);
+
+// Element strides (in elements, not bytes) of a 4-D [B, H, S, D] view whose D
+// axis is contiguous.  Stride 0 on the batch axis broadcasts one batch entry
+// to every batch (used for a shared text context).
+struct Strides {
+    int64_t b, h, s;
+};
+
+// Everything the attention kernels need; pointers are device pointers.
+struct FlashProblem {
+    const void *q, *k, *v;  // f32 or bf16 (see kernel)
+    float *o;
+    Strides qs, ks, vs, os;
+    int B, H, S_q, S_kv, D;
+    float scale;       // softmax scale applied to q.k
+    bool causal;       // mask key j > query i (top-left aligned, like anima_rt)
+};
+
+// f32 inputs, f32 MFMA (D == 128) or the generic kernel (any D <= 1024).
+bool launch_flash_f32(const FlashProblem &p, hipStream_t st);
+// True when launch_flash_f32 would take the MFMA path for this problem.
+bool flash_f32_fast_path(const FlashProblem &p);
+
+// Per-row RMSNorm (+ optional RoPE) "prologue".
+//   x:   rows indexed (b, s, h) through `xs` (D contiguous), f32
+//   out: same indexing through `os`, f32 or bf16 (out_bf16)
+//   w:   [D] weight or nullptr; freqs: [S, D/2, 2, 2] rotate-half table or nullptr
+// Arithmetic follows the reference's serial order exactly (see prologue.hip).
+struct RowProblem {
+    const float *x;
+    void *out;
+    const float *w;
+    const float *freqs;
+    Strides xs, os;
+    int B, S, H, D;
+    float eps;
+    bool norm;      // apply RMSNorm
+    bool out_bf16;  // write bf16 (round to nearest even) instead of f32
+};
+bool launch_rows(const RowProblem &p, hipStream_t st);
+
+}  // namespace anima_hip

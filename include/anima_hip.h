@@ -1,0 +1,121 @@
+/*
+ * anima_hip.h -- C-ABI of libanima_hip.so, the MI355X (gfx950) attention path
+ * of the Anima 2B DiT.
+ *
+ * Part 1 is a drop-in for the anima_rt symbols that the torch-free NumpyDiT
+ * host path binds through ctypes (anima_rt/scripts/anima_rt_ops.py:10-36,
+ * scripts/phone_pipeline_nd.py:46-68): same names, same argument meaning,
+ * host pointers, synchronous, bool result.  Part 2 adds device-pointer entry
+ * points, the fused Q/K prologue, a one-call NumpyAttention core and the
+ * cross-attention context K/V cache.
+ *
+ * Conventions
+ *   - All tensors are row-major with the innermost axis contiguous.
+ *   - A false return means nothing useful was written; the reason is
+ *     available from anima_hip_last_error() (per calling thread).
+ *   - Host-pointer entry points (Part 1, anima_hip_attention*,
+ *     anima_hip_ctx_kv_create) copy to the GPU, run, copy back and return
+ *     when the output is complete.  They are serialised by a library mutex.
+ *   - "_dev" entry points take device pointers and a hipStream_t (passed as
+ *     void*; NULL = HIP's default stream) and are asynchronous: they only
+ *     enqueue work on that stream.
+ *   - Stride arrays are int64[3] = {batch, head, sequence} element strides of
+ *     a [B, H, S, D] view (D contiguous).  NULL means contiguous [B,H,S,D].
+ *     A batch stride of 0 broadcasts batch entry 0 to every batch.
+ */
+#ifndef ANIMA_HIP_H
+#define ANIMA_HIP_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===================== Part 1: anima_rt drop-in ===================== */
+
+/* Replaces anima_rt_init (anima_rt/src/anima_rt.cpp:13-20).  Binds the
+ * current HIP device and creates the library's stream.  Idempotent; returns
+ * false when no GPU is usable. */
+bool anima_rt_init(void);
+
+/* Replaces anima_rt_destroy (anima_rt.cpp:166-171).  Frees the workspace and
+ * the stream; a later call to any entry point may initialise again. */
+void anima_rt_destroy(void);
+
+/* Replaces anima_rt_run_sdpa_flash (anima_rt.cpp:147-156).
+ * Q,out: [BH, S_q, D]; K,V: [BH, S_kv, D]; fp32 host memory.
+ * out = softmax(scale * Q K^T [masked j > i when is_causal]) V.
+ * Like the reference, works without a prior anima_rt_init. */
+bool anima_rt_run_sdpa_flash(const float *Q, const float *K, const float *V, float *out,
+                             int BH, int S_q, int S_kv, int D, float scale, bool is_causal);
+
+/* Replaces anima_rt_run_sdpa (anima_rt.cpp:78-141), the "math" entry.  The
+ * reference scales both Q and K by `scale` (anima_rt.cpp:95-98), so it
+ * computes softmax(scale^2 * Q K^T) V; this entry keeps that result so
+ * existing callers see the same numbers.  Returns false unless
+ * anima_rt_init() succeeded first (anima_rt.cpp:84). */
+bool anima_rt_run_sdpa(const float *Q, const float *K, const float *V, float *out,
+                       int BH, int S_q, int S_kv, int D, float scale, bool is_causal);
+
+/* Replaces anima_rt_run_rmsnorm (anima_rt.cpp:45-50 -> rmsnorm_kernel,
+ * anima_rt/include/cpu/rmsnorm_kernel.h:11-31).  x,out: [m, d]; w: [d] or
+ * NULL.  Bit-identical to the reference.  Returns false unless anima_rt_init()
+ * succeeded first (anima_rt.cpp:47). */
+bool anima_rt_run_rmsnorm(const float *x, const float *w, float *out, int m, int d, float eps);
+
+/* Replaces anima_rt_run_rope (anima_rt.cpp:160-164 -> rope_kernel,
+ * anima_rt/include/cpu/rope_kernel.h:65-97).  t,out: [N, S, D];
+ * freqs: [S, D/2, 2, 2].  Bit-identical to the reference. */
+bool anima_rt_run_rope(const float *t, const float *freqs, float *out, int N, int S, int D);
+
+/* ===================== Part 2: extensions ===================== */
+
+/* Message describing the last failure on this thread ("" if none). */
+const char *anima_hip_last_error(void);
+
+/* ABI version of this header (major*100 + minor). */
+int anima_hip_version(void);
+
+/* Attention arithmetic modes. */
+enum {
+    ANIMA_HIP_F32 = 0,  /* f32 inputs, f32 MFMA, f32 accumulate            */
+    ANIMA_HIP_BF16 = 1  /* bf16 Q/K/V and P, f32 MFMA accumulate + softmax */
+};
+
+/* Flash attention on device f32 tensors (mode ANIMA_HIP_F32).  Same math as
+ * anima_rt_run_sdpa_flash with strided [B,H,S,D] views. */
+bool anima_hip_flash_f32_dev(const float *q, const float *k, const float *v, float *o,
+                             int B, int H, int S_q, int S_kv, int D,
+                             const int64_t *q_strides, const int64_t *k_strides,
+                             const int64_t *v_strides, const int64_t *o_strides,
+                             float scale, bool is_causal, void *stream);
+
+/* Fused per-row prologue on device memory: for each row (b, s, h) of x,
+ * optional RMSNorm (flags & 1; weight w may be NULL) followed by optional
+ * rotate-half RoPE (freqs [S, D/2, 2, 2] or NULL), written through
+ * out_strides as f32 or, with flags & 2, bf16 (round to nearest even).
+ * This is NumpyAttention.forward's q/k path (anima_rt/scripts/numpy_dit.py:285-291):
+ * RMSNorm (numpy_dit.py:285-286) -> RoPE (:288-289) -> transpose (:291). */
+bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const float *freqs,
+                               int B, int S, int H, int D,
+                               const int64_t *x_strides, const int64_t *out_strides,
+                               float eps, int flags, void *stream);
+
+/* One-call core of NumpyAttention.forward (numpy_dit.py:283-294) on host
+ * memory: q [B,S_q,H,D], k/v [B,S_kv,H,D] (the projections), optional
+ * per-head RMSNorm weights [D], optional RoPE table [S_q, D/2, 2, 2]
+ * (self-attention only; requires S_q == S_kv), scale 1/sqrt(D), no mask.
+ * Writes out [B,S_q,H,D], i.e. the [B*S_q, H*D] input of output_proj.
+ * mode: ANIMA_HIP_F32 or ANIMA_HIP_BF16. */
+bool anima_hip_attention(const float *q, const float *k, const float *v,
+                         const float *q_norm_w, const float *k_norm_w, const float *freqs,
+                         float *out, int B, int S_q, int S_kv, int H, int D, float eps,
+                         int mode);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ANIMA_HIP_H */

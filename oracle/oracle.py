@@ -1,0 +1,388 @@
+"""CPU oracle for the Anima DiT attention hot path.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker.  The product (``anima_hip`` + ``libanima_hip.so``) never imports it
+and has no CPU fallback.
+
+Contents
+  * ctypes wrappers over ``liboracle.so`` (``anima_oracle.c``): the plain-C
+    restatement of anima_rt's flash SDPA, math SDPA, RMSNorm, RoPE and bf16
+    GEMM, bit-identical to the reference runtime.
+  * ctypes wrappers over ``_ref/libanima_rt_ref.so``: the reference runtime
+    itself, compiled from its sources (present only where it was built).
+  * numpy restatements of the NumpyDiT host pieces: the 3D RoPE table
+    (anima_rt/scripts/numpy_dit.py:48-60), the rotate-half application
+    (numpy_dit.py:33-37) and the attention dataflow of
+    NumpyAttention.forward (numpy_dit.py:268-297).
+  * fp64 brute-force SDPA / RMSNorm / RoPE used to pin the above.
+
+Pinning status (each function is checked by something other than itself):
+  flash_sdpa, math_sdpa, rmsnorm, rope -- bit-identical to the compiled
+      reference (tests/test_oracle_ref.py) and to fp64 closed forms.
+  rope_freqs -- closed form in fp64 (angle = pos * theta^(-2j/dim)), the
+      [cos,-sin,sin,cos] entry layout, identity on temporal pairs for T=1,
+      and the reference's D=4 known-answer test; bit-for-bit equality with
+      numpy_dit.py's float32 rounding is "parity unpinned" (would need an
+      import of the reference) and is covered only to 1 ulp-level tolerance.
+  numpy_rope -- same arithmetic as rope (checked bit-identical against it).
+"""
+from __future__ import annotations
+
+import ctypes as _ct
+import math
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libanima_rt_ref.so")
+
+_P = _ct.c_void_p
+_I = _ct.c_int
+_F = _ct.c_float
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _f32c(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+_oracle_lib = None
+_ref_lib = None
+
+
+def oracle_lib():
+    """Load liboracle.so (built by `make -C oracle`)."""
+    global _oracle_lib
+    if _oracle_lib is None:
+        if not os.path.exists(ORACLE_SO):
+            raise FileNotFoundError(f"{ORACLE_SO} missing: run `make -C oracle`")
+        lib = _ct.CDLL(ORACLE_SO)
+        sig = [_P] * 4 + [_I] * 4 + [_F, _I]
+        lib.oracle_flash_attention.argtypes = sig
+        lib.oracle_flash_attention.restype = _I
+        lib.oracle_flash_attention_mt.argtypes = sig + [_I]
+        lib.oracle_flash_attention_mt.restype = _I
+        lib.oracle_sdpa_math.argtypes = sig
+        lib.oracle_sdpa_math.restype = _I
+        lib.oracle_rmsnorm.argtypes = [_P, _P, _P, _ct.c_int64, _ct.c_int64, _F]
+        lib.oracle_rmsnorm.restype = None
+        lib.oracle_rope.argtypes = [_P, _P, _P, _I, _I, _I]
+        lib.oracle_rope.restype = None
+        lib.oracle_gemm_bf16.argtypes = [_P, _P, _P, _I, _I, _I]
+        lib.oracle_gemm_bf16.restype = None
+        lib.oracle_f32_to_bf16.argtypes = [_F]
+        lib.oracle_f32_to_bf16.restype = _ct.c_uint16
+        _oracle_lib = lib
+    return _oracle_lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_SO)
+
+
+def ref_lib():
+    """Load the reference runtime compiled from its own sources (oracle/_ref)."""
+    global _ref_lib
+    if _ref_lib is None:
+        lib = _ct.CDLL(REF_SO)
+        sig = [_P] * 4 + [_I] * 4 + [_F, _ct.c_bool]
+        lib.anima_rt_init.restype = _ct.c_bool
+        lib.anima_rt_run_sdpa_flash.argtypes = sig
+        lib.anima_rt_run_sdpa_flash.restype = _ct.c_bool
+        lib.anima_rt_run_sdpa.argtypes = sig
+        lib.anima_rt_run_sdpa.restype = _ct.c_bool
+        lib.anima_rt_run_rmsnorm.argtypes = [_P, _P, _P, _I, _I, _F]
+        lib.anima_rt_run_rmsnorm.restype = _ct.c_bool
+        lib.anima_rt_run_rope.argtypes = [_P, _P, _P, _I, _I, _I]
+        lib.anima_rt_run_rope.restype = _ct.c_bool
+        lib.anima_rt_run_gemm_bf16.argtypes = [_P, _P, _P, _I, _I, _I]
+        lib.anima_rt_run_gemm_bf16.restype = _ct.c_bool
+        if not lib.anima_rt_init():
+            raise RuntimeError("reference anima_rt_init failed")
+        _ref_lib = lib
+    return _ref_lib
+
+
+# ---------------------------------------------------------------- C oracle
+
+def flash_sdpa(q, k, v, scale=None, is_causal=False, threads=1):
+    """anima_rt flash SDPA restated (flash_attention.h:55-208).
+
+    q: [BH,Sq,D], k/v: [BH,Sk,D] float32.  Returns [BH,Sq,D] float32."""
+    q, k, v = _f32c(q), _f32c(k), _f32c(v)
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o = np.zeros((BH, Sq, D), np.float32)
+    lib = oracle_lib()
+    if threads > 1:
+        ok = lib.oracle_flash_attention_mt(_ptr(q), _ptr(k), _ptr(v), _ptr(o), BH, Sq, Sk,
+                                           D, scale, int(is_causal), int(threads))
+    else:
+        ok = lib.oracle_flash_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(o), BH, Sq, Sk, D,
+                                        scale, int(is_causal))
+    if not ok:
+        raise MemoryError("oracle_flash_attention failed")
+    return o
+
+
+def math_sdpa(q, k, v, scale=None, is_causal=False):
+    """anima_rt math SDPA restated (anima_rt.cpp:78-141): softmax(scale^2 QK^T) V."""
+    q, k, v = _f32c(q), _f32c(k), _f32c(v)
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o = np.zeros((BH, Sq, D), np.float32)
+    if not oracle_lib().oracle_sdpa_math(_ptr(q), _ptr(k), _ptr(v), _ptr(o), BH, Sq, Sk, D,
+                                         scale, int(is_causal)):
+        raise MemoryError("oracle_sdpa_math failed")
+    return o
+
+
+def rmsnorm(x, w=None, eps=1e-6):
+    """RMSNorm over the last axis restated (rmsnorm_kernel.h:11-31)."""
+    x = _f32c(x)
+    D = x.shape[-1]
+    M = x.size // D
+    y = np.empty_like(x)
+    wp = None
+    if w is not None:
+        w = _f32c(w)
+        wp = _ptr(w)
+    oracle_lib().oracle_rmsnorm(_ptr(x), wp, _ptr(y), M, D, eps)
+    return y
+
+
+def rope(t, freqs):
+    """Rotate-half RoPE restated (rope_kernel.h:65-97). t: [N,S,D], freqs: [S,D/2,2,2]."""
+    t = _f32c(t)
+    N, S, D = t.shape
+    f = _f32c(freqs).reshape(S, D // 2, 2, 2)
+    out = np.empty_like(t)
+    oracle_lib().oracle_rope(_ptr(t), _ptr(f), _ptr(out), N, S, D)
+    return out
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """Round fp32 to bf16 (nearest-even), returning the uint16 bit patterns
+    (gemm_backend.cpp:77-85), vectorised."""
+    b = _f32c(x).view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFFFFFF
+    return (b >> 16).astype(np.uint16)
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    """bf16 bits -> fp32 by a 16-bit shift (phone_pipeline_nd.py:38-40)."""
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def gemm_bf16(a, w_bits):
+    """C = A . W^T with bf16 W (gemm_backend.cpp:117-131)."""
+    a = _f32c(a)
+    w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    M, K = a.shape
+    N = w_bits.shape[0]
+    c = np.empty((M, N), np.float32)
+    oracle_lib().oracle_gemm_bf16(_ptr(a), _ptr(w_bits), _ptr(c), M, N, K)
+    return c
+
+
+# ------------------------------------------------------- reference runtime
+
+def ref_flash_sdpa(q, k, v, scale=None, is_causal=False):
+    q, k, v = _f32c(q), _f32c(k), _f32c(v)
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o = np.zeros((BH, Sq, D), np.float32)
+    assert ref_lib().anima_rt_run_sdpa_flash(_ptr(q), _ptr(k), _ptr(v), _ptr(o), BH, Sq, Sk,
+                                             D, scale, bool(is_causal))
+    return o
+
+
+def ref_math_sdpa(q, k, v, scale=None, is_causal=False):
+    q, k, v = _f32c(q), _f32c(k), _f32c(v)
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o = np.zeros((BH, Sq, D), np.float32)
+    assert ref_lib().anima_rt_run_sdpa(_ptr(q), _ptr(k), _ptr(v), _ptr(o), BH, Sq, Sk, D,
+                                       scale, bool(is_causal))
+    return o
+
+
+def ref_rmsnorm(x, w=None, eps=1e-6):
+    x = _f32c(x)
+    D = x.shape[-1]
+    M = x.size // D
+    y = np.zeros_like(x)
+    wp = None
+    if w is not None:
+        w = _f32c(w)
+        wp = _ptr(w)
+    assert ref_lib().anima_rt_run_rmsnorm(_ptr(x), wp, _ptr(y), M, D, eps)
+    return y
+
+
+def ref_rope(t, freqs):
+    t = _f32c(t)
+    N, S, D = t.shape
+    f = _f32c(freqs)
+    out = np.zeros_like(t)
+    assert ref_lib().anima_rt_run_rope(_ptr(t), _ptr(f), _ptr(out), N, S, D)
+    return out
+
+
+def ref_gemm_bf16(a, w_bits):
+    a = _f32c(a)
+    w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    M, K = a.shape
+    N = w_bits.shape[0]
+    c = np.zeros((M, N), np.float32)
+    assert ref_lib().anima_rt_run_gemm_bf16(_ptr(a), _ptr(w_bits), _ptr(c), M, N, K)
+    return c
+
+
+# --------------------------------------------------------- numpy host side
+
+def rope_freqs(H: int, W: int, T: int = 1, head_dim: int = 128) -> np.ndarray:
+    """3D RoPE table [T*H*W, head_dim/2, 2, 2] as NumpyDiT builds it
+    (anima_rt/scripts/numpy_dit.py:48-60, mirroring
+    src/position_embedding.py:100-163).
+
+    Pair ranges: the first dim_t/2 pairs rotate with the frame index, the next
+    dim_h/2 with the row index and the last dim_w/2 with the column index,
+    where dim_h = dim_w = head_dim//6*2 and dim_t = head_dim - 2*dim_h.  The
+    spatial bases are 1e4 * 4^(dim/(dim-2)) (NTK extrapolation ratio 4), the
+    temporal base 1e4.  Every entry is [cos a, -sin a, sin a, cos a] with
+    a = position * base^(-2j/dim).  Token order is (t, h, w) row-major.
+    All arithmetic is numpy float32 like the reference's host code."""
+    dh = head_dim // 6 * 2
+    dw = dh
+    dt = head_dim - 2 * dh
+    ntk_h = 4.0 ** (dh / (dh - 2))
+    ntk_w = 4.0 ** (dw / (dw - 2))
+
+    def inv_freq(base, dim):
+        expo = np.arange(0, dim, 2, dtype=np.float32)[: dim // 2] / dim
+        return 1.0 / (base ** expo)
+
+    fh = inv_freq(10000.0 * ntk_h, dh)
+    fw = inv_freq(10000.0 * ntk_w, dw)
+    ft = inv_freq(10000.0, dt)
+
+    def rot(angle):
+        c, s = np.cos(angle), np.sin(angle)
+        return np.stack([c, -s, s, c], axis=-1)
+
+    ang_t = np.outer(np.arange(T, dtype=np.float32), ft)
+    ang_h = np.outer(np.arange(H, dtype=np.float32), fh)
+    ang_w = np.outer(np.arange(W, dtype=np.float32), fw)
+    npair = head_dim // 2
+    table = np.empty((T, H, W, npair, 4), np.float32)
+    nt, nh = dt // 2, dh // 2
+    table[:, :, :, :nt] = rot(ang_t)[:, None, None]
+    table[:, :, :, nt:nt + nh] = rot(ang_h)[None, :, None]
+    table[:, :, :, nt + nh:] = rot(ang_w)[None, None, :]
+    return table.reshape(T * H * W, npair, 2, 2)
+
+
+def numpy_rope(x, freqs):
+    """Rotate-half RoPE on [..., S, H, D] activations with an [S, D/2, 2, 2]
+    table, float32, products then one add per output
+    (numpy_dit.py:33-37 == predict2.apply_rotary_pos_emb)."""
+    x = np.asarray(x, np.float32)
+    D = x.shape[-1]
+    h = D // 2
+    S = x.shape[-3]
+    f = np.asarray(freqs, np.float32).reshape(S, h, 2, 2)[:, None]  # [S,1,h,2,2]
+    a, b = x[..., :h], x[..., h:]
+    out = np.empty_like(x)
+    out[..., :h] = f[..., 0, 0] * a + f[..., 0, 1] * b
+    out[..., h:] = f[..., 1, 0] * a + f[..., 1, 1] * b
+    return out
+
+
+def attention_dataflow(q, k, v, q_norm_w=None, k_norm_w=None, freqs=None, eps=1e-6,
+                       sdpa=None):
+    """The middle of NumpyAttention.forward (numpy_dit.py:283-294) on
+    [B,S,H,D] projections: per-head RMSNorm of q and k (weights optional),
+    RoPE on both when a table is given (self-attention only), transpose to
+    [B,H,S,D], flash SDPA with scale 1/sqrt(D), transpose back.
+    Returns [B,Sq,H,D] float32."""
+    q = np.asarray(q, np.float32)
+    k = np.asarray(k, np.float32)
+    v = np.asarray(v, np.float32)
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    qn = rmsnorm(q, q_norm_w, eps)
+    kn = rmsnorm(k, k_norm_w, eps)
+    if freqs is not None:
+        qn = numpy_rope(qn, freqs)
+        kn = numpy_rope(kn, freqs)
+    qt = qn.transpose(0, 2, 1, 3).reshape(B * H, Sq, D)
+    kt = kn.transpose(0, 2, 1, 3).reshape(B * H, Sk, D)
+    vt = v.transpose(0, 2, 1, 3).reshape(B * H, Sk, D)
+    run = sdpa or flash_sdpa
+    o = run(qt, kt, vt)
+    return o.reshape(B, H, Sq, D).transpose(0, 2, 1, 3).copy()
+
+
+# ------------------------------------------------------------ fp64 checks
+
+def sdpa_fp64(q, k, v, scale=None, is_causal=False):
+    """Textbook softmax(scale*QK^T)V in float64 (independent of the tiling)."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    D = q.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    s = np.einsum("bqd,bkd->bqk", q, k) * scale
+    if is_causal:
+        Sq, Sk = s.shape[1:]
+        mask = np.arange(Sk)[None, :] > np.arange(Sq)[:, None]
+        s = np.where(mask[None], -np.inf, s)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return np.einsum("bqk,bkd->bqd", p, v)
+
+
+def rmsnorm_fp64(x, w=None, eps=1e-6):
+    x = np.asarray(x, np.float64)
+    y = x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+    if w is not None:
+        y = y * np.asarray(w, np.float64)
+    return y
+
+
+def rope_freqs_fp64(H: int, W: int, T: int = 1, head_dim: int = 128) -> np.ndarray:
+    """The RoPE table from the closed form in float64: per pair j of each
+    axis block, angle = pos * base^(-2j/dim)."""
+    dh = head_dim // 6 * 2
+    dt = head_dim - 2 * dh
+    tab = np.empty((T, H, W, head_dim // 2), np.float64)
+    bases = [(dt, 10000.0), (dh, 10000.0 * 4.0 ** (dh / (dh - 2))),
+             (dh, 10000.0 * 4.0 ** (dh / (dh - 2)))]
+    col = 0
+    for axis, (dim, base) in enumerate(bases):
+        for j in range(dim // 2):
+            fr = base ** (-(2.0 * j) / dim)
+            pos = [np.arange(T), np.arange(H), np.arange(W)][axis].astype(np.float64)
+            shape = [1, 1, 1]
+            shape[axis] = -1
+            tab[..., col] = pos.reshape(shape) * fr
+            col += 1
+    c, s = np.cos(tab), np.sin(tab)
+    return np.stack([c, -s, s, c], axis=-1).reshape(T * H * W, head_dim // 2, 2, 2)

@@ -1,0 +1,74 @@
+"""The C-ABI library without a GPU: it loads, exports every declared symbol,
+and reports errors instead of returning silently (no compute is launched)."""
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import anima_hip
+from anima_hip import _lib, rt
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "anima_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(anima_(?:rt|hip)_\w+)\s*\(", text)))
+
+
+def test_library_built_and_loads():
+    assert os.path.exists(_lib.LIB_PATH), "run __graft_entry__.build()"
+    _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    names = declared_functions()
+    assert "anima_rt_run_sdpa_flash" in names and len(names) >= 10
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [n for n in names if n not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+    assert sorted(_lib.SIGNATURES) == names, "ctypes declarations out of sync with the header"
+
+
+def test_reference_drop_in_signatures():
+    # The ctypes argtypes the reference's binding uses (anima_rt_ops.py:28-34).
+    import ctypes as ct
+    sig = _lib.SIGNATURES
+    assert sig["anima_rt_run_sdpa_flash"][1] == [ct.c_void_p] * 4 + [ct.c_int] * 4 + [
+        ct.c_float, ct.c_bool]
+    assert sig["anima_rt_run_sdpa"][1] == sig["anima_rt_run_sdpa_flash"][1]
+    assert sig["anima_rt_run_rmsnorm"][1] == [ct.c_void_p] * 3 + [ct.c_int] * 2 + [ct.c_float]
+    assert sig["anima_rt_run_rope"][1] == [ct.c_void_p] * 3 + [ct.c_int] * 3
+    for name in ("anima_rt_init", "anima_rt_run_sdpa_flash", "anima_rt_run_sdpa",
+                 "anima_rt_run_rmsnorm", "anima_rt_run_rope"):
+        assert sig[name][0] is ct.c_bool
+
+
+def test_rmsnorm_and_math_sdpa_require_init():
+    # anima_rt.cpp:47 and :84 return false before anima_rt_init(); so does the
+    # drop-in, and the Python layer turns that into an exception.
+    rt.destroy()
+    lib = _lib.load()
+    x = np.ones((2, 8), np.float32)
+    out = np.zeros_like(x)
+    assert not lib.anima_rt_run_rmsnorm(x.ctypes.data, None, out.ctypes.data, 2, 8, 1e-6)
+    assert "anima_rt_init" in _lib.last_error()
+    with pytest.raises(anima_hip.AnimaHipError):
+        rt.rmsnorm(x)
+    q = np.ones((1, 4, 8), np.float32)
+    with pytest.raises(anima_hip.AnimaHipError, match="anima_rt_init"):
+        rt.sdpa_math(q, q, q)
+
+
+def test_python_shape_validation():
+    q = np.zeros((2, 4, 8), np.float32)
+    with pytest.raises(ValueError):
+        rt.sdpa_flash(q, np.zeros((2, 5, 9), np.float32), np.zeros((2, 5, 9), np.float32))
+    with pytest.raises(ValueError):
+        rt.rope(q, np.zeros((3, 4, 2, 2), np.float32))

@@ -1,0 +1,55 @@
+"""The oracle against the reference runtime compiled from its sources.
+
+oracle/_ref/libanima_rt_ref.so exists where `make -C oracle ref` ran next to
+the reference tree; elsewhere these tests skip and the golden vectors of
+tests/test_oracle.py carry the same check.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built")
+
+
+@pytest.mark.parametrize("bh,sq,sk,d,causal", [
+    (2, 256, 256, 128, False),   # config-1 tile choice qSplit=64
+    (1, 800, 520, 128, False),   # qSplit=256, two kv blocks (512 + 8)
+    (3, 31, 77, 64, True),
+    (1, 1, 1, 128, False),
+    (2, 70, 9, 100, True),
+])
+def test_flash_bitwise_vs_reference(bh, sq, sk, d, causal):
+    rng = np.random.default_rng(sq * 7 + sk)
+    q = rng.standard_normal((bh, sq, d)).astype(np.float32)
+    k = rng.standard_normal((bh, sk, d)).astype(np.float32)
+    v = rng.standard_normal((bh, sk, d)).astype(np.float32)
+    s = 1.0 / math.sqrt(d)
+    np.testing.assert_array_equal(oracle.flash_sdpa(q, k, v, s, causal),
+                                  oracle.ref_flash_sdpa(q, k, v, s, causal))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_math_bitwise_vs_reference(causal):
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((2, 40, 128)).astype(np.float32)
+    k = rng.standard_normal((2, 40, 128)).astype(np.float32)
+    v = rng.standard_normal((2, 40, 128)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.math_sdpa(q, k, v, 0.088, causal),
+                                  oracle.ref_math_sdpa(q, k, v, 0.088, causal))
+
+
+def test_rmsnorm_rope_gemm_bitwise_vs_reference():
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((257, 128)).astype(np.float32)
+    w = rng.standard_normal(128).astype(np.float32)
+    np.testing.assert_array_equal(oracle.rmsnorm(x, w), oracle.ref_rmsnorm(x, w))
+    np.testing.assert_array_equal(oracle.rmsnorm(x, None, 1e-5), oracle.ref_rmsnorm(x, None, 1e-5))
+    t = rng.standard_normal((4, 96, 128)).astype(np.float32)
+    f = oracle.rope_freqs(12, 8)
+    np.testing.assert_array_equal(oracle.rope(t, f), oracle.ref_rope(t, f))
+    a = rng.standard_normal((5, 64)).astype(np.float32)
+    wb = oracle.f32_to_bf16_bits(rng.standard_normal((9, 64)).astype(np.float32))
+    np.testing.assert_array_equal(oracle.gemm_bf16(a, wb), oracle.ref_gemm_bf16(a, wb))
