@@ -54,6 +54,22 @@ def sdpa_flash(q, k, v, scale=None, is_causal=False) -> np.ndarray:
     return o
 
 
+def sdpa(q, k, v, scale=None, is_causal=False, mode=F32) -> np.ndarray:
+    """anima_hip_sdpa: sdpa_flash with an arithmetic mode (F32 or BF16)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    BH, Sq, D = q.shape
+    Sk = k.shape[1]
+    if k.shape != (BH, Sk, D) or v.shape != (BH, Sk, D):
+        raise ValueError(f"sdpa shapes q{q.shape} k{k.shape} v{v.shape}")
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    o = np.zeros((BH, Sq, D), np.float32)
+    ok = _lib.load().anima_hip_sdpa(_p(q), _p(k), _p(v), _p(o), BH, Sq, Sk, D, ct.c_float(scale),
+                                    ct.c_bool(is_causal), int(mode))
+    _lib.check(ok, "anima_hip_sdpa")
+    return o
+
+
 def sdpa_math(q, k, v, scale=None, is_causal=False) -> np.ndarray:
     """anima_rt_run_sdpa (anima_rt.cpp:78-141): the reference's math entry,
     whose effective logit scale is scale**2.  Needs init() first."""

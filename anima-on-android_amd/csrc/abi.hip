@@ -126,9 +126,9 @@ bool d2h(void *dst, const void *src, size_t n, hipStream_t st)
 
 bool sync(hipStream_t st) { return hip_ok(hipStreamSynchronize(st), "hipStreamSynchronize"); }
 
-// Shared body of the two host-pointer SDPA entries.
+// Shared body of the host-pointer SDPA entries ([BH, S, D] f32 host arrays).
 bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int BH, int S_q,
-               int S_kv, int D, float scale, bool causal)
+               int S_kv, int D, float scale, bool causal, bool bf16 = false)
 {
     if (!check_dims(1, BH, S_q, S_kv, D))
         return false;
@@ -159,8 +159,46 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
     p.D = D;
     p.scale = scale;
     p.causal = causal;
-    if (!launch_flash_f32(p, st))
+    if (bf16) {
+        if (D != 128)
+            return fail("sdpa: the bf16 mode needs D == 128");
+        // bf16 copies of Q and K (row kernel without norm/RoPE) and packed V^T.
+        const int64_t sp = vt_padded_len(S_kv);
+        if (!r.q2.reserve(nq * 2, "workspace q bf16") || !r.k2.reserve(nk * 2, "workspace k bf16") ||
+            !r.v2.reserve(size_t(BH) * D * sp * 2, "workspace v^T"))
+            return false;
+        RowProblem c;
+        c.x = static_cast<const float *>(r.q.p);
+        c.out = r.q2.p;
+        c.w = nullptr;
+        c.freqs = nullptr;
+        c.xs = c.os = Strides{0, int64_t(S_q) * D, int64_t(D)};
+        c.B = 1;
+        c.S = S_q;
+        c.H = BH;
+        c.D = D;
+        c.eps = 0.0f;
+        c.norm = false;
+        c.out_bf16 = true;
+        RowProblem ck = c;
+        ck.x = static_cast<const float *>(r.k.p);
+        ck.out = r.k2.p;
+        ck.xs = ck.os = Strides{0, int64_t(S_kv) * D, int64_t(D)};
+        ck.S = S_kv;
+        const Strides vts{0, int64_t(D) * sp, sp};
+        if (!launch_rows(c, st) || !launch_rows(ck, st) ||
+            !launch_vt_pack(static_cast<const float *>(r.v.p), p.vs,
+                            static_cast<uint16_t *>(r.v2.p), vts, 1, BH, S_kv, D, st))
+            return false;
+        p.q = r.q2.p;
+        p.k = r.k2.p;
+        p.v = r.v2.p;
+        p.vs = vts;
+        if (!launch_flash_bf16(p, st))
+            return false;
+    } else if (!launch_flash_f32(p, st)) {
         return false;
+    }
     if (!d2h(out, r.o.p, f32_bytes(nq), st))
         return false;
     return sync(st);
@@ -294,6 +332,18 @@ bool anima_rt_run_rope(const float *t, const float *freqs, float *out, int N, in
     return sync(st);
 }
 
+bool anima_hip_sdpa(const float *Q, const float *K, const float *V, float *out, int BH, int S_q,
+                    int S_kv, int D, float scale, bool is_causal, int mode)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!ensure_ready(r))
+        return false;
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16)
+        return fail("anima_hip_sdpa: unknown mode " + std::to_string(mode));
+    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale, is_causal, mode == ANIMA_HIP_BF16);
+}
+
 const char *anima_hip_last_error(void) { return t_last_error.c_str(); }
 
 int anima_hip_version(void) { return 100; }
@@ -330,6 +380,66 @@ bool anima_hip_flash_f32_dev(const float *q, const float *k, const float *v, flo
     p.scale = scale;
     p.causal = is_causal;
     return launch_flash_f32(p, pick_stream(stream));
+}
+
+bool anima_hip_flash_bf16_dev(const uint16_t *q, const uint16_t *k, const uint16_t *vt, float *o,
+                              int B, int H, int S_q, int S_kv, int D, const int64_t *q_strides,
+                              const int64_t *k_strides, const int64_t *vt_strides,
+                              const int64_t *o_strides, float scale, bool is_causal, void *stream)
+{
+    Runtime &r = rt();
+    {
+        std::lock_guard<std::recursive_mutex> g(r.mu);
+        if (!ensure_ready(r))
+            return false;
+    }
+    if (!check_dims(B, H, S_q, S_kv, D))
+        return false;
+    if (int64_t(B) * H * S_q * D > 0 && (!q || !o || (S_kv > 0 && (!k || !vt))))
+        return fail("flash_bf16_dev: null pointer");
+    const int64_t sp = vt_padded_len(S_kv);
+    FlashProblem p;
+    p.q = q;
+    p.k = k;
+    p.v = vt;
+    p.o = o;
+    p.qs = from_array(q_strides, H, S_q, D);
+    p.ks = from_array(k_strides, H, S_kv, D);
+    p.vs = vt_strides ? Strides{vt_strides[0], vt_strides[1], vt_strides[2]}
+                      : Strides{int64_t(H) * D * sp, int64_t(D) * sp, sp};
+    p.os = from_array(o_strides, H, S_q, D);
+    p.B = B;
+    p.H = H;
+    p.S_q = S_q;
+    p.S_kv = S_kv;
+    p.D = D;
+    p.scale = scale;
+    p.causal = is_causal;
+    return launch_flash_bf16(p, pick_stream(stream));
+}
+
+int64_t anima_hip_vt_padded_len(int S_kv) { return S_kv > 0 ? vt_padded_len(S_kv) : 0; }
+
+bool anima_hip_pack_vt_dev(const float *v, uint16_t *vt, int B, int H, int S_kv, int D,
+                           const int64_t *v_strides, const int64_t *vt_strides, void *stream)
+{
+    Runtime &r = rt();
+    {
+        std::lock_guard<std::recursive_mutex> g(r.mu);
+        if (!ensure_ready(r))
+            return false;
+    }
+    if (!check_dims(B, H, S_kv, S_kv, D))
+        return false;
+    if (int64_t(B) * H * S_kv * D > 0 && (!v || !vt))
+        return fail("pack_vt_dev: null pointer");
+    const int64_t sp = vt_padded_len(S_kv);
+    const Strides ts = vt_strides ? Strides{vt_strides[0], vt_strides[1], vt_strides[2]}
+                                  : Strides{int64_t(H) * D * sp, int64_t(D) * sp, sp};
+    if (ts.s != sp)
+        return fail("pack_vt_dev: V^T row stride must equal the padded key count");
+    return launch_vt_pack(v, from_array(v_strides, H, S_kv, D), vt, ts, B, H, S_kv, D,
+                          pick_stream(stream));
 }
 
 bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const float *freqs,
@@ -374,8 +484,11 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
         return false;
     if (!check_dims(B, H, S_q, S_kv, D))
         return false;
-    if (mode != ANIMA_HIP_F32)
-        return fail("anima_hip_attention: mode " + std::to_string(mode) + " is not available");
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16)
+        return fail("anima_hip_attention: unknown mode " + std::to_string(mode));
+    const bool bf16 = mode == ANIMA_HIP_BF16;
+    if (bf16 && D != 128)
+        return fail("anima_hip_attention: the bf16 mode needs D == 128");
     if (freqs && S_q != S_kv)
         return fail("anima_hip_attention: RoPE needs S_q == S_kv (self-attention)");
     const int64_t nq = int64_t(B) * S_q * H * D, nk = int64_t(B) * S_kv * H * D;
@@ -385,9 +498,12 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
         return fail("anima_hip_attention: null pointer");
     const hipStream_t st = r.stream;
     const int64_t nf = freqs ? int64_t(S_q) * D * 2 : 0;
+    const int64_t sp = vt_padded_len(S_kv);
+    const size_t vt_bytes = size_t(B) * H * D * sp * sizeof(uint16_t);
     if (!r.q.reserve(f32_bytes(nq), "workspace q") || !r.k.reserve(f32_bytes(nk), "workspace k") ||
         !r.v.reserve(f32_bytes(nk), "workspace v") || !r.o.reserve(f32_bytes(nq), "workspace o") ||
-        !r.q2.reserve(f32_bytes(nq), "workspace q'") || !r.k2.reserve(f32_bytes(nk), "workspace k'"))
+        !r.q2.reserve(f32_bytes(nq), "workspace q'") || !r.k2.reserve(f32_bytes(nk), "workspace k'") ||
+        (bf16 && !r.v2.reserve(vt_bytes, "workspace v^T")))
         return false;
     if ((q_norm_w && !r.w0.reserve(f32_bytes(D), "workspace q_norm")) ||
         (k_norm_w && !r.w1.reserve(f32_bytes(D), "workspace k_norm")) ||
@@ -414,7 +530,7 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
     pq.D = D;
     pq.eps = eps;
     pq.norm = true;
-    pq.out_bf16 = false;
+    pq.out_bf16 = bf16;
     RowProblem pk = pq;
     pk.x = static_cast<const float *>(r.k.p);
     pk.out = r.k2.p;
@@ -423,13 +539,18 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
     pk.S = S_kv;
     if (!launch_rows(pq, st) || !launch_rows(pk, st))
         return false;
+    const Strides vts{int64_t(H) * D * sp, int64_t(D) * sp, sp};
+    if (bf16 && !launch_vt_pack(static_cast<const float *>(r.v.p), kv,
+                                static_cast<uint16_t *>(r.v2.p), vts, B, H, S_kv, D, st))
+        return false;
     FlashProblem p;
     p.q = r.q2.p;
     p.k = r.k2.p;
-    p.v = r.v.p;
+    p.v = bf16 ? r.v2.p : r.v.p;
     p.o = static_cast<float *>(r.o.p);
     p.qs = p.os = qv;
-    p.ks = p.vs = kv;
+    p.ks = kv;
+    p.vs = bf16 ? vts : kv;
     p.B = B;
     p.H = H;
     p.S_q = S_q;
@@ -437,7 +558,8 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
     p.D = D;
     p.scale = float(1.0 / std::sqrt(double(D)));  // as NumpyRT.run_sdpa passes it
     p.causal = false;
-    if (!launch_flash_f32(p, st) || !d2h(out, r.o.p, f32_bytes(nq), st))
+    if (!(bf16 ? launch_flash_bf16(p, st) : launch_flash_f32(p, st)) ||
+        !d2h(out, r.o.p, f32_bytes(nq), st))
         return false;
     return sync(st);
 }

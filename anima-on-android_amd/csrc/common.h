@@ -36,6 +36,29 @@ bool launch_flash_f32(const FlashProblem &p, hipStream_t st);
 // True when launch_flash_f32 would take the MFMA path for this problem.
 bool flash_f32_fast_path(const FlashProblem &p);
 
+// bf16 inputs (Q, K row-major [.., S, D]; V transposed, layout below),
+// bf16 MFMA with f32 accumulation and f32 softmax; D == 128 and scale > 0.
+// `v` points at the packed V^T and `vs` holds its {batch, head, d-row}
+// strides (the d-row stride is vt_padded_len(S_kv)).
+bool launch_flash_bf16(const FlashProblem &p, hipStream_t st);
+
+// V^T layout of the bf16 path: per (batch, head) a [D][Sp] bf16 matrix with
+// Sp = vt_padded_len(S_kv), zero beyond S_kv, and within every group of 16
+// keys the key with offset c stored at position vt_key_pos(c) (bits 2 and 3
+// of c swapped).  With this order one 16-byte LDS read yields the 8 keys
+// that pair with the P values a lane holds in its MFMA accumulators.
+constexpr int kVtTile = 64;
+inline int64_t vt_padded_len(int64_t S_kv) { return (S_kv + kVtTile - 1) / kVtTile * kVtTile; }
+__host__ __device__ inline int vt_key_pos(int c)
+{
+    return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1);
+}
+
+// Pack V (f32, [B,H,S,D] view through `vs`, D == 128) into the V^T layout
+// above at `vt` with strides {batch, head} = vts.b, vts.h (d-row stride Sp).
+bool launch_vt_pack(const float *v, Strides vs, uint16_t *vt, Strides vts, int B, int H,
+                    int S_kv, int D, hipStream_t st);
+
 // Per-row RMSNorm (+ optional RoPE) "prologue".
 //   x:   rows indexed (b, s, h) through `xs` (D contiguous), f32
 //   out: same indexing through `os`, f32 or bf16 (out_bf16)

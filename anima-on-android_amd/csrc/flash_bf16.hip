@@ -1,0 +1,375 @@
+// Flash attention with bf16 inputs, bf16 MFMA and f32 accumulation (gfx950).
+//
+// Same computation as anima_rt_run_sdpa_flash (anima_rt/src/anima_rt.cpp:147-156 ->
+// anima/include/cpu/flash_attention.h:55-208) with Q, K, V and the softmax
+// probabilities P rounded to bf16 before the two products; scores, the
+// online max/sum and the output accumulate in f32.
+//
+// Kernel shape (D = 128), per workgroup NW waves x 32 query rows:
+//   * S^T = K Q^T with v_mfma_f32_32x32x16_bf16; lane l holds query row l%32
+//     in every accumulator (lane-local softmax, one exchange with lane l^32);
+//   * O^T += V^T P^T with the same instruction: P's B operand is the S^T
+//     accumulator converted to bf16 in place (8 consecutive accumulator
+//     registers = 8 keys); V^T's A operand is one 16-byte LDS read thanks to
+//     the key order of the packed V^T (vt_key_pos);
+//   * K tiles [64 keys][128 d] and V^T tiles [128 d][64 keys] are staged
+//     through LDS, double-buffered, one barrier per tile; row pitches are
+//     padded by 16 bytes so the per-lane 16-byte reads are conflict-free;
+//   * the softmax scale is folded into the exponent: p = exp2(s*c - m) with
+//     c = scale*log2(e) > 0, so the tile max is taken on raw scores.
+// Also here: the V -> packed V^T conversion kernel of this path.
+#include "common.h"
+
+#include <cmath>
+
+namespace anima_hip {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16;
+
+constexpr int kD = 128;
+constexpr int kBN = 64;          // keys per tile (== kVtTile)
+constexpr int kKPitch = kD + 8;  // bf16 per LDS K row (272 bytes)
+constexpr int kVPitch = kBN + 8; // bf16 per LDS V^T row (144 bytes)
+constexpr float kLog2e = 1.4426950408889634f;
+static_assert(kBN == kVtTile, "V^T padding must match the key tile");
+
+struct Bf16Args {
+    const u16 *q, *k, *vt;
+    float *o;
+    int64_t qb, qh, qs, kb, kh, ks, vb, vh, vd, ob, oh, os;
+    int H, S_q, S_kv, n_qtiles;
+    float c;  // scale * log2(e), > 0
+    int causal;
+};
+
+__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+__device__ __forceinline__ bf16x8 pack8(const f32x16 &s, int base)
+{
+    bf16x8 r;
+    const bf16x2 p0 = __builtin_convertvector(f32x2{s[base + 0], s[base + 1]}, bf16x2);
+    const bf16x2 p1 = __builtin_convertvector(f32x2{s[base + 2], s[base + 3]}, bf16x2);
+    const bf16x2 p2 = __builtin_convertvector(f32x2{s[base + 4], s[base + 5]}, bf16x2);
+    const bf16x2 p3 = __builtin_convertvector(f32x2{s[base + 6], s[base + 7]}, bf16x2);
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
+{
+    constexpr int NT = NW * 64;
+    constexpr int BM = NW * 32;
+    constexpr int KCH = kBN * kD / 8;  // 16-byte chunks per K tile
+    constexpr int VCH = kD * kBN / 8;  // 16-byte chunks per V^T tile
+    constexpr int LK = KCH / NT, LV = VCH / NT;
+    static_assert(KCH % NT == 0 && VCH % NT == 0, "tiles must split evenly");
+
+    __shared__ __attribute__((aligned(16))) u16 Ks[2][kBN * kKPitch];
+    __shared__ __attribute__((aligned(16))) u16 Vs[2][kD * kVPitch];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+
+    const int qt = blockIdx.x % a.n_qtiles;
+    const int bh = blockIdx.x / a.n_qtiles;
+    const int b = bh / a.H;
+    const int h = bh - b * a.H;
+    const int q_tile0 = qt * BM;
+    const int qrow = q_tile0 + wave * 32 + col;
+
+    const u16 *qp = a.q + b * a.qb + h * a.qh;
+    const u16 *kp = a.k + b * a.kb + h * a.kh;
+    const u16 *vp = a.vt + b * a.vb + h * a.vh;
+
+    // Q fragment: Q[qrow][64*half + 8t .. +7], t = 0..7.
+    bf16x8 qf[8];
+    if (qrow < a.S_q) {
+        const bf16x8 *src = reinterpret_cast<const bf16x8 *>(qp + qrow * a.qs + 64 * half);
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            qf[t] = src[t];
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            qf[t] = bf16x8{};
+    }
+
+    int kv_end = a.S_kv;
+    if (a.causal)
+        kv_end = min(kv_end, min(a.S_q, q_tile0 + BM));
+    const int ntiles = (kv_end + kBN - 1) / kBN;
+
+    f32x4 kst[LK], vst[LV];
+    auto gload = [&](int key0) {
+#pragma unroll
+        for (int i = 0; i < LK; ++i) {
+            const int f = tid + i * NT;
+            const int r = f >> 4, c = f & 15;
+            const int key = key0 + r;
+            kst[i] = key < a.S_kv ? *reinterpret_cast<const f32x4 *>(kp + key * a.ks + 8 * c)
+                                  : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int i = 0; i < LV; ++i) {
+            const int f = tid + i * NT;
+            const int d = f >> 3, c = f & 7;
+            vst[i] = *reinterpret_cast<const f32x4 *>(vp + d * a.vd + key0 + 8 * c);
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < LK; ++i) {
+            const int f = tid + i * NT;
+            const int r = f >> 4, c = f & 15;
+            *reinterpret_cast<f32x4 *>(&Ks[buf][r * kKPitch + 8 * c]) = kst[i];
+        }
+#pragma unroll
+        for (int i = 0; i < LV; ++i) {
+            const int f = tid + i * NT;
+            const int d = f >> 3, c = f & 7;
+            *reinterpret_cast<f32x4 *>(&Vs[buf][d * kVPitch + 8 * c]) = vst[i];
+        }
+    };
+
+    f32x16 o0 = {}, o1 = {}, o2 = {}, o3 = {};
+    float m = -INFINITY;
+    float l = 0.0f;
+
+    if (ntiles > 0) {
+        gload(0);
+        lstore(0);
+    }
+    __syncthreads();
+
+    for (int j = 0; j < ntiles; ++j) {
+        const int buf = j & 1;
+        const bool more = j + 1 < ntiles;
+        if (more)
+            gload((j + 1) * kBN);
+
+        f32x16 s0 = {}, s1 = {};
+        const u16 *kr0 = &Ks[buf][col * kKPitch + 64 * half];
+        const u16 *kr1 = kr0 + 32 * kKPitch;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const bf16x8 k0 = *reinterpret_cast<const bf16x8 *>(kr0 + 8 * t);
+            const bf16x8 k1 = *reinterpret_cast<const bf16x8 *>(kr1 + 8 * t);
+            s0 = mfma_bf16(k0, qf[t], s0);
+            s1 = mfma_bf16(k1, qf[t], s1);
+        }
+
+        const int key0 = j * kBN;
+        if ((key0 + kBN > a.S_kv) || a.causal) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int k0i = key0 + acc_row(r, half);
+                const int k1i = k0i + 32;
+                if (k0i >= a.S_kv || (a.causal && k0i > qrow))
+                    s0[r] = -INFINITY;
+                if (k1i >= a.S_kv || (a.causal && k1i > qrow))
+                    s1[r] = -INFINITY;
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m, mx * a.c);
+        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+        m = m_new;
+
+        float psum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            s0[r] = __builtin_amdgcn_exp2f(fmaf(s0[r], a.c, -m_use));
+            s1[r] = __builtin_amdgcn_exp2f(fmaf(s1[r], a.c, -m_use));
+            psum += s0[r] + s1[r];
+        }
+        l = l * alpha + psum;
+        o0 *= alpha;
+        o1 *= alpha;
+        o2 *= alpha;
+        o3 *= alpha;
+
+        const bf16x8 p00 = pack8(s0, 0), p01 = pack8(s0, 8);
+        const bf16x8 p10 = pack8(s1, 0), p11 = pack8(s1, 8);
+        const u16 *vr = &Vs[buf][col * kVPitch + 8 * half];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+            const u16 *vrow = vr + 32 * blk * kVPitch;
+            const bf16x8 v00 = *reinterpret_cast<const bf16x8 *>(vrow + 0);
+            const bf16x8 v01 = *reinterpret_cast<const bf16x8 *>(vrow + 16);
+            const bf16x8 v10 = *reinterpret_cast<const bf16x8 *>(vrow + 32);
+            const bf16x8 v11 = *reinterpret_cast<const bf16x8 *>(vrow + 48);
+            f32x16 &ob = blk == 0 ? o0 : blk == 1 ? o1 : blk == 2 ? o2 : o3;
+            ob = mfma_bf16(v00, p00, ob);
+            ob = mfma_bf16(v01, p01, ob);
+            ob = mfma_bf16(v10, p10, ob);
+            ob = mfma_bf16(v11, p11, ob);
+        }
+
+        if (more)
+            lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    l += __shfl_xor(l, 32);
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    if (qrow < a.S_q) {
+        float *op = a.o + b * a.ob + h * a.oh + qrow * a.os;
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+            const f32x16 &ob = blk == 0 ? o0 : blk == 1 ? o1 : blk == 2 ? o2 : o3;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d0 = 32 * blk + acc_row(4 * g, half);
+                *reinterpret_cast<f32x4 *>(op + d0) =
+                    f32x4{ob[4 * g] * inv, ob[4 * g + 1] * inv, ob[4 * g + 2] * inv,
+                          ob[4 * g + 3] * inv};
+            }
+        }
+    }
+}
+
+// V (f32, [B,H,S,D] view, D = 128) -> packed bf16 V^T [B,H][D][Sp].  One block
+// per (batch*head, 64-key tile): coalesced float4 reads of the V rows,
+// transpose through LDS, 16-byte coalesced writes along the key axis.  Each
+// thread converts a pair of adjacent keys (2p, 2p+1), which vt_key_pos keeps
+// adjacent, and writes them as one 32-bit LDS word: lanes never share an LDS
+// dword within one store.
+struct PackArgs {
+    const float *v;
+    u16 *vt;
+    int64_t vb, vh, vs, tb, th;
+    int H, S_kv, n_tiles;
+    int64_t sp;
+};
+
+constexpr int kTPitchW = (kBN + 8) / 2;  // 32-bit words per LDS row of the transposed tile
+
+__global__ __launch_bounds__(256) void vt_pack_kernel(PackArgs a)
+{
+    __shared__ __attribute__((aligned(16))) unsigned int T[kD * kTPitchW];
+    const int tile = blockIdx.x % a.n_tiles;
+    const int bh = blockIdx.x / a.n_tiles;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int key0 = tile * kBN;
+    const float *vp = a.v + b * a.vb + h * a.vh;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int f = threadIdx.x + 256 * i;  // (key pair, float4 column) of the tile
+        const int pr = f >> 5, c4 = f & 31;
+        const int k0 = key0 + 2 * pr, k1 = k0 + 1;
+        const f32x4 x0 = k0 < a.S_kv ? *reinterpret_cast<const f32x4 *>(vp + k0 * a.vs + 4 * c4)
+                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 x1 = k1 < a.S_kv ? *reinterpret_cast<const f32x4 *>(vp + k1 * a.vs + 4 * c4)
+                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+        const int w = vt_key_pos(2 * pr) >> 1;  // word holding positions (2w, 2w+1)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bf16x2 pair = __builtin_convertvector(f32x2{x0[e], x1[e]}, bf16x2);
+            T[(4 * c4 + e) * kTPitchW + w] = __builtin_bit_cast(unsigned int, pair);
+        }
+    }
+    __syncthreads();
+    u16 *tp = a.vt + b * a.tb + h * a.th + key0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int f = threadIdx.x + 256 * i;  // 16-byte chunk: d row, 8 keys
+        const int d = f >> 3, c = f & 7;
+        *reinterpret_cast<f32x4 *>(tp + d * a.sp + 8 * c) =
+            *reinterpret_cast<const f32x4 *>(&T[d * kTPitchW + 4 * c]);
+    }
+}
+
+bool aligned(const void *ptr, unsigned m) { return (reinterpret_cast<uintptr_t>(ptr) & (m - 1)) == 0; }
+
+constexpr int kWaves = 8;
+
+}  // namespace
+
+bool launch_flash_bf16(const FlashProblem &p, hipStream_t st)
+{
+    const int64_t BH = int64_t(p.B) * p.H;
+    if (BH == 0 || p.S_q == 0)
+        return true;
+    if (p.D != kD)
+        return fail("flash_bf16: head dim must be 128 (got " + std::to_string(p.D) + ")");
+    if (!(p.scale > 0.0f))
+        return fail("flash_bf16: scale must be positive");
+    const int64_t sp = vt_padded_len(p.S_kv);
+    if (p.vs.s != sp)
+        return fail("flash_bf16: V^T row stride must equal the padded key count");
+    const auto s8 = [](const Strides &x) { return x.b % 8 == 0 && x.h % 8 == 0 && x.s % 8 == 0; };
+    if (!aligned(p.q, 16) || !aligned(p.k, 16) || !aligned(p.v, 16) || !aligned(p.o, 16) ||
+        !s8(p.qs) || !s8(p.ks) || !s8(p.vs) || p.os.b % 4 || p.os.h % 4 || p.os.s % 4)
+        return fail("flash_bf16: operands must be 16-byte aligned with 16-byte row strides");
+    Bf16Args a;
+    a.q = static_cast<const u16 *>(p.q);
+    a.k = static_cast<const u16 *>(p.k);
+    a.vt = static_cast<const u16 *>(p.v);
+    a.o = p.o;
+    a.qb = p.qs.b; a.qh = p.qs.h; a.qs = p.qs.s;
+    a.kb = p.ks.b; a.kh = p.ks.h; a.ks = p.ks.s;
+    a.vb = p.vs.b; a.vh = p.vs.h; a.vd = sp;
+    a.ob = p.os.b; a.oh = p.os.h; a.os = p.os.s;
+    a.H = p.H;
+    a.S_q = p.S_q;
+    a.S_kv = p.S_kv;
+    constexpr int BM = kWaves * 32;
+    a.n_qtiles = (p.S_q + BM - 1) / BM;
+    a.c = p.scale * kLog2e;
+    a.causal = p.causal ? 1 : 0;
+    const int64_t nblk = BH * a.n_qtiles;
+    if (nblk > INT32_MAX)
+        return fail("flash_bf16: problem too large for one launch");
+    hipLaunchKernelGGL(flash_bf16_d128<kWaves>, dim3(unsigned(nblk)), dim3(kWaves * 64), 0, st, a);
+    return hip_ok(hipGetLastError(), "flash_bf16_d128 launch");
+}
+
+bool launch_vt_pack(const float *v, Strides vs, uint16_t *vt, Strides vts, int B, int H,
+                    int S_kv, int D, hipStream_t st)
+{
+    const int64_t BH = int64_t(B) * H;
+    if (BH == 0 || S_kv == 0)
+        return true;
+    if (D != kD)
+        return fail("vt_pack: head dim must be 128");
+    if (!aligned(v, 16) || !aligned(vt, 16) || vs.b % 4 || vs.h % 4 || vs.s % 4 || vts.b % 8 ||
+        vts.h % 8)
+        return fail("vt_pack: operands must be 16-byte aligned");
+    PackArgs a;
+    a.v = v;
+    a.vt = vt;
+    a.vb = vs.b; a.vh = vs.h; a.vs = vs.s;
+    a.tb = vts.b; a.th = vts.h;
+    a.H = H;
+    a.S_kv = S_kv;
+    a.sp = vt_padded_len(S_kv);
+    a.n_tiles = int(a.sp / kBN);
+    const int64_t nblk = BH * a.n_tiles;
+    if (nblk > INT32_MAX)
+        return fail("vt_pack: problem too large for one launch");
+    hipLaunchKernelGGL(vt_pack_kernel, dim3(unsigned(nblk)), dim3(256), 0, st, a);
+    return hip_ok(hipGetLastError(), "vt_pack_kernel launch");
+}
+
+}  // namespace anima_hip

@@ -57,29 +57,74 @@ __device__ __forceinline__ void row_coords(const RowArgs &a, int64_t r, int64_t 
     ooff = b * a.ob + int64_t(h) * a.oh + int64_t(s) * a.os;
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Output element (row, d) from the staged row: y = x * inv [* w], then the
+// rotate-half rotation when a table is given.  Contraction is off in this
+// file, so every product and sum rounds like the reference's fp32 code.
+__device__ __forceinline__ float norm_elem(const RowArgs &a, const float *row, float inv, int d)
+{
+    if (!a.norm)
+        return row[d];
+    float v = row[d] * inv;
+    if (a.w)
+        v = v * a.w[d];
+    return v;
+}
+
+__device__ __forceinline__ float out_elem(const RowArgs &a, const float *row, float inv, int s,
+                                          int d)
+{
+    if (!a.freqs)
+        return norm_elem(a, row, inv, d);
+    const int half = a.D >> 1;
+    const bool lower = d < half;
+    const int p = lower ? d : d - half;
+    const float ya = norm_elem(a, row, inv, p);
+    const float yb = norm_elem(a, row, inv, p + half);
+    const float *fq = a.freqs + int64_t(s) * a.D * 2 + 4 * p + (lower ? 0 : 2);
+    return fq[0] * ya + fq[1] * yb;
+}
+
+__device__ __forceinline__ float inv_rms(float ss, int D, float eps)
+{
+    // f32 divide and sqrt, each correctly rounded: evaluated in f64 and
+    // rounded once (exact for f32 operands).
+    const float ms = (float)((double)ss / (double)D);
+    const float root = (float)sqrt((double)(ms + eps));
+    return (float)(1.0 / (double)root);
+}
+
+// Any D: rows staged in LDS with an odd pitch, per-row offsets computed once.
 __global__ __launch_bounds__(256) void rows_kernel(RowArgs a)
 {
     extern __shared__ float lds[];
     const int D = a.D;
     const int pitch = D + 1;  // odd pitch: serial per-row reads are conflict-free
     const int RB = a.rows_per_block;
-    float *xs = lds;                       // [RB][pitch]
-    float *inv = lds + RB * pitch;         // [RB]
+    const int nwords = RB * pitch + 2 * RB;
+    float *xs = lds;                                  // [RB][pitch]
+    float *inv = lds + RB * pitch;                    // [RB]
+    int *spos = reinterpret_cast<int *>(inv + RB);    // [RB]
+    int64_t *offs = reinterpret_cast<int64_t *>(lds + nwords + (nwords & 1));  // [RB][2]
     const int64_t r0 = int64_t(blockIdx.x) * RB;
     const int nrows = int(min<int64_t>(RB, a.rows - r0));
     const int n = nrows * D;
 
-    // Stage the rows (coalesced along D).
-    for (int e = threadIdx.x; e < n; e += blockDim.x) {
-        const int rr = e / D, d = e - rr * D;
+    for (int rr = threadIdx.x; rr < nrows; rr += blockDim.x) {
         int64_t xo, oo;
         int s;
         row_coords(a, r0 + rr, xo, oo, s);
-        xs[rr * pitch + d] = a.x[xo + d];
+        offs[2 * rr] = xo;
+        offs[2 * rr + 1] = oo;
+        spos[rr] = s;
     }
     __syncthreads();
-
-    // Serial sum of squares, one thread per row, index order.
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        const int rr = e / D, d = e - rr * D;
+        xs[rr * pitch + d] = a.x[offs[2 * rr] + d];
+    }
+    __syncthreads();
     for (int rr = threadIdx.x; rr < nrows; rr += blockDim.x) {
         float f = 1.0f;
         if (a.norm) {
@@ -87,46 +132,96 @@ __global__ __launch_bounds__(256) void rows_kernel(RowArgs a)
             float ss = 0.0f;
             for (int d = 0; d < D; ++d)
                 ss = ss + row[d] * row[d];
-            // f32 divide and sqrt, each correctly rounded: evaluated in f64
-            // and rounded once (exact for f32 operands), since the f32
-            // device routines may differ from IEEE rounding by an ulp.
-            const float ms = (float)((double)ss / (double)D);
-            const float root = (float)sqrt((double)(ms + a.eps));
-            f = (float)(1.0 / (double)root);
+            f = inv_rms(ss, D, a.eps);
         }
         inv[rr] = f;
     }
     __syncthreads();
-
-    const int halfD = D >> 1;
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
         const int rr = e / D, d = e - rr * D;
+        const float v = out_elem(a, xs + rr * pitch, inv[rr], spos[rr], d);
+        const int64_t oo = offs[2 * rr + 1] + d;
+        if (a.out_bf16)
+            static_cast<unsigned short *>(a.out)[oo] = f32_to_bf16_rne(v);
+        else
+            static_cast<float *>(a.out)[oo] = v;
+    }
+}
+
+// D = 128 with 16-byte aligned rows: 64 rows per block, float4 traffic.
+// LDS pitch 132 floats keeps float4 accesses aligned and makes the per-row
+// float4 reads of the serial sum (lanes 528 bytes apart) bank-conflict free.
+constexpr int kRows128 = 64;
+constexpr int kPitch128 = 132;
+
+__global__ __launch_bounds__(256) void rows_d128(RowArgs a)
+{
+    __shared__ __attribute__((aligned(16))) float xs[kRows128 * kPitch128];
+    __shared__ float inv[kRows128];
+    __shared__ int spos[kRows128];
+    __shared__ int64_t xoff[kRows128], ooff[kRows128];
+    const int t = threadIdx.x;
+    const int64_t r0 = int64_t(blockIdx.x) * kRows128;
+    const int nrows = int(min<int64_t>(kRows128, a.rows - r0));
+
+    if (t < nrows) {
         int64_t xo, oo;
         int s;
-        row_coords(a, r0 + rr, xo, oo, s);
-        const float *row = xs + rr * pitch;
-        const float f = inv[rr];
-        auto y_at = [&](int dd) {
-            if (!a.norm)
-                return row[dd];
-            float v = row[dd] * f;
-            if (a.w)
-                v = v * a.w[dd];
-            return v;
-        };
-        float out;
-        if (a.freqs) {
-            const int p = d < halfD ? d : d - halfD;
-            const float ya = y_at(p), yb = y_at(p + halfD);
-            const float *fq = a.freqs + int64_t(s) * D * 2 + 4 * p + (d < halfD ? 0 : 2);
-            out = fq[0] * ya + fq[1] * yb;
-        } else {
-            out = y_at(d);
+        row_coords(a, r0 + t, xo, oo, s);
+        xoff[t] = xo;
+        ooff[t] = oo;
+        spos[t] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int f = t + 256 * i;
+        const int rr = f >> 5, c4 = f & 31;
+        if (rr < nrows)
+            *reinterpret_cast<f32x4 *>(&xs[rr * kPitch128 + 4 * c4]) =
+                *reinterpret_cast<const f32x4 *>(a.x + xoff[rr] + 4 * c4);
+    }
+    __syncthreads();
+    if (t < nrows) {
+        float f = 1.0f;
+        if (a.norm) {
+            float ss = 0.0f;
+            const float *row = xs + t * kPitch128;
+#pragma unroll 8
+            for (int j = 0; j < 32; ++j) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(row + 4 * j);
+                ss = ss + v.x * v.x;
+                ss = ss + v.y * v.y;
+                ss = ss + v.z * v.z;
+                ss = ss + v.w * v.w;
+            }
+            f = inv_rms(ss, 128, a.eps);
         }
-        if (a.out_bf16)
-            static_cast<unsigned short *>(a.out)[oo + d] = f32_to_bf16_rne(out);
-        else
-            static_cast<float *>(a.out)[oo + d] = out;
+        inv[t] = f;
+    }
+    __syncthreads();
+#pragma unroll 2
+    for (int i = 0; i < 8; ++i) {
+        const int f = t + 256 * i;
+        const int rr = f >> 5, c4 = f & 31;
+        if (rr >= nrows)
+            continue;
+        const float *row = xs + rr * kPitch128;
+        const float fi = inv[rr];
+        const int s = spos[rr];
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = out_elem(a, row, fi, s, 4 * c4 + e);
+        const int64_t oo = ooff[rr] + 4 * c4;
+        if (a.out_bf16) {
+            const unsigned int lo = f32_to_bf16_rne(o[0]) | (unsigned(f32_to_bf16_rne(o[1])) << 16);
+            const unsigned int hi = f32_to_bf16_rne(o[2]) | (unsigned(f32_to_bf16_rne(o[3])) << 16);
+            *reinterpret_cast<uint2 *>(static_cast<unsigned short *>(a.out) + oo) = uint2{lo, hi};
+        } else {
+            *reinterpret_cast<f32x4 *>(static_cast<float *>(a.out) + oo) =
+                f32x4{o[0], o[1], o[2], o[3]};
+        }
     }
 }
 
@@ -139,14 +234,6 @@ bool launch_rows(const RowProblem &p, hipStream_t st)
         return true;
     if (p.freqs && (p.D & 1))
         return fail("rope: head dim must be even");
-    // Up to 64 rows per block within 48 KiB of LDS; at least one row.
-    const int64_t budget = 48 * 1024 / 4;
-    int rb = int(std::min<int64_t>(64, budget / (p.D + 2)));
-    if (rb < 1)
-        return fail("rows kernel: D=" + std::to_string(p.D) + " exceeds the per-row LDS budget");
-    const int64_t nblk = (rows + rb - 1) / rb;
-    if (nblk > INT32_MAX)
-        return fail("rows kernel: too many rows");
     RowArgs a;
     a.x = p.x;
     a.out = p.out;
@@ -158,11 +245,36 @@ bool launch_rows(const RowProblem &p, hipStream_t st)
     a.S = p.S;
     a.H = p.H;
     a.D = p.D;
-    a.rows_per_block = rb;
     a.eps = p.eps;
     a.norm = p.norm ? 1 : 0;
     a.out_bf16 = p.out_bf16 ? 1 : 0;
-    const size_t shm = sizeof(float) * (size_t(rb) * (p.D + 1) + rb);
+
+    const auto al = [](const void *ptr, unsigned m) {
+        return (reinterpret_cast<uintptr_t>(ptr) & (m - 1)) == 0;
+    };
+    const auto st4 = [](const Strides &x) { return x.b % 4 == 0 && x.h % 4 == 0 && x.s % 4 == 0; };
+    if (p.D == 128 && al(p.x, 16) && al(p.out, p.out_bf16 ? 8 : 16) && st4(p.xs) && st4(p.os)) {
+        a.rows_per_block = kRows128;
+        const int64_t nblk = (rows + kRows128 - 1) / kRows128;
+        if (nblk > INT32_MAX)
+            return fail("rows kernel: too many rows");
+        hipLaunchKernelGGL(rows_d128, dim3(unsigned(nblk)), dim3(256), 0, st, a);
+        return hip_ok(hipGetLastError(), "rows_d128 launch");
+    }
+
+    // Generic D: up to 64 rows per block within 48 KiB of LDS; at least one row.
+    const int64_t budget = 48 * 1024 / 4;
+    const int rb = int(std::min<int64_t>(64, budget / (p.D + 8)));
+    if (rb < 1)
+        return fail("rows kernel: D=" + std::to_string(p.D) + " exceeds the per-row LDS budget");
+    const int64_t nblk = (rows + rb - 1) / rb;
+    if (nblk > INT32_MAX)
+        return fail("rows kernel: too many rows");
+    a.rows_per_block = rb;
+    // LDS: rows [rb][D+1] f32, inv [rb] f32, s [rb] i32, (pad to 8 bytes),
+    // offsets [rb][2] i64 -- the layout rows_kernel computes.
+    const size_t nwords = size_t(rb) * (p.D + 1) + 2 * size_t(rb);
+    const size_t shm = 4 * (nwords + (nwords & 1)) + sizeof(int64_t) * 2 * size_t(rb);
     hipLaunchKernelGGL(rows_kernel, dim3(unsigned(nblk)), dim3(256), shm, st, a);
     return hip_ok(hipGetLastError(), "rows_kernel launch");
 }

@@ -44,8 +44,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--variant", choices=["f32"], default="f32")
-    ap.add_argument("--cpu-heads", type=int, default=4,
+    ap.add_argument("--variant", choices=["f32", "bf16"], default="f32",
+                    help="f32: f32 MFMA on f32 inputs; bf16: bf16 inputs, f32 accumulate")
+    ap.add_argument("--cpu-heads", type=int, default=8,
                     help="(batch, head) slices timed single-core for cpu_baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
@@ -75,11 +76,11 @@ def cpu_baseline(qn, kn, v, B, H, S, D, heads):
     fn = oracle.ref_flash_sdpa if kind == "reference" else oracle.flash_sdpa
     scale = 1.0 / math.sqrt(D)
 
-    def slice_heads(x, n):  # [B,S,H,D] device -> n contiguous [S,D] host slices
+    def slice_heads(x, n):  # [B,S,H,D] device -> n contiguous [S,D] f32 host slices
         sl = []
         for i in range(n):
             b, h = divmod(i, H)
-            sl.append(x[b, :, h, :].contiguous().cpu().numpy())
+            sl.append(x[b, :, h, :].float().contiguous().cpu().numpy())
         return sl
 
     n1 = max(1, min(heads, B * H))
@@ -144,31 +145,43 @@ def main():
     rng = np.random.default_rng(3003)
     host = [rng.standard_normal((B, S, H, D), dtype=np.float32) for _ in range(3)]
     q, k, v = (torch.from_numpy(x).to(dev) for x in host)
-    qn = torch.empty_like(q)
-    kn = torch.empty_like(k)
+    bf16 = args.variant == "bf16"
+    qn = torch.empty(q.shape, dtype=torch.bfloat16 if bf16 else torch.float32, device=dev)
+    kn = torch.empty_like(qn)
     o = torch.empty_like(q)
+    sp = lib.anima_hip_vt_padded_len(S)
+    vt = torch.empty((B, H, D, sp), dtype=torch.bfloat16, device=dev) if bf16 else None
     freqs = torch.from_numpy(generate_rope_freqs(64, 64)).to(dev)
     ones = torch.ones(D, device=dev)
     st = torch.cuda.Stream(device=dev)
-    sp = ct.c_void_p(st.cuda_stream)
+    stp = ct.c_void_p(st.cuda_stream)
     bshd = _lib.strides([S * H * D, D, H * D])  # [B,S,H,D] viewed as [B,H,S,D]
     scale = ct.c_float(1.0 / math.sqrt(D))
 
     def prologue(x, y):
+        flags = 1 | (2 if bf16 else 0)  # RMSNorm (+ bf16 output)
         ok = lib.anima_hip_qk_prologue_dev(x.data_ptr(), y.data_ptr(), ones.data_ptr(),
                                            freqs.data_ptr(), B, S, H, D, bshd, bshd,
-                                           ct.c_float(1e-6), 1, sp)
+                                           ct.c_float(1e-6), flags, stp)
         _lib.check(ok, "qk_prologue")
 
     def flash():
-        ok = lib.anima_hip_flash_f32_dev(qn.data_ptr(), kn.data_ptr(), v.data_ptr(),
-                                         o.data_ptr(), B, H, S, S, D, bshd, bshd, bshd, bshd,
-                                         scale, False, sp)
-        _lib.check(ok, "flash_f32")
+        if bf16:
+            ok = lib.anima_hip_flash_bf16_dev(qn.data_ptr(), kn.data_ptr(), vt.data_ptr(),
+                                              o.data_ptr(), B, H, S, S, D, bshd, bshd, None,
+                                              bshd, scale, False, stp)
+        else:
+            ok = lib.anima_hip_flash_f32_dev(qn.data_ptr(), kn.data_ptr(), v.data_ptr(),
+                                             o.data_ptr(), B, H, S, S, D, bshd, bshd, bshd,
+                                             bshd, scale, False, stp)
+        _lib.check(ok, f"flash_{args.variant}")
 
     def step(ev=None):
         prologue(q, qn)
         prologue(k, kn)
+        if bf16:
+            _lib.check(lib.anima_hip_pack_vt_dev(v.data_ptr(), vt.data_ptr(), B, H, S, D, bshd,
+                                                 None, stp), "pack_vt")
         if ev is not None:
             ev[0].record(st)
         flash()
@@ -206,7 +219,7 @@ def main():
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                 "traffic": traffic_for(f"flash_{args.variant}", workload),
-                "kernel": "flash_f32_d128", "avg_launch_ms": round(ms_flash, 4)}
+                "kernel": f"flash_{args.variant}_d128", "avg_launch_ms": round(ms_flash, 4)}
 
     cpu = multi = None
     if not args.no_cpu_baseline:
@@ -219,8 +232,9 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": args.variant,
         "data": "synthetic (seeded N(0,1) q/k/v, unit RMSNorm weights)",
         "config": {"workload": workload, "B": B, "H": H, "S_q": S, "S_kv": S, "D": D,
-                   "step": "qk prologue (RMSNorm+RoPE) x2 + flash attention",
-                   "mfma": "v_mfma_f32_32x32x2_f32"},
+                   "step": "qk prologue (RMSNorm+RoPE) x2 " + ("+ V^T bf16 pack " if bf16 else "")
+                           + "+ flash attention",
+                   "mfma": "v_mfma_f32_32x32x16_bf16" if bf16 else "v_mfma_f32_32x32x2_f32"},
         "pct_mfma_peak": round(100.0 * value / peak, 2),
         "roofline": roofline,
         "cpu_baseline": cpu,

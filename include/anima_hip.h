@@ -84,6 +84,12 @@ enum {
     ANIMA_HIP_BF16 = 1  /* bf16 Q/K/V and P, f32 MFMA accumulate + softmax */
 };
 
+/* anima_rt_run_sdpa_flash with an arithmetic mode: host pointers, same
+ * layouts and semantics; mode ANIMA_HIP_F32 is identical to the drop-in,
+ * ANIMA_HIP_BF16 rounds Q, K, V (and P) to bf16 for the MFMAs (D == 128). */
+bool anima_hip_sdpa(const float *Q, const float *K, const float *V, float *out, int BH, int S_q,
+                    int S_kv, int D, float scale, bool is_causal, int mode);
+
 /* Flash attention on device f32 tensors (mode ANIMA_HIP_F32).  Same math as
  * anima_rt_run_sdpa_flash with strided [B,H,S,D] views. */
 bool anima_hip_flash_f32_dev(const float *q, const float *k, const float *v, float *o,
@@ -91,6 +97,28 @@ bool anima_hip_flash_f32_dev(const float *q, const float *k, const float *v, flo
                              const int64_t *q_strides, const int64_t *k_strides,
                              const int64_t *v_strides, const int64_t *o_strides,
                              float scale, bool is_causal, void *stream);
+
+/* Flash attention on device bf16 tensors (mode ANIMA_HIP_BF16): q, k are
+ * bf16 [B,H,S,D] views (strides as above), vt is V packed by
+ * anima_hip_pack_vt_dev, o is f32.  D must be 128 and scale > 0.  Scores,
+ * softmax and accumulation are f32; Q, K, V and P enter the MFMAs as bf16.
+ * vt_strides = {batch, head, d-row} (the d-row stride must equal
+ * anima_hip_vt_padded_len(S_kv)); NULL = packed contiguous. */
+bool anima_hip_flash_bf16_dev(const uint16_t *q, const uint16_t *k, const uint16_t *vt,
+                              float *o, int B, int H, int S_q, int S_kv, int D,
+                              const int64_t *q_strides, const int64_t *k_strides,
+                              const int64_t *vt_strides, const int64_t *o_strides,
+                              float scale, bool is_causal, void *stream);
+
+/* Key count of one packed V^T row: S_kv rounded up to a multiple of 64. */
+int64_t anima_hip_vt_padded_len(int S_kv);
+
+/* Pack f32 V ([B,H,S_kv,D] view through v_strides, D = 128) into the bf16
+ * V^T layout of anima_hip_flash_bf16_dev: per (batch, head) a
+ * [D][anima_hip_vt_padded_len(S_kv)] matrix, zero-padded, with keys permuted
+ * inside each group of 16 (offsets 4-7 and 8-11 swapped). */
+bool anima_hip_pack_vt_dev(const float *v, uint16_t *vt, int B, int H, int S_kv, int D,
+                           const int64_t *v_strides, const int64_t *vt_strides, void *stream);
 
 /* Fused per-row prologue on device memory: for each row (b, s, h) of x,
  * optional RMSNorm (flags & 1; weight w may be NULL) followed by optional
