@@ -24,6 +24,8 @@ SIGNATURES = {
     "anima_rt_run_sdpa": (_B, [_P] * 4 + [_I] * 4 + [_F, _B]),
     "anima_rt_run_rmsnorm": (_B, [_P, _P, _P, _I, _I, _F]),
     "anima_rt_run_rope": (_B, [_P, _P, _P, _I, _I, _I]),
+    "anima_rt_run_gemm_fp32": (_B, [_P] * 3 + [_I] * 3),
+    "anima_rt_run_gemm_bf16": (_B, [_P] * 3 + [_I] * 3),
     "anima_hip_last_error": (ct.c_char_p, []),
     "anima_hip_version": (_I, []),
     "anima_hip_sdpa": (_B, [_P] * 4 + [_I] * 4 + [_F, _B, _I]),
@@ -33,6 +35,15 @@ SIGNATURES = {
     "anima_hip_pack_vt_dev": (_B, [_P, _P] + [_I] * 4 + [_I64P] * 2 + [_P]),
     "anima_hip_qk_prologue_dev": (_B, [_P] * 4 + [_I] * 4 + [_I64P] * 2 + [_F, _I, _P]),
     "anima_hip_attention": (_B, [_P] * 7 + [_I] * 5 + [_F, _I]),
+    "anima_hip_gemm_dev": (_B, [_P, ct.c_int64, _P, _I, ct.c_int64, _P, ct.c_int64] + [_I] * 3
+                           + [_P]),
+    "anima_hip_attention_scratch_bytes": (ct.c_size_t, [_I] * 7),
+    "anima_hip_attention_dev": (_B, [_P] * 8 + [ct.c_size_t] + [_I] * 6 + [_F, _I, _P]),
+    "anima_hip_ctx_kv_create": (_P, [_P] * 4 + [_I] * 5 + [_F, _I]),
+    "anima_hip_ctx_kv_destroy": (None, [_P]),
+    "anima_hip_cross_attention": (_B, [_P] * 4 + [_I] * 2 + [_F]),
+    "anima_hip_cross_attention_scratch_bytes": (ct.c_size_t, [_P, _I, _I]),
+    "anima_hip_cross_attention_dev": (_B, [_P] * 5 + [ct.c_size_t] + [_I] * 2 + [_F, _P]),
 }
 
 

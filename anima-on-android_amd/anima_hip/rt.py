@@ -132,6 +132,93 @@ def attention(q, k, v, q_norm_w=None, k_norm_w=None, freqs=None, eps=1e-6,
     return out
 
 
+def gemm_fp32(a, b) -> np.ndarray:
+    """anima_rt_run_gemm_fp32: C = A . B^T (gemm_backend.cpp:140-148)."""
+    a, b = _f32(a), _f32(b)
+    M, K = a.shape
+    N = b.shape[0]
+    if b.shape != (N, K):
+        raise ValueError(f"gemm shapes a{a.shape} b{b.shape}")
+    c = np.zeros((M, N), np.float32)
+    _lib.check(_lib.load().anima_rt_run_gemm_fp32(_p(a), _p(b), _p(c), M, N, K),
+               "anima_rt_run_gemm_fp32")
+    return c
+
+
+def gemm_bf16(a, w_bits) -> np.ndarray:
+    """anima_rt_run_gemm_bf16: C = A . W^T with W as bf16 bit patterns
+    (uint16 [N, K], gemm_backend.cpp:154-173)."""
+    a = _f32(a)
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape != (N, K):
+        raise ValueError(f"gemm shapes a{a.shape} w{w.shape}")
+    c = np.zeros((M, N), np.float32)
+    _lib.check(_lib.load().anima_rt_run_gemm_bf16(_p(a), _p(w), _p(c), M, N, K),
+               "anima_rt_run_gemm_bf16")
+    return c
+
+
+class ContextKV:
+    """Cross-attention K/V of one text context, kept on the GPU
+    (anima_hip_ctx_kv_create).  K = RMSNorm_head(ctx . Wk^T), V = ctx . Wv^T,
+    computed once; every denoise step and both CFG branches reuse them.
+
+    ctx: [S_kv, C] or [Bc, S_kv, C] float32; wk_bits / wv_bits: bf16 bit
+    patterns [H*D, C] (uint16); k_norm_w: [D] or None."""
+
+    def __init__(self, ctx, wk_bits, wv_bits, k_norm_w=None, heads=16, head_dim=128, eps=1e-6,
+                 mode=F32):
+        ctx = _f32(ctx)
+        if ctx.ndim == 2:
+            ctx = ctx[None]
+        Bc, S, C = ctx.shape
+        wk = np.ascontiguousarray(wk_bits, dtype=np.uint16)
+        wv = np.ascontiguousarray(wv_bits, dtype=np.uint16)
+        if wk.shape != (heads * head_dim, C) or wv.shape != wk.shape:
+            raise ValueError(f"weights must be [{heads * head_dim}, {C}]")
+        kw = None if k_norm_w is None else _f32(k_norm_w)
+        self.batch, self.tokens, self.heads, self.head_dim = Bc, S, heads, head_dim
+        self.mode = mode
+        h = _lib.load().anima_hip_ctx_kv_create(_p(ctx), _p(wk), _p(wv), _p(kw), Bc, S, C, heads,
+                                                head_dim, ct.c_float(eps), int(mode))
+        if not h:
+            raise _lib.AnimaHipError(f"anima_hip_ctx_kv_create failed: {_lib.last_error()}")
+        self._h = ct.c_void_p(h)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def attend(self, q, q_norm_w=None, eps=1e-6) -> np.ndarray:
+        """Cross-attention of q [B, S_q, H, D] (q_proj output) against the
+        cached context; returns [B, S_q, H, D] float32."""
+        if self._h is None:
+            raise _lib.AnimaHipError("context cache already closed")
+        q = _f32(q)
+        B, Sq, H, D = q.shape
+        if (H, D) != (self.heads, self.head_dim):
+            raise ValueError(f"q heads/dim {H}x{D} != cache {self.heads}x{self.head_dim}")
+        qw = None if q_norm_w is None else _f32(q_norm_w)
+        out = np.zeros_like(q)
+        ok = _lib.load().anima_hip_cross_attention(_p(q), _p(qw), self._h, _p(out), B, Sq,
+                                                   ct.c_float(eps))
+        _lib.check(ok, "anima_hip_cross_attention")
+        return out
+
+    def close(self):
+        if getattr(self, "_h", None) is not None:
+            _lib.load().anima_hip_ctx_kv_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class AnimaRT:
     """Drop-in for NumpyDiT's ``rt`` (NumpyRT, scripts/phone_pipeline_nd.py:46-68).
 

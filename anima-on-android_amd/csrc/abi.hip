@@ -1,6 +1,7 @@
 // C-ABI layer of libanima_hip.so: argument checking, the device context
-// (device, stream, grow-only workspace) and host<->device marshaling for the
-// anima_rt drop-in entry points.  Kernels live in the other translation units.
+// (device, stream, grow-only workspace), host<->device marshaling for the
+// anima_rt drop-in entry points, and the cross-attention context K/V cache.
+// Kernels live in the other translation units.
 #include "common.h"
 
 #include "anima_hip.h"
@@ -39,14 +40,12 @@ struct DevBuf {
     {
         if (bytes <= cap)
             return true;
-        if (p) {
-            (void)hipFree(p);
-            p = nullptr;
-            cap = 0;
-        }
+        release();
         const size_t want = std::max<size_t>(bytes, 256);
-        if (!hip_ok(hipMalloc(&p, want), what))
+        if (!hip_ok(hipMalloc(&p, want), what)) {
+            p = nullptr;
             return false;
+        }
         cap = want;
         return true;
     }
@@ -61,11 +60,11 @@ struct DevBuf {
 
 struct Runtime {
     std::recursive_mutex mu;
-    bool ready = false;        // device + stream exist
-    bool user_init = false;    // anima_rt_init() succeeded (gates rmsnorm/math sdpa)
+    bool ready = false;      // device + stream exist
+    bool user_init = false;  // anima_rt_init() succeeded (gates rmsnorm / math sdpa)
     int device = 0;
     hipStream_t stream = nullptr;
-    DevBuf q, k, v, o, w0, w1, fr, q2, k2, v2;
+    DevBuf q, k, v, o, w0, w1, fr, q2, k2, v2, scratch;
 };
 
 Runtime &rt()
@@ -89,6 +88,15 @@ bool ensure_ready(Runtime &r)
         return false;
     r.ready = true;
     return true;
+}
+
+// Context check for the device-pointer entries: the mutex is held only to
+// create the context once, never across the launches themselves.
+bool ready_for_device_call()
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    return ensure_ready(r);
 }
 
 // Device entry points run on the caller's stream; NULL is HIP's default
@@ -128,7 +136,7 @@ bool sync(hipStream_t st) { return hip_ok(hipStreamSynchronize(st), "hipStreamSy
 
 // Shared body of the host-pointer SDPA entries ([BH, S, D] f32 host arrays).
 bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int BH, int S_q,
-               int S_kv, int D, float scale, bool causal, bool bf16 = false)
+               int S_kv, int D, float scale, bool causal, bool bf16)
 {
     if (!check_dims(1, BH, S_q, S_kv, D))
         return false;
@@ -137,6 +145,8 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
         return true;
     if (!Q || !out || (nk > 0 && (!K || !V)))
         return fail("sdpa: null pointer");
+    if (bf16 && D != 128)
+        return fail("sdpa: the bf16 mode needs D == 128");
     Runtime &r = rt();
     const hipStream_t st = r.stream;
     if (!r.q.reserve(f32_bytes(nq), "workspace Q") || !r.o.reserve(f32_bytes(nq), "workspace O") ||
@@ -160,8 +170,6 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
     p.scale = scale;
     p.causal = causal;
     if (bf16) {
-        if (D != 128)
-            return fail("sdpa: the bf16 mode needs D == 128");
         // bf16 copies of Q and K (row kernel without norm/RoPE) and packed V^T.
         const int64_t sp = vt_padded_len(S_kv);
         if (!r.q2.reserve(nq * 2, "workspace q bf16") || !r.k2.reserve(nk * 2, "workspace k bf16") ||
@@ -204,10 +212,58 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
     return sync(st);
 }
 
+// Host -> device copy of an optional per-head weight or RoPE table.
+bool upload_optional(DevBuf &buf, const float *src, size_t n, const char *what, hipStream_t st,
+                     const float *&dev)
+{
+    dev = nullptr;
+    if (!src)
+        return true;
+    if (!buf.reserve(f32_bytes(n), what) || !h2d(buf.p, src, f32_bytes(n), st))
+        return false;
+    dev = static_cast<const float *>(buf.p);
+    return true;
+}
+
+bool host_gemm(const float *A, const void *W, bool w_bf16, float *C, int M, int N, int K)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!ensure_ready(r))
+        return false;
+    if (M < 0 || N < 0 || K < 0)
+        return fail("gemm: negative dimension");
+    if (int64_t(M) * N == 0)
+        return true;
+    if (!C || (K > 0 && (!A || !W)))
+        return fail("gemm: null pointer");
+    const hipStream_t st = r.stream;
+    const size_t wbytes = size_t(N) * K * (w_bf16 ? 2 : 4);
+    if (!r.q.reserve(f32_bytes(int64_t(M) * K), "workspace A") ||
+        !r.k.reserve(wbytes, "workspace W") || !r.o.reserve(f32_bytes(int64_t(M) * N), "workspace C"))
+        return false;
+    if (!h2d(r.q.p, A, f32_bytes(int64_t(M) * K), st) || !h2d(r.k.p, W, wbytes, st))
+        return false;
+    if (!launch_gemm(static_cast<const float *>(r.q.p), K, r.k.p, w_bf16, K,
+                     static_cast<float *>(r.o.p), N, M, N, K, st) ||
+        !d2h(C, r.o.p, f32_bytes(int64_t(M) * N), st))
+        return false;
+    return sync(st);
+}
+
 }  // namespace
 }  // namespace anima_hip
 
 using namespace anima_hip;
+
+// Device-resident K/V of one text context (see anima_hip_ctx_kv_create).
+struct anima_hip_ctx_kv {
+    int mode = ANIMA_HIP_F32;
+    int Bc = 0, S_kv = 0, H = 0, D = 0;
+    int device = 0;
+    void *k = nullptr;  // prepared K (layout per mode, see AttnInputs)
+    void *v = nullptr;  // prepared V (f32 rows or packed bf16 V^T)
+};
 
 extern "C" {
 
@@ -228,7 +284,7 @@ void anima_rt_destroy(void)
     if (!r.ready)
         return;
     (void)hipStreamSynchronize(r.stream);
-    for (DevBuf *b : {&r.q, &r.k, &r.v, &r.o, &r.w0, &r.w1, &r.fr, &r.q2, &r.k2, &r.v2})
+    for (DevBuf *b : {&r.q, &r.k, &r.v, &r.o, &r.w0, &r.w1, &r.fr, &r.q2, &r.k2, &r.v2, &r.scratch})
         b->release();
     (void)hipStreamDestroy(r.stream);
     r.stream = nullptr;
@@ -243,7 +299,7 @@ bool anima_rt_run_sdpa_flash(const float *Q, const float *K, const float *V, flo
     std::lock_guard<std::recursive_mutex> g(r.mu);
     if (!ensure_ready(r))
         return false;
-    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale, is_causal);
+    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale, is_causal, false);
 }
 
 bool anima_rt_run_sdpa(const float *Q, const float *K, const float *V, float *out, int BH,
@@ -254,7 +310,7 @@ bool anima_rt_run_sdpa(const float *Q, const float *K, const float *V, float *ou
     if (!r.user_init)
         return fail("anima_rt_run_sdpa: anima_rt_init() has not been called");
     // The reference multiplies both Q and K by `scale`: softmax(scale^2 QK^T)V.
-    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale * scale, is_causal);
+    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale * scale, is_causal, false);
 }
 
 bool anima_rt_run_rmsnorm(const float *x, const float *w, float *out, int m, int d, float eps)
@@ -273,14 +329,13 @@ bool anima_rt_run_rmsnorm(const float *x, const float *w, float *out, int m, int
     const hipStream_t st = r.stream;
     if (!r.q.reserve(f32_bytes(n), "workspace x") || !r.o.reserve(f32_bytes(n), "workspace y"))
         return false;
-    if (w && !r.w0.reserve(f32_bytes(d), "workspace w"))
-        return false;
-    if (!h2d(r.q.p, x, f32_bytes(n), st) || (w && !h2d(r.w0.p, w, f32_bytes(d), st)))
+    const float *wd = nullptr;
+    if (!h2d(r.q.p, x, f32_bytes(n), st) || !upload_optional(r.w0, w, d, "workspace w", st, wd))
         return false;
     RowProblem p;
     p.x = static_cast<const float *>(r.q.p);
     p.out = r.o.p;
-    p.w = w ? static_cast<const float *>(r.w0.p) : nullptr;
+    p.w = wd;
     p.freqs = nullptr;
     p.xs = p.os = Strides{0, 0, int64_t(d)};
     p.B = 1;
@@ -332,6 +387,16 @@ bool anima_rt_run_rope(const float *t, const float *freqs, float *out, int N, in
     return sync(st);
 }
 
+bool anima_rt_run_gemm_fp32(const float *A, const float *B, float *C, int M, int N, int K)
+{
+    return host_gemm(A, B, false, C, M, N, K);
+}
+
+bool anima_rt_run_gemm_bf16(const float *A, const uint16_t *W, float *C, int M, int N, int K)
+{
+    return host_gemm(A, W, true, C, M, N, K);
+}
+
 bool anima_hip_sdpa(const float *Q, const float *K, const float *V, float *out, int BH, int S_q,
                     int S_kv, int D, float scale, bool is_causal, int mode)
 {
@@ -353,13 +418,7 @@ bool anima_hip_flash_f32_dev(const float *q, const float *k, const float *v, flo
                              const int64_t *k_strides, const int64_t *v_strides,
                              const int64_t *o_strides, float scale, bool is_causal, void *stream)
 {
-    Runtime &r = rt();
-    {
-        std::lock_guard<std::recursive_mutex> g(r.mu);
-        if (!ensure_ready(r))
-            return false;
-    }
-    if (!check_dims(B, H, S_q, S_kv, D))
+    if (!ready_for_device_call() || !check_dims(B, H, S_q, S_kv, D))
         return false;
     if (int64_t(B) * H * S_q * D > 0 && (!q || !o || (S_kv > 0 && (!k || !v))))
         return fail("flash_f32_dev: null pointer");
@@ -387,13 +446,7 @@ bool anima_hip_flash_bf16_dev(const uint16_t *q, const uint16_t *k, const uint16
                               const int64_t *k_strides, const int64_t *vt_strides,
                               const int64_t *o_strides, float scale, bool is_causal, void *stream)
 {
-    Runtime &r = rt();
-    {
-        std::lock_guard<std::recursive_mutex> g(r.mu);
-        if (!ensure_ready(r))
-            return false;
-    }
-    if (!check_dims(B, H, S_q, S_kv, D))
+    if (!ready_for_device_call() || !check_dims(B, H, S_q, S_kv, D))
         return false;
     if (int64_t(B) * H * S_q * D > 0 && (!q || !o || (S_kv > 0 && (!k || !vt))))
         return fail("flash_bf16_dev: null pointer");
@@ -423,13 +476,7 @@ int64_t anima_hip_vt_padded_len(int S_kv) { return S_kv > 0 ? vt_padded_len(S_kv
 bool anima_hip_pack_vt_dev(const float *v, uint16_t *vt, int B, int H, int S_kv, int D,
                            const int64_t *v_strides, const int64_t *vt_strides, void *stream)
 {
-    Runtime &r = rt();
-    {
-        std::lock_guard<std::recursive_mutex> g(r.mu);
-        if (!ensure_ready(r))
-            return false;
-    }
-    if (!check_dims(B, H, S_kv, S_kv, D))
+    if (!ready_for_device_call() || !check_dims(B, H, S_kv, S_kv, D))
         return false;
     if (int64_t(B) * H * S_kv * D > 0 && (!v || !vt))
         return fail("pack_vt_dev: null pointer");
@@ -446,12 +493,8 @@ bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const 
                                int B, int S, int H, int D, const int64_t *x_strides,
                                const int64_t *out_strides, float eps, int flags, void *stream)
 {
-    Runtime &r = rt();
-    {
-        std::lock_guard<std::recursive_mutex> g(r.mu);
-        if (!ensure_ready(r))
-            return false;
-    }
+    if (!ready_for_device_call())
+        return false;
     if (B < 0 || S < 0 || H < 0 || D < 0)
         return fail("qk_prologue: negative dimension");
     if (int64_t(B) * S * H * D > 0 && (!x || !out))
@@ -474,15 +517,66 @@ bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const 
     return launch_rows(p, pick_stream(stream));
 }
 
+bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, int64_t ldw,
+                        float *c, int64_t ldc, int M, int N, int K, void *stream)
+{
+    if (!ready_for_device_call())
+        return false;
+    if (int64_t(M) * N > 0 && (!c || (K > 0 && (!a || !w))))
+        return fail("gemm_dev: null pointer");
+    return launch_gemm(a, lda, w, w_bf16 != 0, ldw, c, ldc, M, N, K, pick_stream(stream));
+}
+
+size_t anima_hip_attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D,
+                                         int mode)
+{
+    if (B < 0 || S_q < 0 || Bk < 0 || S_kv < 0 || H < 0 || D < 0)
+        return 0;
+    return attention_scratch_bytes(B, S_q, Bk, S_kv, H, D, mode == ANIMA_HIP_BF16, false);
+}
+
+bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
+                             const float *q_norm_w, const float *k_norm_w, const float *freqs,
+                             float *out, void *scratch, size_t scratch_bytes, int B, int S_q,
+                             int Bk, int S_kv, int H, int D, float eps, int mode, void *stream)
+{
+    if (!ready_for_device_call() || !check_dims(B, H, S_q, S_kv, D))
+        return false;
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16)
+        return fail("attention_dev: unknown mode " + std::to_string(mode));
+    if (int64_t(B) * S_q * H * D == 0)
+        return true;
+    const bool bf16 = mode == ANIMA_HIP_BF16;
+    if (!q || !out || !scratch || (S_kv > 0 && (!k || !v)))
+        return fail("attention_dev: null pointer");
+    if (scratch_bytes < attention_scratch_bytes(B, S_q, Bk, S_kv, H, D, bf16, false))
+        return fail("attention_dev: scratch smaller than anima_hip_attention_scratch_bytes()");
+    AttnInputs in;
+    in.q = q;
+    in.q_norm_w = q_norm_w;
+    in.freqs = freqs;
+    in.k = k;
+    in.v = v;
+    in.k_norm_w = k_norm_w;
+    in.out = out;
+    in.B = B;
+    in.Bk = Bk;
+    in.S_q = S_q;
+    in.S_kv = S_kv;
+    in.H = H;
+    in.D = D;
+    in.eps = eps;
+    in.bf16 = bf16;
+    return run_attention(in, scratch, pick_stream(stream));
+}
+
 bool anima_hip_attention(const float *q, const float *k, const float *v, const float *q_norm_w,
                          const float *k_norm_w, const float *freqs, float *out, int B, int S_q,
                          int S_kv, int H, int D, float eps, int mode)
 {
     Runtime &r = rt();
     std::lock_guard<std::recursive_mutex> g(r.mu);
-    if (!ensure_ready(r))
-        return false;
-    if (!check_dims(B, H, S_q, S_kv, D))
+    if (!ensure_ready(r) || !check_dims(B, H, S_q, S_kv, D))
         return false;
     if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16)
         return fail("anima_hip_attention: unknown mode " + std::to_string(mode));
@@ -497,68 +591,204 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
     if (!q || !out || (nk > 0 && (!k || !v)))
         return fail("anima_hip_attention: null pointer");
     const hipStream_t st = r.stream;
-    const int64_t nf = freqs ? int64_t(S_q) * D * 2 : 0;
-    const int64_t sp = vt_padded_len(S_kv);
-    const size_t vt_bytes = size_t(B) * H * D * sp * sizeof(uint16_t);
+    const size_t scratch = attention_scratch_bytes(B, S_q, B, S_kv, H, D, bf16, false);
     if (!r.q.reserve(f32_bytes(nq), "workspace q") || !r.k.reserve(f32_bytes(nk), "workspace k") ||
         !r.v.reserve(f32_bytes(nk), "workspace v") || !r.o.reserve(f32_bytes(nq), "workspace o") ||
-        !r.q2.reserve(f32_bytes(nq), "workspace q'") || !r.k2.reserve(f32_bytes(nk), "workspace k'") ||
-        (bf16 && !r.v2.reserve(vt_bytes, "workspace v^T")))
+        !r.scratch.reserve(scratch, "workspace scratch"))
         return false;
-    if ((q_norm_w && !r.w0.reserve(f32_bytes(D), "workspace q_norm")) ||
-        (k_norm_w && !r.w1.reserve(f32_bytes(D), "workspace k_norm")) ||
-        (nf && !r.fr.reserve(f32_bytes(nf), "workspace freqs")))
-        return false;
+    AttnInputs in;
     if (!h2d(r.q.p, q, f32_bytes(nq), st) || !h2d(r.k.p, k, f32_bytes(nk), st) ||
         !h2d(r.v.p, v, f32_bytes(nk), st) ||
-        (q_norm_w && !h2d(r.w0.p, q_norm_w, f32_bytes(D), st)) ||
-        (k_norm_w && !h2d(r.w1.p, k_norm_w, f32_bytes(D), st)) ||
-        (nf && !h2d(r.fr.p, freqs, f32_bytes(nf), st)))
+        !upload_optional(r.w0, q_norm_w, D, "workspace q_norm", st, in.q_norm_w) ||
+        !upload_optional(r.w1, k_norm_w, D, "workspace k_norm", st, in.k_norm_w) ||
+        !upload_optional(r.fr, freqs, size_t(S_q) * D * 2, "workspace freqs", st, in.freqs))
         return false;
-    // [B, S, H, D] viewed as [B, H, S, D]: strides {S*H*D, D, H*D}.
-    const Strides qv{int64_t(S_q) * H * D, int64_t(D), int64_t(H) * D};
-    const Strides kv{int64_t(S_kv) * H * D, int64_t(D), int64_t(H) * D};
-    RowProblem pq;
-    pq.x = static_cast<const float *>(r.q.p);
-    pq.out = r.q2.p;
-    pq.w = q_norm_w ? static_cast<const float *>(r.w0.p) : nullptr;
-    pq.freqs = nf ? static_cast<const float *>(r.fr.p) : nullptr;
-    pq.xs = pq.os = qv;
-    pq.B = B;
-    pq.S = S_q;
-    pq.H = H;
-    pq.D = D;
-    pq.eps = eps;
-    pq.norm = true;
-    pq.out_bf16 = bf16;
-    RowProblem pk = pq;
-    pk.x = static_cast<const float *>(r.k.p);
-    pk.out = r.k2.p;
-    pk.w = k_norm_w ? static_cast<const float *>(r.w1.p) : nullptr;
-    pk.xs = pk.os = kv;
-    pk.S = S_kv;
-    if (!launch_rows(pq, st) || !launch_rows(pk, st))
+    in.q = static_cast<const float *>(r.q.p);
+    in.k = static_cast<const float *>(r.k.p);
+    in.v = static_cast<const float *>(r.v.p);
+    in.out = static_cast<float *>(r.o.p);
+    in.B = B;
+    in.Bk = B;
+    in.S_q = S_q;
+    in.S_kv = S_kv;
+    in.H = H;
+    in.D = D;
+    in.eps = eps;
+    in.bf16 = bf16;
+    if (!run_attention(in, r.scratch.p, st) || !d2h(out, r.o.p, f32_bytes(nq), st))
         return false;
-    const Strides vts{int64_t(H) * D * sp, int64_t(D) * sp, sp};
-    if (bf16 && !launch_vt_pack(static_cast<const float *>(r.v.p), kv,
-                                static_cast<uint16_t *>(r.v2.p), vts, B, H, S_kv, D, st))
+    return sync(st);
+}
+
+anima_hip_ctx_kv *anima_hip_ctx_kv_create(const float *ctx, const uint16_t *wk, const uint16_t *wv,
+                                          const float *k_norm_w, int Bc, int S_kv, int C, int H,
+                                          int D, float eps, int mode)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!ensure_ready(r))
+        return nullptr;
+    if (Bc <= 0 || S_kv <= 0 || C <= 0 || H <= 0 || D <= 0) {
+        fail("ctx_kv_create: all dimensions must be positive");
+        return nullptr;
+    }
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16) {
+        fail("ctx_kv_create: unknown mode " + std::to_string(mode));
+        return nullptr;
+    }
+    const bool bf16 = mode == ANIMA_HIP_BF16;
+    if (bf16 && D != 128) {
+        fail("ctx_kv_create: the bf16 mode needs D == 128");
+        return nullptr;
+    }
+    if (!ctx || !wk || !wv) {
+        fail("ctx_kv_create: null pointer");
+        return nullptr;
+    }
+    const hipStream_t st = r.stream;
+    const int M = Bc * S_kv, N = H * D;
+    const size_t wbytes = size_t(N) * C * 2;
+    DevBuf kf, vf;
+    const float *kw = nullptr;
+    if (!r.q.reserve(f32_bytes(int64_t(M) * C), "workspace ctx") ||
+        !r.k.reserve(wbytes, "workspace Wk") || !r.v.reserve(wbytes, "workspace Wv") ||
+        !kf.reserve(f32_bytes(int64_t(M) * N), "ctx K projection") ||
+        !vf.reserve(f32_bytes(int64_t(M) * N), "ctx V projection") ||
+        !h2d(r.q.p, ctx, f32_bytes(int64_t(M) * C), st) || !h2d(r.k.p, wk, wbytes, st) ||
+        !h2d(r.v.p, wv, wbytes, st) ||
+        !upload_optional(r.w1, k_norm_w, D, "workspace k_norm", st, kw)) {
+        (void)hipStreamSynchronize(st);
+        kf.release();
+        vf.release();
+        return nullptr;
+    }
+    auto *kv = new anima_hip_ctx_kv;
+    kv->mode = mode;
+    kv->Bc = Bc;
+    kv->S_kv = S_kv;
+    kv->H = H;
+    kv->D = D;
+    kv->device = r.device;
+    bool ok = launch_gemm(static_cast<const float *>(r.q.p), C, r.k.p, true, C,
+                          static_cast<float *>(kf.p), N, M, N, C, st) &&
+              launch_gemm(static_cast<const float *>(r.q.p), C, r.v.p, true, C,
+                          static_cast<float *>(vf.p), N, M, N, C, st);
+    if (ok && bf16) {
+        ok = hip_ok(hipMalloc(&kv->k, prepared_k_bytes(Bc, S_kv, H, D, true)), "ctx K cache") &&
+             hip_ok(hipMalloc(&kv->v, prepared_v_bytes(Bc, S_kv, H, D, true)), "ctx V cache") &&
+             prepare_kv(static_cast<const float *>(kf.p), static_cast<const float *>(vf.p), kw,
+                        nullptr, kv->k, kv->v, Bc, S_kv, H, D, eps, true, st) &&
+             sync(st);
+    } else if (ok) {
+        // f32: normalise K in place (each row is staged in LDS before it is
+        // rewritten); the two projections become the cache.
+        ok = prepare_kv(static_cast<const float *>(kf.p), nullptr, kw, nullptr, kf.p, nullptr, Bc,
+                        S_kv, H, D, eps, false, st) &&
+             sync(st);
+        if (ok) {
+            kv->k = kf.p;
+            kv->v = vf.p;
+            kf.p = vf.p = nullptr;
+        }
+    }
+    (void)hipStreamSynchronize(st);
+    kf.release();
+    vf.release();
+    if (!ok) {
+        if (kv->k)
+            (void)hipFree(kv->k);
+        if (kv->v)
+            (void)hipFree(kv->v);
+        delete kv;
+        return nullptr;
+    }
+    return kv;
+}
+
+void anima_hip_ctx_kv_destroy(anima_hip_ctx_kv *kv)
+{
+    if (!kv)
+        return;
+    // Work that may still read the cache can sit on any stream: drain the device.
+    (void)hipDeviceSynchronize();
+    if (kv->k)
+        (void)hipFree(kv->k);
+    if (kv->v)
+        (void)hipFree(kv->v);
+    delete kv;
+}
+
+size_t anima_hip_cross_attention_scratch_bytes(const anima_hip_ctx_kv *kv, int B, int S_q)
+{
+    if (!kv || B < 0 || S_q < 0)
+        return 0;
+    return attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D,
+                                   kv->mode == ANIMA_HIP_BF16, true);
+}
+
+bool anima_hip_cross_attention_dev(const float *q, const float *q_norm_w,
+                                   const anima_hip_ctx_kv *kv, float *out, void *scratch,
+                                   size_t scratch_bytes, int B, int S_q, float eps, void *stream)
+{
+    if (!ready_for_device_call())
         return false;
-    FlashProblem p;
-    p.q = r.q2.p;
-    p.k = r.k2.p;
-    p.v = bf16 ? r.v2.p : r.v.p;
-    p.o = static_cast<float *>(r.o.p);
-    p.qs = p.os = qv;
-    p.ks = kv;
-    p.vs = bf16 ? vts : kv;
-    p.B = B;
-    p.H = H;
-    p.S_q = S_q;
-    p.S_kv = S_kv;
-    p.D = D;
-    p.scale = float(1.0 / std::sqrt(double(D)));  // as NumpyRT.run_sdpa passes it
-    p.causal = false;
-    if (!(bf16 ? launch_flash_bf16(p, st) : launch_flash_f32(p, st)) ||
+    if (!kv)
+        return fail("cross_attention_dev: null cache handle");
+    if (B < 0 || S_q < 0)
+        return fail("cross_attention_dev: negative dimension");
+    if (int64_t(B) * S_q == 0)
+        return true;
+    if (!q || !out || !scratch)
+        return fail("cross_attention_dev: null pointer");
+    const bool bf16 = kv->mode == ANIMA_HIP_BF16;
+    if (scratch_bytes < attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D, bf16, true))
+        return fail("cross_attention_dev: scratch smaller than "
+                    "anima_hip_cross_attention_scratch_bytes()");
+    AttnInputs in;
+    in.q = q;
+    in.q_norm_w = q_norm_w;
+    in.k_prep = kv->k;
+    in.v_prep = kv->v;
+    in.out = out;
+    in.B = B;
+    in.Bk = kv->Bc;
+    in.S_q = S_q;
+    in.S_kv = kv->S_kv;
+    in.H = kv->H;
+    in.D = kv->D;
+    in.eps = eps;
+    in.bf16 = bf16;
+    return run_attention(in, scratch, pick_stream(stream));
+}
+
+bool anima_hip_cross_attention(const float *q, const float *q_norm_w, const anima_hip_ctx_kv *kv,
+                               float *out, int B, int S_q, float eps)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!ensure_ready(r))
+        return false;
+    if (!kv)
+        return fail("cross_attention: null cache handle");
+    if (B < 0 || S_q < 0)
+        return fail("cross_attention: negative dimension");
+    const int64_t nq = int64_t(B) * S_q * kv->H * kv->D;
+    if (nq == 0)
+        return true;
+    if (!q || !out)
+        return fail("cross_attention: null pointer");
+    const hipStream_t st = r.stream;
+    const bool bf16 = kv->mode == ANIMA_HIP_BF16;
+    const size_t scratch =
+        attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D, bf16, true);
+    const float *qw = nullptr;
+    if (!r.q.reserve(f32_bytes(nq), "workspace q") || !r.o.reserve(f32_bytes(nq), "workspace o") ||
+        !r.scratch.reserve(scratch, "workspace scratch") || !h2d(r.q.p, q, f32_bytes(nq), st) ||
+        !upload_optional(r.w0, q_norm_w, kv->D, "workspace q_norm", st, qw))
+        return false;
+    if (!anima_hip_cross_attention_dev(static_cast<const float *>(r.q.p), qw, kv,
+                                       static_cast<float *>(r.o.p), r.scratch.p, scratch, B, S_q,
+                                       eps, st) ||
         !d2h(out, r.o.p, f32_bytes(nq), st))
         return false;
     return sync(st);

@@ -59,6 +59,11 @@ __host__ __device__ inline int vt_key_pos(int c)
 bool launch_vt_pack(const float *v, Strides vs, uint16_t *vt, Strides vts, int B, int H,
                     int S_kv, int D, hipStream_t st);
 
+// C[M,N] = A[M,K] . W[N,K]^T with f32 A/C and bf16 (w_bf16) or f32 W, f32
+// accumulation; leading dimensions in elements.
+bool launch_gemm(const float *a, int64_t lda, const void *w, bool w_bf16, int64_t ldw, float *c,
+                 int64_t ldc, int M, int N, int K, hipStream_t st);
+
 // Per-row RMSNorm (+ optional RoPE) "prologue".
 //   x:   rows indexed (b, s, h) through `xs` (D contiguous), f32
 //   out: same indexing through `os`, f32 or bf16 (out_bf16)
@@ -76,5 +81,31 @@ struct RowProblem {
     bool out_bf16;  // write bf16 (round to nearest even) instead of f32
 };
 bool launch_rows(const RowProblem &p, hipStream_t st);
+
+// ---- Composite attention core (attention.hip) ----
+// Prepared K/V layouts: f32 mode K and V f32 [Bk, S_kv, H, D]; bf16 mode K
+// bf16 [Bk, S_kv, H, D] and V packed bf16 V^T [Bk, H, D, vt_padded_len(S_kv)].
+struct AttnInputs {
+    const float *q = nullptr;         // [B, S_q, H, D] f32 projections
+    const float *q_norm_w = nullptr;  // [D] or null
+    const float *freqs = nullptr;     // [S_q, D/2, 2, 2] or null (self-attention)
+    const float *k = nullptr;         // raw [Bk, S_kv, H, D] f32 (when not prepared)
+    const float *v = nullptr;
+    const float *k_norm_w = nullptr;
+    const void *k_prep = nullptr;     // prepared K/V (context cache), or null
+    const void *v_prep = nullptr;
+    float *out = nullptr;             // [B, S_q, H, D] f32
+    int B = 0, Bk = 0, S_q = 0, S_kv = 0, H = 0, D = 0;
+    float eps = 1e-6f;
+    bool bf16 = false;
+};
+size_t prepared_k_bytes(int Bk, int S_kv, int H, int D, bool bf16);
+size_t prepared_v_bytes(int Bk, int S_kv, int H, int D, bool bf16);
+size_t attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D, bool bf16,
+                               bool kv_prepared);
+bool prepare_kv(const float *k, const float *v, const float *k_norm_w, const float *freqs,
+                void *k_out, void *v_out, int Bk, int S_kv, int H, int D, float eps, bool bf16,
+                hipStream_t st);
+bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st);
 
 }  // namespace anima_hip

@@ -200,27 +200,56 @@ __global__ __launch_bounds__(256) void rows_d128(RowArgs a)
         inv[t] = f;
     }
     __syncthreads();
-#pragma unroll 2
-    for (int i = 0; i < 8; ++i) {
-        const int f = t + 256 * i;
-        const int rr = f >> 5, c4 = f & 31;
+    // Each thread owns the four rotation pairs (p, p+64), p = p0..p0+3, of
+    // one row per iteration: the weights come once into registers, a row
+    // needs one float4 of the RoPE table per pair, and both halves are
+    // written as float4 (or 4 x bf16).
+    const int p0 = 4 * (t & 15);
+    f32x4 wl = f32x4{1.f, 1.f, 1.f, 1.f}, wh = wl;
+    if (a.norm && a.w) {
+        wl = *reinterpret_cast<const f32x4 *>(a.w + p0);
+        wh = *reinterpret_cast<const f32x4 *>(a.w + 64 + p0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int rr = (t >> 4) + 16 * i;
         if (rr >= nrows)
             continue;
         const float *row = xs + rr * kPitch128;
         const float fi = inv[rr];
-        const int s = spos[rr];
-        float o[4];
+        f32x4 ya = *reinterpret_cast<const f32x4 *>(row + p0);
+        f32x4 yb = *reinterpret_cast<const f32x4 *>(row + 64 + p0);
+        if (a.norm) {
+            ya = ya * fi;
+            yb = yb * fi;
+            if (a.w) {
+                ya = ya * wl;
+                yb = yb * wh;
+            }
+        }
+        f32x4 lo = ya, hi = yb;
+        if (a.freqs) {
+            const f32x4 *fq = reinterpret_cast<const f32x4 *>(a.freqs + int64_t(spos[rr]) * 256 + 4 * p0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            o[e] = out_elem(a, row, fi, s, 4 * c4 + e);
-        const int64_t oo = ooff[rr] + 4 * c4;
+            for (int e = 0; e < 4; ++e) {
+                const f32x4 r = fq[e];  // [c00, c01, c10, c11] of pair p0 + e
+                lo[e] = r.x * ya[e] + r.y * yb[e];
+                hi[e] = r.z * ya[e] + r.w * yb[e];
+            }
+        }
+        const int64_t oo = ooff[rr] + p0;
         if (a.out_bf16) {
-            const unsigned int lo = f32_to_bf16_rne(o[0]) | (unsigned(f32_to_bf16_rne(o[1])) << 16);
-            const unsigned int hi = f32_to_bf16_rne(o[2]) | (unsigned(f32_to_bf16_rne(o[3])) << 16);
-            *reinterpret_cast<uint2 *>(static_cast<unsigned short *>(a.out) + oo) = uint2{lo, hi};
+            unsigned short *ob = static_cast<unsigned short *>(a.out) + oo;
+            *reinterpret_cast<uint2 *>(ob) =
+                uint2{f32_to_bf16_rne(lo[0]) | (unsigned(f32_to_bf16_rne(lo[1])) << 16),
+                      f32_to_bf16_rne(lo[2]) | (unsigned(f32_to_bf16_rne(lo[3])) << 16)};
+            *reinterpret_cast<uint2 *>(ob + 64) =
+                uint2{f32_to_bf16_rne(hi[0]) | (unsigned(f32_to_bf16_rne(hi[1])) << 16),
+                      f32_to_bf16_rne(hi[2]) | (unsigned(f32_to_bf16_rne(hi[3])) << 16)};
         } else {
-            *reinterpret_cast<f32x4 *>(static_cast<float *>(a.out) + oo) =
-                f32x4{o[0], o[1], o[2], o[3]};
+            float *of = static_cast<float *>(a.out) + oo;
+            *reinterpret_cast<f32x4 *>(of) = lo;
+            *reinterpret_cast<f32x4 *>(of + 64) = hi;
         }
     }
 }
@@ -253,7 +282,8 @@ bool launch_rows(const RowProblem &p, hipStream_t st)
         return (reinterpret_cast<uintptr_t>(ptr) & (m - 1)) == 0;
     };
     const auto st4 = [](const Strides &x) { return x.b % 4 == 0 && x.h % 4 == 0 && x.s % 4 == 0; };
-    if (p.D == 128 && al(p.x, 16) && al(p.out, p.out_bf16 ? 8 : 16) && st4(p.xs) && st4(p.os)) {
+    if (p.D == 128 && al(p.x, 16) && al(p.out, p.out_bf16 ? 8 : 16) && st4(p.xs) && st4(p.os) &&
+        (!p.w || al(p.w, 16)) && (!p.freqs || al(p.freqs, 16))) {
         a.rows_per_block = kRows128;
         const int64_t nblk = (rows + kRows128 - 1) / kRows128;
         if (nblk > INT32_MAX)

@@ -27,6 +27,7 @@
 #define ANIMA_HIP_H
 
 #include <stdbool.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -69,6 +70,17 @@ bool anima_rt_run_rmsnorm(const float *x, const float *w, float *out, int m, int
  * anima_rt/include/cpu/rope_kernel.h:65-97).  t,out: [N, S, D];
  * freqs: [S, D/2, 2, 2].  Bit-identical to the reference. */
 bool anima_rt_run_rope(const float *t, const float *freqs, float *out, int N, int S, int D);
+
+/* Replaces anima_rt_run_gemm_fp32 (anima_rt/src/gemm_backend.cpp:140-148):
+ * C[M,N] = A[M,K] . B[N,K]^T, f32 host arrays, f32 accumulation.  Off the
+ * attention path; exported so the library can stand in for all of libanima_rt's
+ * GEMM symbols. */
+bool anima_rt_run_gemm_fp32(const float *A, const float *B, float *C, int M, int N, int K);
+
+/* Replaces anima_rt_run_gemm_bf16 (gemm_backend.cpp:154-173):
+ * C[M,N] = A[M,K] . W[N,K]^T with W as bf16 bit patterns (uint16), A and C
+ * f32, f32 accumulation. */
+bool anima_rt_run_gemm_bf16(const float *A, const uint16_t *W, float *C, int M, int N, int K);
 
 /* ===================== Part 2: extensions ===================== */
 
@@ -131,6 +143,25 @@ bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const 
                                const int64_t *x_strides, const int64_t *out_strides,
                                float eps, int flags, void *stream);
 
+/* C[M,N] = A[M,K] . W[N,K]^T on device memory; W is bf16 bit patterns when
+ * w_bf16 != 0, else f32; leading dimensions in elements. */
+bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, int64_t ldw,
+                        float *c, int64_t ldc, int M, int N, int K, void *stream);
+
+/* Device scratch needed by anima_hip_attention_dev for these sizes (bytes). */
+size_t anima_hip_attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D,
+                                         int mode);
+
+/* Device-memory form of anima_hip_attention: q [B,S_q,H,D], k/v
+ * [Bk,S_kv,H,D] f32 projections with Bk == B or Bk == 1 (one K/V batch shared
+ * by every query batch); weights [D] and RoPE table [S_q,D/2,2,2] may be NULL;
+ * out [B,S_q,H,D] f32.  `scratch` holds at least
+ * anima_hip_attention_scratch_bytes() bytes; nothing is allocated. */
+bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
+                             const float *q_norm_w, const float *k_norm_w, const float *freqs,
+                             float *out, void *scratch, size_t scratch_bytes, int B, int S_q,
+                             int Bk, int S_kv, int H, int D, float eps, int mode, void *stream);
+
 /* One-call core of NumpyAttention.forward (numpy_dit.py:283-294) on host
  * memory: q [B,S_q,H,D], k/v [B,S_kv,H,D] (the projections), optional
  * per-head RMSNorm weights [D], optional RoPE table [S_q, D/2, 2, 2]
@@ -141,6 +172,39 @@ bool anima_hip_attention(const float *q, const float *k, const float *v,
                          const float *q_norm_w, const float *k_norm_w, const float *freqs,
                          float *out, int B, int S_q, int S_kv, int H, int D, float eps,
                          int mode);
+
+/* ---- Cross-attention over a cached text context ----
+ * The context K/V of a cross-attention block depend only on the text context
+ * and the block's weights, not on the latent or the denoise step
+ * (anima_rt/scripts/sampling.py:121-138 feeds the same context every step;
+ * numpy_dit.py:277-286 recomputes the projections and k_norm each call).  A
+ * cache holds them on the GPU in the attention layout of `mode`:
+ *   K = RMSNorm_head(ctx . Wk^T) (k_norm weight, eps), V = ctx . Wv^T.
+ * ctx: [Bc, S_kv, C] f32 host; Wk, Wv: [H*D, C] bf16 bit patterns (the
+ * safetensors [out_features, in_features] layout); k_norm_w: [D] or NULL.
+ * Bc = 1 serves every query batch (both CFG branches share one context);
+ * otherwise Bc must equal the query batch.  Returns NULL on failure. */
+typedef struct anima_hip_ctx_kv anima_hip_ctx_kv;
+
+anima_hip_ctx_kv *anima_hip_ctx_kv_create(const float *ctx, const uint16_t *wk, const uint16_t *wv,
+                                          const float *k_norm_w, int Bc, int S_kv, int C, int H,
+                                          int D, float eps, int mode);
+void anima_hip_ctx_kv_destroy(anima_hip_ctx_kv *kv);
+
+/* Cross-attention of q [B, S_q, H, D] (q_proj output, f32 host) against the
+ * cached context: q = RMSNorm_head(q) (q_norm_w [D] or NULL), no RoPE, no mask,
+ * scale 1/sqrt(D).  out: [B, S_q, H, D] f32 host. */
+bool anima_hip_cross_attention(const float *q, const float *q_norm_w, const anima_hip_ctx_kv *kv,
+                               float *out, int B, int S_q, float eps);
+
+/* Device scratch for anima_hip_cross_attention_dev (bytes). */
+size_t anima_hip_cross_attention_scratch_bytes(const anima_hip_ctx_kv *kv, int B, int S_q);
+
+/* Device-memory form of anima_hip_cross_attention (q, q_norm_w, out on the
+ * device; nothing is allocated). */
+bool anima_hip_cross_attention_dev(const float *q, const float *q_norm_w,
+                                   const anima_hip_ctx_kv *kv, float *out, void *scratch,
+                                   size_t scratch_bytes, int B, int S_q, float eps, void *stream);
 
 #ifdef __cplusplus
 }

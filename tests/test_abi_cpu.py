@@ -36,6 +36,54 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert sorted(_lib.SIGNATURES) == names, "ctypes declarations out of sync with the header"
 
 
+def _prototypes():
+    """name -> (return type, [parameter types]) parsed from the header."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    text = "\n".join(ln for ln in text.splitlines() if not ln.lstrip().startswith("#"))
+    protos = {}
+    for m in re.finditer(r"^([\w ]+?\**)\s*\b(anima_(?:rt|hip)_\w+)\s*\(([^)]*)\)\s*;", text,
+                         flags=re.M):
+        ret, name, params = m.group(1).strip(), m.group(2), m.group(3).strip()
+        plist = [] if params in ("", "void") else [p.strip() for p in params.split(",")]
+        types = []
+        for prm in plist:
+            prm = re.sub(r"\b\w+$", "", prm).strip() if not prm.endswith("*") else prm
+            types.append(" ".join(prm.split()))
+        protos[name] = (" ".join(ret.split()), types)
+    return protos
+
+
+def _ctype_of(c):
+    import ctypes as ct
+    c = c.replace("const ", "").strip()
+    if c.endswith("*"):
+        return "int64*" if c.startswith("int64_t") else "ptr"
+    return {"bool": ct.c_bool, "int": ct.c_int, "float": ct.c_float, "size_t": ct.c_size_t,
+            "int64_t": ct.c_int64, "void": None}[c]
+
+
+def test_ctypes_declarations_match_header_prototypes():
+    import ctypes as ct
+    protos = _prototypes()
+    assert set(protos) == set(_lib.SIGNATURES)
+    for name, (ret, params) in protos.items():
+        res, args = _lib.SIGNATURES[name]
+        assert len(args) == len(params), f"{name}: {len(args)} ctypes args, header has {len(params)}"
+        for i, (c, py) in enumerate(zip(params, args)):
+            want = _ctype_of(c)
+            if want == "ptr":
+                assert py is ct.c_void_p, f"{name} arg {i}: {c}"
+            elif want == "int64*":
+                assert py is ct.POINTER(ct.c_int64), f"{name} arg {i}: {c}"
+            else:
+                assert py is want, f"{name} arg {i}: {c} vs {py}"
+        rwant = _ctype_of(ret)
+        if rwant == "ptr":
+            assert res in (ct.c_void_p, ct.c_char_p), name
+        else:
+            assert res is rwant, f"{name} return {ret} vs {res}"
+
+
 def test_reference_drop_in_signatures():
     # The ctypes argtypes the reference's binding uses (anima_rt_ops.py:28-34).
     import ctypes as ct

@@ -1,0 +1,140 @@
+"""Cross-attention with the cached text-context K/V, the projection GEMM, and
+the rectangular high-resolution configuration, against the oracle.
+
+Tolerances: max-abs 1e-4 for the f32 path; normwise relative 2e-2
+(max|out-ref| <= 2e-2 max|ref|) for the bf16-input path.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from anima_hip import AnimaHipError, rt
+from anima_hip.rope import generate_rope_freqs
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+REL = 2e-2
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "anima_rt_ref_vectors.npz")
+
+
+def randn(rng, *shape, sigma=1.0):
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(sigma)).astype(np.float32)
+
+
+def rel_err(out, ref):
+    return float(np.abs(out - ref).max() / np.abs(ref).max())
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    rt.init()
+
+
+def test_gemm_bf16_golden_and_shapes():
+    g = np.load(GOLDEN)
+    c = rt.gemm_bf16(g["gemm_a"], g["gemm_w_bf16"])
+    assert np.abs(c - g["gemm_out"]).max() <= 1e-5 * max(1.0, np.abs(g["gemm_out"]).max())
+    rng = np.random.default_rng(4)
+    for M, N, K in [(37, 130, 77), (1, 1, 1), (300, 257, 1024), (5, 9, 0)]:
+        a = randn(rng, M, K)
+        w = oracle.f32_to_bf16_bits(randn(rng, N, K, sigma=0.02))
+        ref = oracle.gemm_bf16(a, w) if K else np.zeros((M, N), np.float32)
+        out = rt.gemm_bf16(a, w)
+        assert np.abs(out - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max()), (M, N, K)
+    a, b = randn(rng, 64, 96), randn(rng, 40, 96)
+    np.testing.assert_allclose(rt.gemm_fp32(a, b), a.astype(np.float64) @ b.T.astype(np.float64),
+                               atol=2e-5)
+
+
+def _config2(seed=2002, Bc=1):
+    """B=2 CFG, Sq=256 latent tokens, Sk=512 context tokens, 16 heads x 128.
+    x ~ N(0,1) [2,256,2048]; ctx ~ N(0,0.5) [Bc,512,1024]; Wq/Wk/Wv bf16 ~ N(0,0.02)."""
+    rng = np.random.default_rng(seed)
+    x = randn(rng, 2, 256, 2048)
+    ctx = randn(rng, Bc, 512, 1024, sigma=0.5)
+    wq = oracle.f32_to_bf16_bits(randn(rng, 2048, 2048, sigma=0.02))
+    wk = oracle.f32_to_bf16_bits(randn(rng, 2048, 1024, sigma=0.02))
+    wv = oracle.f32_to_bf16_bits(randn(rng, 2048, 1024, sigma=0.02))
+    return x, ctx, wq, wk, wv
+
+
+@pytest.mark.parametrize("Bc", [1, 2])
+def test_config2_cross_attention_cached_kv(Bc):
+    x, ctx, wq, wk, wv = _config2(Bc=Bc)
+    ones = np.ones(128, np.float32)
+    # Oracle: projections with anima_rt's bf16 GEMM, then NumpyAttention's
+    # norm -> SDPA dataflow (no RoPE for cross-attention).
+    q_ref = oracle.gemm_bf16(x.reshape(-1, 2048), wq).reshape(2, 256, 16, 128)
+    k_ref = np.stack([oracle.gemm_bf16(ctx[b], wk) for b in range(Bc)]).reshape(Bc, 512, 16, 128)
+    v_ref = np.stack([oracle.gemm_bf16(ctx[b], wv) for b in range(Bc)]).reshape(Bc, 512, 16, 128)
+    kb = np.broadcast_to(k_ref, (2, 512, 16, 128))
+    vb = np.broadcast_to(v_ref, (2, 512, 16, 128))
+    ref = oracle.attention_dataflow(q_ref, kb, vb, ones, ones, None,
+                                    sdpa=lambda a, b, c: oracle.flash_sdpa(a, b, c, threads=8))
+
+    q = rt.gemm_bf16(x.reshape(-1, 2048), wq).reshape(2, 256, 16, 128)
+    assert np.abs(q - q_ref).max() <= 1e-4
+    cache = rt.ContextKV(ctx, wk, wv, ones, heads=16, head_dim=128)
+    try:
+        out = cache.attend(q, ones)
+        err = float(np.abs(out - ref).max())
+        print(f"config2 Bc={Bc} f32 max_abs={err:.3e}", flush=True)
+        assert err <= TOL
+        # The cache is reused: a second call (next denoise step) is identical.
+        np.testing.assert_array_equal(cache.attend(q, ones), out)
+    finally:
+        cache.close()
+
+    cache = rt.ContextKV(ctx, wk, wv, ones, heads=16, head_dim=128, mode=rt.BF16)
+    try:
+        out = cache.attend(q, ones)
+        err = rel_err(out, ref)
+        print(f"config2 Bc={Bc} bf16 rel={err:.3e}", flush=True)
+        assert err <= REL
+    finally:
+        cache.close()
+
+
+def test_cross_attention_errors():
+    rng = np.random.default_rng(1)
+    ctx = randn(rng, 3, 16, 32)
+    w = oracle.f32_to_bf16_bits(randn(rng, 2 * 64, 32, sigma=0.02))
+    cache = rt.ContextKV(ctx, w, w, None, heads=2, head_dim=64)
+    try:
+        with pytest.raises(AnimaHipError, match="batch"):
+            cache.attend(randn(rng, 2, 8, 2, 64))  # Bc=3 cannot serve B=2
+        out = cache.attend(randn(rng, 3, 8, 2, 64))  # generic head dim path
+        assert np.isfinite(out).all()
+    finally:
+        cache.close()
+    with pytest.raises(AnimaHipError, match="D == 128"):
+        rt.ContextKV(ctx, w, w, None, heads=2, head_dim=64, mode=rt.BF16)
+
+
+def test_config5_rectangular_6144_sampled_heads():
+    """B=2, H=16, S=6144 (96x64 grid, rectangular RoPE) self-attention and
+    cross-attention 6144x512; two (batch, head) slices of each vs the oracle."""
+    rng = np.random.default_rng(5005)
+    B, S, H, D = 2, 6144, 16, 128
+    q, k, v = randn(rng, B, S, H, D), randn(rng, B, S, H, D), randn(rng, B, S, H, D)
+    f = generate_rope_freqs(96, 64)
+    ones = np.ones(D, np.float32)
+    for mode, check in [(rt.F32, lambda o, r: float(np.abs(o - r).max()) <= TOL),
+                        (rt.BF16, lambda o, r: rel_err(o, r) <= REL)]:
+        out = rt.attention(q, k, v, ones, ones, f, mode=mode)
+        for b, h in [(0, 7), (1, 2)]:
+            ref = oracle.attention_dataflow(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, h:h + 1],
+                                            v[b:b + 1, :, h:h + 1], ones, ones, f)
+            print(f"config5 self mode={mode} b={b} h={h} "
+                  f"max_abs={np.abs(out[b, :, h] - ref[0, :, 0]).max():.3e}", flush=True)
+            assert check(out[b, :, h], ref[0, :, 0])
+    # cross 6144 x 512 (no RoPE), K/V [B, 512, H, D]
+    kc, vc = randn(rng, B, 512, H, D), randn(rng, B, 512, H, D)
+    out = rt.attention(q, kc, vc, ones, ones, None)
+    for b, h in [(0, 9), (1, 0)]:
+        ref = oracle.attention_dataflow(q[b:b + 1, :, h:h + 1], kc[b:b + 1, :, h:h + 1],
+                                        vc[b:b + 1, :, h:h + 1], ones, ones, None)
+        assert float(np.abs(out[b, :, h] - ref[0, :, 0]).max()) <= TOL
