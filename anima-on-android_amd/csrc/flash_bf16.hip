@@ -15,8 +15,14 @@
 //   * K tiles [64 keys][128 d] and V^T tiles [128 d][64 keys] are staged
 //     through LDS, double-buffered, one barrier per tile; row pitches are
 //     padded by 16 bytes so the per-lane 16-byte reads are conflict-free;
+//   * software-pipelined per wave: the MFMAs computing the scores of tile
+//     j+1 are interleaved (sched_group_barrier) with the VALU softmax of
+//     tile j, then P.V of tile j follows, so the MFMA pipe and the VALU
+//     overlap inside every wave;
 //   * the softmax scale is folded into the exponent: p = exp2(s*c - m) with
-//     c = scale*log2(e) > 0, so the tile max is taken on raw scores.
+//     c = scale*log2(e) > 0, so the tile max is taken on raw scores; the
+//     running max m is updated lazily (only when a tile max exceeds it by
+//     more than 8 in log2 units), so the O rescale is usually skipped.
 // Also here: the V -> packed V^T conversion kernel of this path.
 #include "common.h"
 
@@ -37,6 +43,8 @@ constexpr int kBN = 64;          // keys per tile (== kVtTile)
 constexpr int kKPitch = kD + 8;  // bf16 per LDS K row (272 bytes)
 constexpr int kVPitch = kBN + 8; // bf16 per LDS V^T row (144 bytes)
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15)
+constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold: p <= 2^8
 static_assert(kBN == kVtTile, "V^T padding must match the key tile");
 
 struct Bf16Args {
@@ -51,6 +59,16 @@ struct Bf16Args {
 __device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c)
 {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Max of v over the two lanes l and l^32 (the two halves of a query row) with
+// one v_permlane32_swap: r[0] holds the low half in both halves, r[1] the
+// high half.
+__device__ __forceinline__ float row_pair_max(float v)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
@@ -109,14 +127,22 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
         for (int t = 0; t < 8; ++t)
             qf[t] = bf16x8{};
     }
+    // Retire the Q loads here.  Otherwise the compiler still counts them as
+    // outstanding inside the tile loop and waits for vmcnt(0) before the
+    // first MFMAs, which also waits for the next tile's prefetch.
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
 
     int kv_end = a.S_kv;
     if (a.causal)
         kv_end = min(kv_end, min(a.S_q, q_tile0 + BM));
     const int ntiles = (kv_end + kBN - 1) / kBN;
 
+    // K is fetched two tiles ahead and V one tile ahead: iteration j reads
+    // K(j+1) (scores of the next tile) and V(j) (P.V of this tile) while
+    // K(j+2) and V(j+1) travel from HBM through registers into the buffers
+    // that K(j) and V(j-1) used.  One barrier per tile keeps this safe.
     f32x4 kst[LK], vst[LV];
-    auto gload = [&](int key0) {
+    auto gload_k = [&](int key0) {
 #pragma unroll
         for (int i = 0; i < LK; ++i) {
             const int f = tid + i * NT;
@@ -125,6 +151,8 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
             kst[i] = key < a.S_kv ? *reinterpret_cast<const f32x4 *>(kp + key * a.ks + 8 * c)
                                   : f32x4{0.f, 0.f, 0.f, 0.f};
         }
+    };
+    auto gload_v = [&](int key0) {
 #pragma unroll
         for (int i = 0; i < LV; ++i) {
             const int f = tid + i * NT;
@@ -132,13 +160,15 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
             vst[i] = *reinterpret_cast<const f32x4 *>(vp + d * a.vd + key0 + 8 * c);
         }
     };
-    auto lstore = [&](int buf) {
+    auto lstore_k = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < LK; ++i) {
             const int f = tid + i * NT;
             const int r = f >> 4, c = f & 15;
             *reinterpret_cast<f32x4 *>(&Ks[buf][r * kKPitch + 8 * c]) = kst[i];
         }
+    };
+    auto lstore_v = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < LV; ++i) {
             const int f = tid + i * NT;
@@ -146,26 +176,13 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
             *reinterpret_cast<f32x4 *>(&Vs[buf][d * kVPitch + 8 * c]) = vst[i];
         }
     };
-
-    f32x16 o0 = {}, o1 = {}, o2 = {}, o3 = {};
-    float m = -INFINITY;
-    float l = 0.0f;
-
-    if (ntiles > 0) {
-        gload(0);
-        lstore(0);
-    }
-    __syncthreads();
-
-    for (int j = 0; j < ntiles; ++j) {
-        const int buf = j & 1;
-        const bool more = j + 1 < ntiles;
-        if (more)
-            gload((j + 1) * kBN);
-
-        f32x16 s0 = {}, s1 = {};
+    // S^T of one 64-key tile from the K buffer `buf`: keys [0,32) in s0,
+    // [32,64) in s1.
+    auto scores = [&](int buf, f32x16 &s0, f32x16 &s1) {
         const u16 *kr0 = &Ks[buf][col * kKPitch + 64 * half];
         const u16 *kr1 = kr0 + 32 * kKPitch;
+        s0 = f32x16{};
+        s1 = f32x16{};
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const bf16x8 k0 = *reinterpret_cast<const bf16x8 *>(kr0 + 8 * t);
@@ -173,45 +190,125 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
             s0 = mfma_bf16(k0, qf[t], s0);
             s1 = mfma_bf16(k1, qf[t], s1);
         }
+    };
 
+    f32x16 o0 = {}, o1 = {}, o2 = {}, o3 = {};
+    float m = -INFINITY;
+    float l = 0.0f;
+    f32x16 sc0 = {}, sc1 = {};  // scores of the tile being consumed
+
+    if (ntiles > 0) {
+        gload_k(0);
+        gload_v(0);
+        lstore_k(0);
+        lstore_v(0);
+        if (ntiles > 1) {
+            gload_k(kBN);
+            lstore_k(1);
+        }
+    }
+    __syncthreads();
+    if (ntiles > 0)
+        scores(0, sc0, sc1);
+    __syncthreads();  // K buffer 0 is rewritten in the first iteration
+
+    // Raw-score tile max over a lane's 32 scores, combined across the two
+    // lanes of the row (c > 0, so the max commutes with the scaling).
+    auto tile_max = [&](const f32x16 &s0, const f32x16 &s1) {
+        float a0 = -INFINITY, a1 = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+            a0 = fmaxf(a0, fmaxf(s0[r], s0[r + 1]));
+            a1 = fmaxf(a1, fmaxf(s1[r], s1[r + 1]));
+        }
+        return row_pair_max(fmaxf(a0, a1));
+    };
+    // Max of the unmasked scores of the tile consumed next; the pipelined
+    // section computes it for tile j+1 while the P.V MFMAs of tile j run.
+    float mx_next = ntiles > 0 ? tile_max(sc0, sc1) : -INFINITY;
+
+    for (int j = 0; j < ntiles; ++j) {
+        const int buf = j & 1;
+        const bool has1 = j + 1 < ntiles, has2 = j + 2 < ntiles;
+        if (has2)
+            gload_k((j + 2) * kBN);
+        if (has1)
+            gload_v((j + 1) * kBN);
+
+        float mx = mx_next;
         const int key0 = j * kBN;
         if ((key0 + kBN > a.S_kv) || a.causal) {
+            // Tail tile or causal: mask, then take the max again.
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int k0i = key0 + acc_row(r, half);
                 const int k1i = k0i + 32;
                 if (k0i >= a.S_kv || (a.causal && k0i > qrow))
-                    s0[r] = -INFINITY;
+                    sc0[r] = -INFINITY;
                 if (k1i >= a.S_kv || (a.causal && k1i > qrow))
-                    s1[r] = -INFINITY;
+                    sc1[r] = -INFINITY;
             }
+            mx = tile_max(sc0, sc1);
         }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-            mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m, mx * a.c);
-        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-        m = m_new;
 
-        float psum = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            s0[r] = __builtin_amdgcn_exp2f(fmaf(s0[r], a.c, -m_use));
-            s1[r] = __builtin_amdgcn_exp2f(fmaf(s1[r], a.c, -m_use));
-            psum += s0[r] + s1[r];
+        // Lazy rescale: the reference max m (log2 domain) moves only when some
+        // row of the wave sees a tile max above m + kRescaleLog2, and then for
+        // the whole wave at once; otherwise exp2 values stay <= 2^kRescaleLog2
+        // and O, l keep accumulating against the same m (exact, since the
+        // final O / l shares it).  The rare rescale happens here, before the
+        // branch-free pipelined section below.
+        const float cand = mx * a.c;
+        if (__any(cand > m + kRescaleLog2)) {
+            const float m_new = fmaxf(m, cand);
+            const float alpha =
+                m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+            m = m_new;
+            l *= alpha;
+            o0 *= alpha;
+            o1 *= alpha;
+            o2 *= alpha;
+            o3 *= alpha;
         }
-        l = l * alpha + psum;
-        o0 *= alpha;
-        o1 *= alpha;
-        o2 *= alpha;
-        o3 *= alpha;
+        const float neg_m = (m == -INFINITY) ? 0.0f : -m;
 
-        const bf16x8 p00 = pack8(s0, 0), p01 = pack8(s0, 8);
-        const bf16x8 p10 = pack8(s1, 0), p11 = pack8(s1, 8);
+        // ---- Pipelined section, one basic block, hand-interleaved: each step
+        // issues the K reads of the next step, one score MFMA of tile j+1, two
+        // exponentials of tile j, the other score MFMA and two more
+        // exponentials.  sched_barrier keeps the steps in this order so the
+        // MFMA pipe and the VALU work side by side.  (On the last tile the next
+        // K buffer holds stale data; those scores are never used.)
+        const u16 *kr0 = &Ks[buf ^ 1][col * kKPitch + 64 * half];
+        const u16 *kr1 = kr0 + 32 * kKPitch;
+        f32x16 sn0 = {}, sn1 = {};
+        float ps0 = 0.0f, ps1 = 0.0f;
+        bf16x8 k0 = *reinterpret_cast<const bf16x8 *>(kr0);
+        bf16x8 k1 = *reinterpret_cast<const bf16x8 *>(kr1);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            bf16x8 k0n = k0, k1n = k1;
+            if (t < 7) {
+                k0n = *reinterpret_cast<const bf16x8 *>(kr0 + 8 * (t + 1));
+                k1n = *reinterpret_cast<const bf16x8 *>(kr1 + 8 * (t + 1));
+            }
+            sn0 = mfma_bf16(k0, qf[t], sn0);
+            sc0[2 * t] = __builtin_amdgcn_exp2f(fmaf(sc0[2 * t], a.c, neg_m));
+            sc0[2 * t + 1] = __builtin_amdgcn_exp2f(fmaf(sc0[2 * t + 1], a.c, neg_m));
+            ps0 += sc0[2 * t] + sc0[2 * t + 1];
+            sn1 = mfma_bf16(k1, qf[t], sn1);
+            sc1[2 * t] = __builtin_amdgcn_exp2f(fmaf(sc1[2 * t], a.c, neg_m));
+            sc1[2 * t + 1] = __builtin_amdgcn_exp2f(fmaf(sc1[2 * t + 1], a.c, neg_m));
+            ps1 += sc1[2 * t] + sc1[2 * t + 1];
+            __builtin_amdgcn_sched_barrier(0);
+            k0 = k0n;
+            k1 = k1n;
+        }
+        l += ps0 + ps1;
+        const bf16x8 p00 = pack8(sc0, 0), p01 = pack8(sc0, 8);
+        const bf16x8 p10 = pack8(sc1, 0), p11 = pack8(sc1, 8);
+
+        // P.V of tile j; meanwhile the VALU takes the max of tile j+1.
         const u16 *vr = &Vs[buf][col * kVPitch + 8 * half];
+        float a0 = -INFINITY, a1 = -INFINITY;
 #pragma unroll
         for (int blk = 0; blk < 4; ++blk) {
             const u16 *vrow = vr + 32 * blk * kVPitch;
@@ -221,14 +318,24 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
             const bf16x8 v11 = *reinterpret_cast<const bf16x8 *>(vrow + 48);
             f32x16 &ob = blk == 0 ? o0 : blk == 1 ? o1 : blk == 2 ? o2 : o3;
             ob = mfma_bf16(v00, p00, ob);
+            a0 = fmaxf(a0, fmaxf(sn0[4 * blk], sn0[4 * blk + 1]));
             ob = mfma_bf16(v01, p01, ob);
+            a0 = fmaxf(a0, fmaxf(sn0[4 * blk + 2], sn0[4 * blk + 3]));
             ob = mfma_bf16(v10, p10, ob);
+            a1 = fmaxf(a1, fmaxf(sn1[4 * blk], sn1[4 * blk + 1]));
             ob = mfma_bf16(v11, p11, ob);
+            a1 = fmaxf(a1, fmaxf(sn1[4 * blk + 2], sn1[4 * blk + 3]));
+            __builtin_amdgcn_sched_barrier(0);
         }
+        mx_next = row_pair_max(fmaxf(a0, a1));
 
-        if (more)
-            lstore(buf ^ 1);
+        if (has2)
+            lstore_k(buf);
+        if (has1)
+            lstore_v(buf ^ 1);
         __syncthreads();
+        sc0 = sn0;
+        sc1 = sn1;
     }
 
     l += __shfl_xor(l, 32);

@@ -36,6 +36,7 @@ constexpr int kBN = 64;          // keys per K/V tile
 constexpr int kKStride = kD + 4; // LDS row pitch of K (floats): 16-byte skew per row
 constexpr int kVStride = kD;     // LDS row pitch of V: rows are read whole
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15)
 
 struct F32Args {
     const float *q, *k, *v;
@@ -52,6 +53,16 @@ __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c)
 }
 
 // Row index inside a 32x32 MFMA accumulator: register r of lane half h.
+// Max of v over the two lanes l and l^32 (the two halves of a query row) with
+// one v_permlane32_swap: r[0] holds the low half in both halves, r[1] the
+// high half.
+__device__ __forceinline__ float row_pair_max(float v)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ int acc_row(int r, int h)
 {
     return 8 * (r >> 2) + 4 * h + (r & 3);
@@ -103,6 +114,10 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_f32_d128(F32Args a)
         for (int i = 0; i < 64; ++i)
             qf[i] = 0.0f;
     }
+    // Retire the Q loads here.  Otherwise the compiler still counts them as
+    // outstanding inside the tile loop and waits for vmcnt(0) before the
+    // first MFMAs, which also waits for the next tile's prefetch.
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
 
     int kv_end = a.S_kv;
     if (a.causal) {
@@ -192,7 +207,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_f32_d128(F32Args a)
             s1[r] = x1;
             mx = fmaxf(mx, fmaxf(x0, x1));
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = row_pair_max(mx);
         const float m_new = fmaxf(m, mx);
         const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m - m_use);
