@@ -155,6 +155,9 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
     if (!h2d(r.q.p, Q, f32_bytes(nq), st) || !h2d(r.k.p, K, f32_bytes(nk), st) ||
         !h2d(r.v.p, V, f32_bytes(nk), st))
         return false;
+    const size_t part_bytes = flash_plan(BH, S_q, S_kv, D).bytes;
+    if (!r.scratch.reserve(part_bytes, "workspace split-KV partials"))
+        return false;
     FlashProblem p;
     p.q = r.q.p;
     p.k = r.k.p;
@@ -202,9 +205,9 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
         p.k = r.k2.p;
         p.v = r.v2.p;
         p.vs = vts;
-        if (!launch_flash_bf16(p, st))
+        if (!launch_flash_bf16(p, st, r.scratch.p, part_bytes))
             return false;
-    } else if (!launch_flash_f32(p, st)) {
+    } else if (!launch_flash_f32(p, st, r.scratch.p, part_bytes)) {
         return false;
     }
     if (!d2h(out, r.o.p, f32_bytes(nq), st))

@@ -44,7 +44,7 @@ size_t attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D, b
         if (bf16)
             n += round_up(prepared_v_bytes(Bk, S_kv, H, D, true));
     }
-    return n;
+    return n + round_up(flash_plan(int64_t(B) * H, S_q, S_kv, D).bytes);
 }
 
 bool prepare_kv(const float *k, const float *v, const float *k_norm_w, const float *freqs,
@@ -105,7 +105,12 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
             return false;
         kp = kn;
         vp = in.bf16 ? vt : static_cast<const void *>(in.v);
+        if (in.bf16)
+            cur += round_up(prepared_v_bytes(in.Bk, S_kv, H, D, true));
     }
+    // Split-KV partials (small problems only).
+    void *part = cur;
+    const size_t part_bytes = flash_plan(int64_t(B) * H, S_q, S_kv, D).bytes;
 
     RowProblem pq;
     pq.x = in.q;
@@ -144,7 +149,8 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     p.D = D;
     p.scale = float(1.0 / std::sqrt(double(D)));
     p.causal = false;
-    return in.bf16 ? launch_flash_bf16(p, st) : launch_flash_f32(p, st);
+    return in.bf16 ? launch_flash_bf16(p, st, part, part_bytes)
+                   : launch_flash_f32(p, st, part, part_bytes);
 }
 
 }  // namespace anima_hip

@@ -31,8 +31,43 @@ struct FlashProblem {
     bool causal;       // mask key j > query i (top-left aligned, like anima_rt)
 };
 
+// Launch shape of the D == 128 flash kernels.  A grid of B*H*ceil(S_q/256)
+// workgroups of 8 waves fills the GPU when it has at least one workgroup per
+// CU.  Smaller problems (short sequences, few heads) use workgroups of 4
+// waves and, when the caller provides scratch, split the key range over
+// `splits` workgroups per query tile ("split-KV"): split s takes key tiles
+// [s*tiles, (s+1)*tiles) (64 keys each) and writes its output normalised by
+// its own row sum, plus that row's (max, sum), to scratch; flash_combine
+// merges the splits into O.
+struct FlashPlan {
+    int waves = 8;
+    int splits = 1;
+    int tiles = 1 << 30;  // key tiles per split
+    size_t bytes = 0;     // scratch for the partials (0 when unsplit)
+};
+FlashPlan flash_plan(int64_t BH, int S_q, int S_kv, int D);
+
+// What a split workgroup writes (device view).  Partials are laid out
+// [splits][BH][S_q][128] f32 and (max, sum) pairs [splits][BH][S_q] float2,
+// the max in log2 units of the scaled scores.
+struct FlashSplitArgs {
+    int n = 1;
+    int tiles = 1 << 30;
+    int64_t BH = 0;
+    float *part = nullptr;
+    float2 *ml = nullptr;
+};
+// Split descriptor for plan `pl` over scratch `part` (nullptr or too small:
+// unsplit).
+FlashSplitArgs flash_split_args(const FlashPlan &pl, int64_t BH, int S_q, void *part,
+                                size_t part_bytes);
+// O[b,h,q,:] = sum_s w_s P_s[bh,q,:] / sum_s w_s, w_s = l_s * 2^(m_s - max_s m_s).
+bool launch_flash_combine(const FlashProblem &p, const FlashSplitArgs &sa, hipStream_t st);
+
 // f32 inputs, f32 MFMA (D == 128) or the generic kernel (any D <= 1024).
-bool launch_flash_f32(const FlashProblem &p, hipStream_t st);
+// `part` is optional split-KV scratch of flash_plan(...).bytes.
+bool launch_flash_f32(const FlashProblem &p, hipStream_t st, void *part = nullptr,
+                      size_t part_bytes = 0);
 // True when launch_flash_f32 would take the MFMA path for this problem.
 bool flash_f32_fast_path(const FlashProblem &p);
 
@@ -40,7 +75,8 @@ bool flash_f32_fast_path(const FlashProblem &p);
 // bf16 MFMA with f32 accumulation and f32 softmax; D == 128 and scale > 0.
 // `v` points at the packed V^T and `vs` holds its {batch, head, d-row}
 // strides (the d-row stride is vt_padded_len(S_kv)).
-bool launch_flash_bf16(const FlashProblem &p, hipStream_t st);
+bool launch_flash_bf16(const FlashProblem &p, hipStream_t st, void *part = nullptr,
+                       size_t part_bytes = 0);
 
 // V^T layout of the bf16 path: per (batch, head) a [D][Sp] bf16 matrix with
 // Sp = vt_padded_len(S_kv), zero beyond S_kv, and within every group of 16

@@ -54,6 +54,7 @@ struct Bf16Args {
     int H, S_q, S_kv, n_qtiles;
     float c;  // scale * log2(e), > 0
     int causal;
+    FlashSplitArgs split;  // n == 1: write O; n > 1: write this split's partial
 };
 
 __device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c)
@@ -104,8 +105,9 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     const int col = lane & 31;
     const int half = lane >> 5;
 
-    const int qt = blockIdx.x % a.n_qtiles;
-    const int bh = blockIdx.x / a.n_qtiles;
+    const int sp = blockIdx.x % a.split.n;
+    const int qt = (blockIdx.x / a.split.n) % a.n_qtiles;
+    const int bh = (blockIdx.x / a.split.n) / a.n_qtiles;
     const int b = bh / a.H;
     const int h = bh - b * a.H;
     const int q_tile0 = qt * BM;
@@ -135,7 +137,9 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     int kv_end = a.S_kv;
     if (a.causal)
         kv_end = min(kv_end, min(a.S_q, q_tile0 + BM));
-    const int ntiles = (kv_end + kBN - 1) / kBN;
+    // Key tiles [j0, j0 + ntiles) of this split (all of them when unsplit).
+    const int j0 = sp * a.split.tiles;
+    const int ntiles = max(0, min((kv_end + kBN - 1) / kBN - j0, a.split.tiles));
 
     // K is fetched two tiles ahead and V one tile ahead: iteration j reads
     // K(j+1) (scores of the next tile) and V(j) (P.V of this tile) while
@@ -198,12 +202,12 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     f32x16 sc0 = {}, sc1 = {};  // scores of the tile being consumed
 
     if (ntiles > 0) {
-        gload_k(0);
-        gload_v(0);
+        gload_k(j0 * kBN);
+        gload_v(j0 * kBN);
         lstore_k(0);
         lstore_v(0);
         if (ntiles > 1) {
-            gload_k(kBN);
+            gload_k((j0 + 1) * kBN);
             lstore_k(1);
         }
     }
@@ -231,12 +235,12 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
         const int buf = j & 1;
         const bool has1 = j + 1 < ntiles, has2 = j + 2 < ntiles;
         if (has2)
-            gload_k((j + 2) * kBN);
+            gload_k((j0 + j + 2) * kBN);
         if (has1)
-            gload_v((j + 1) * kBN);
+            gload_v((j0 + j + 1) * kBN);
 
         float mx = mx_next;
-        const int key0 = j * kBN;
+        const int key0 = (j0 + j) * kBN;
         if ((key0 + kBN > a.S_kv) || a.causal) {
             // Tail tile or causal: mask, then take the max again.
 #pragma unroll
@@ -342,6 +346,12 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     if (qrow < a.S_q) {
         float *op = a.o + b * a.ob + h * a.oh + qrow * a.os;
+        if (a.split.n > 1) {
+            const int64_t prow = (int64_t(sp) * a.split.BH + bh) * a.S_q + qrow;
+            op = a.split.part + prow * kD;
+            if (half == 0)
+                a.split.ml[prow] = make_float2(m, l);
+        }
 #pragma unroll
         for (int blk = 0; blk < 4; ++blk) {
             const f32x16 &ob = blk == 0 ? o0 : blk == 1 ? o1 : blk == 2 ? o2 : o3;
@@ -409,11 +419,22 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(PackArgs a)
 
 bool aligned(const void *ptr, unsigned m) { return (reinterpret_cast<uintptr_t>(ptr) & (m - 1)) == 0; }
 
-constexpr int kWaves = 8;
+template <int NW>
+bool launch_d128(const Bf16Args &a, int64_t BH, hipStream_t st)
+{
+    constexpr int BM = NW * 32;
+    Bf16Args g = a;
+    g.n_qtiles = (g.S_q + BM - 1) / BM;
+    const int64_t nblk = BH * g.n_qtiles * g.split.n;
+    if (nblk > INT32_MAX)
+        return fail("flash_bf16: problem too large for one launch");
+    hipLaunchKernelGGL(flash_bf16_d128<NW>, dim3(unsigned(nblk)), dim3(NW * 64), 0, st, g);
+    return hip_ok(hipGetLastError(), "flash_bf16_d128 launch");
+}
 
 }  // namespace
 
-bool launch_flash_bf16(const FlashProblem &p, hipStream_t st)
+bool launch_flash_bf16(const FlashProblem &p, hipStream_t st, void *part, size_t part_bytes)
 {
     const int64_t BH = int64_t(p.B) * p.H;
     if (BH == 0 || p.S_q == 0)
@@ -441,15 +462,13 @@ bool launch_flash_bf16(const FlashProblem &p, hipStream_t st)
     a.H = p.H;
     a.S_q = p.S_q;
     a.S_kv = p.S_kv;
-    constexpr int BM = kWaves * 32;
-    a.n_qtiles = (p.S_q + BM - 1) / BM;
     a.c = p.scale * kLog2e;
     a.causal = p.causal ? 1 : 0;
-    const int64_t nblk = BH * a.n_qtiles;
-    if (nblk > INT32_MAX)
-        return fail("flash_bf16: problem too large for one launch");
-    hipLaunchKernelGGL(flash_bf16_d128<kWaves>, dim3(unsigned(nblk)), dim3(kWaves * 64), 0, st, a);
-    return hip_ok(hipGetLastError(), "flash_bf16_d128 launch");
+    const FlashPlan pl = flash_plan(BH, p.S_q, p.S_kv, p.D);
+    a.split = flash_split_args(pl, BH, p.S_q, part, part_bytes);
+    if (!(pl.waves == 4 ? launch_d128<4>(a, BH, st) : launch_d128<8>(a, BH, st)))
+        return false;
+    return a.split.n == 1 || launch_flash_combine(p, a.split, st);
 }
 
 bool launch_vt_pack(const float *v, Strides vs, uint16_t *vt, Strides vts, int B, int H,

@@ -45,6 +45,7 @@ struct F32Args {
     int H, S_q, S_kv, n_qtiles;
     float c;     // scale * log2(e)
     int causal;
+    FlashSplitArgs split;  // n == 1: write O; n > 1: write this split's partial
 };
 
 __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c)
@@ -86,8 +87,9 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_f32_d128(F32Args a)
     const int col = lane & 31;
     const int half = lane >> 5;
 
-    const int qt = blockIdx.x % a.n_qtiles;
-    const int bh = blockIdx.x / a.n_qtiles;
+    const int sp = blockIdx.x % a.split.n;
+    const int qt = (blockIdx.x / a.split.n) % a.n_qtiles;
+    const int bh = (blockIdx.x / a.split.n) / a.n_qtiles;
     const int b = bh / a.H;
     const int h = bh - b * a.H;
     const int q_tile0 = qt * BM;
@@ -124,7 +126,9 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_f32_d128(F32Args a)
         const int last_row = min(a.S_q, q_tile0 + BM);
         kv_end = min(kv_end, last_row);
     }
-    const int ntiles = (kv_end + kBN - 1) / kBN;
+    // Key tiles [j0, j1) of this split (all of them when unsplit).
+    const int j0 = sp * a.split.tiles;
+    const int j1 = min((kv_end + kBN - 1) / kBN, j0 + a.split.tiles);
 
     // Next-tile staging registers, used for V then for K so only one
     // half-tile is held at a time.
@@ -155,17 +159,17 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_f32_d128(F32Args a)
     float m = -INFINITY;  // running max of scaled logits (log2 domain)
     float l = 0.0f;       // running partial sum of this lane's keys
 
-    if (ntiles > 0) {
-        gload(kp, a.ks, 0);
+    if (j0 < j1) {
+        gload(kp, a.ks, j0 * kBN);
         lstore(Ks[0], kKStride);
-        gload(vp, a.vs, 0);
+        gload(vp, a.vs, j0 * kBN);
         lstore(Vs[0], kVStride);
     }
     __syncthreads();
 
-    for (int j = 0; j < ntiles; ++j) {
-        const int buf = j & 1;
-        const bool more = j + 1 < ntiles;
+    for (int j = j0; j < j1; ++j) {
+        const int buf = (j - j0) & 1;
+        const bool more = j + 1 < j1;
         if (more)
             gload(vp, a.vs, (j + 1) * kBN);
 
@@ -259,6 +263,12 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_f32_d128(F32Args a)
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     if (qrow < a.S_q) {
         float *op = a.o + b * a.ob + h * a.oh + qrow * a.os;
+        if (a.split.n > 1) {
+            const int64_t prow = (int64_t(sp) * a.split.BH + bh) * a.S_q + qrow;
+            op = a.split.part + prow * kD;
+            if (half == 0)
+                a.split.ml[prow] = make_float2(m, l);
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int d0 = 4 * acc_row(r, half);
@@ -358,7 +368,18 @@ void fill_common(T &g, const FlashProblem &p)
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 bool stride4(const Strides &s) { return s.b % 4 == 0 && s.h % 4 == 0 && s.s % 4 == 0; }
 
-constexpr int kWaves = 8;  // waves per workgroup of the MFMA kernel
+template <int NW>
+bool launch_d128(const F32Args &a, int64_t BH, hipStream_t st)
+{
+    constexpr int BM = NW * 32;
+    F32Args g = a;
+    g.n_qtiles = (g.S_q + BM - 1) / BM;
+    const int64_t nblk = BH * g.n_qtiles * g.split.n;
+    if (nblk > INT32_MAX)
+        return fail("flash_f32: problem too large for one launch");
+    hipLaunchKernelGGL(flash_f32_d128<NW>, dim3(unsigned(nblk)), dim3(NW * 64), 0, st, g);
+    return hip_ok(hipGetLastError(), "flash_f32_d128 launch");
+}
 
 }  // namespace
 
@@ -368,7 +389,7 @@ bool flash_f32_fast_path(const FlashProblem &p)
            stride4(p.qs) && stride4(p.ks) && stride4(p.vs) && stride4(p.os);
 }
 
-bool launch_flash_f32(const FlashProblem &p, hipStream_t st)
+bool launch_flash_f32(const FlashProblem &p, hipStream_t st, void *part, size_t part_bytes)
 {
     const int64_t BH = int64_t(p.B) * p.H;
     if (BH == 0 || p.S_q == 0)
@@ -376,14 +397,11 @@ bool launch_flash_f32(const FlashProblem &p, hipStream_t st)
     if (flash_f32_fast_path(p)) {
         F32Args a;
         fill_common(a, p);
-        constexpr int BM = kWaves * 32;
-        a.n_qtiles = (p.S_q + BM - 1) / BM;
-        const int64_t nblk = BH * a.n_qtiles;
-        if (nblk > INT32_MAX)
-            return fail("flash_f32: problem too large for one launch");
-        hipLaunchKernelGGL(flash_f32_d128<kWaves>, dim3(unsigned(nblk)), dim3(kWaves * 64), 0, st,
-                           a);
-        return hip_ok(hipGetLastError(), "flash_f32_d128 launch");
+        const FlashPlan pl = flash_plan(BH, p.S_q, p.S_kv, p.D);
+        a.split = flash_split_args(pl, BH, p.S_q, part, part_bytes);
+        if (!(pl.waves == 4 ? launch_d128<4>(a, BH, st) : launch_d128<8>(a, BH, st)))
+            return false;
+        return a.split.n == 1 || launch_flash_combine(p, a.split, st);
     }
     if (p.D > 1024)
         return fail("flash_f32: head dim " + std::to_string(p.D) + " > 1024 is not supported");
