@@ -247,9 +247,17 @@ bool host_gemm(const float *A, const void *W, bool w_bf16, float *C, int M, int 
         return false;
     if (!h2d(r.q.p, A, f32_bytes(int64_t(M) * K), st) || !h2d(r.k.p, W, wbytes, st))
         return false;
-    if (!launch_gemm(static_cast<const float *>(r.q.p), K, r.k.p, w_bf16, K,
-                     static_cast<float *>(r.o.p), N, M, N, K, st) ||
-        !d2h(C, r.o.p, f32_bytes(int64_t(M) * N), st))
+    // bf16 weights: bf16 MFMA with A as exact hi + lo terms; f32 weights: f32 MFMA.
+    const size_t sb = w_bf16 ? linear_scratch_bytes(M, K, true) : 0;
+    if (!r.scratch.reserve(sb, "workspace linear"))
+        return false;
+    const bool ok =
+        w_bf16 ? launch_linear(static_cast<const float *>(r.q.p), K,
+                               static_cast<const uint16_t *>(r.k.p), K,
+                               static_cast<float *>(r.o.p), N, M, N, K, true, r.scratch.p, sb, st)
+               : launch_gemm(static_cast<const float *>(r.q.p), K, r.k.p, false, K,
+                             static_cast<float *>(r.o.p), N, M, N, K, st);
+    if (!ok || !d2h(C, r.o.p, f32_bytes(int64_t(M) * N), st))
         return false;
     return sync(st);
 }
@@ -530,6 +538,25 @@ bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, 
     return launch_gemm(a, lda, w, w_bf16 != 0, ldw, c, ldc, M, N, K, pick_stream(stream));
 }
 
+size_t anima_hip_linear_scratch_bytes(int M, int K, int mode)
+{
+    return linear_scratch_bytes(M, K, mode != ANIMA_HIP_BF16);
+}
+
+bool anima_hip_linear_dev(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *c,
+                          int64_t ldc, int M, int N, int K, int mode, void *scratch,
+                          size_t scratch_bytes, void *stream)
+{
+    if (!ready_for_device_call())
+        return false;
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16)
+        return fail("linear_dev: unknown mode " + std::to_string(mode));
+    if (int64_t(M) * N > 0 && (!c || (K > 0 && (!a || !w))))
+        return fail("linear_dev: null pointer");
+    return launch_linear(a, lda, w, ldw, c, ldc, M, N, K, mode == ANIMA_HIP_F32, scratch,
+                         scratch_bytes, pick_stream(stream));
+}
+
 size_t anima_hip_attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D,
                                          int mode)
 {
@@ -672,10 +699,16 @@ anima_hip_ctx_kv *anima_hip_ctx_kv_create(const float *ctx, const uint16_t *wk, 
     kv->H = H;
     kv->D = D;
     kv->device = r.device;
-    bool ok = launch_gemm(static_cast<const float *>(r.q.p), C, r.k.p, true, C,
-                          static_cast<float *>(kf.p), N, M, N, C, st) &&
-              launch_gemm(static_cast<const float *>(r.q.p), C, r.v.p, true, C,
-                          static_cast<float *>(vf.p), N, M, N, C, st);
+    // K/V projections of the context on bf16 MFMA: the context enters as
+    // exact hi + lo bf16 terms in f32 mode, rounded to bf16 in bf16 mode.
+    const size_t sb = linear_scratch_bytes(M, C, !bf16);
+    bool ok = r.scratch.reserve(sb, "workspace linear") &&
+              launch_linear(static_cast<const float *>(r.q.p), C,
+                            static_cast<const uint16_t *>(r.k.p), C, static_cast<float *>(kf.p),
+                            N, M, N, C, !bf16, r.scratch.p, sb, st) &&
+              launch_linear(static_cast<const float *>(r.q.p), C,
+                            static_cast<const uint16_t *>(r.v.p), C, static_cast<float *>(vf.p),
+                            N, M, N, C, !bf16, r.scratch.p, sb, st);
     if (ok && bf16) {
         ok = hip_ok(hipMalloc(&kv->k, prepared_k_bytes(Bc, S_kv, H, D, true)), "ctx K cache") &&
              hip_ok(hipMalloc(&kv->v, prepared_v_bytes(Bc, S_kv, H, D, true)), "ctx V cache") &&

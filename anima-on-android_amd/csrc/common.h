@@ -100,6 +100,15 @@ bool launch_vt_pack(const float *v, Strides vs, uint16_t *vt, Strides vts, int B
 bool launch_gemm(const float *a, int64_t lda, const void *w, bool w_bf16, int64_t ldw, float *c,
                  int64_t ldc, int M, int N, int K, hipStream_t st);
 
+// Projection GEMM C[M,N] = A[M,K] . W[N,K]^T, f32 A/C, bf16 W, on bf16 MFMA
+// (linear.hip).  exact: A enters as bf16 hi + lo terms (per-element error
+// <= 2^-16 |a|); otherwise A is rounded to bf16.  Scratch holds the bf16
+// terms: linear_scratch_bytes(M, K, exact) bytes, 16-byte aligned.
+size_t linear_scratch_bytes(int M, int K, bool exact);
+bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *c,
+                   int64_t ldc, int M, int N, int K, bool exact, void *scratch,
+                   size_t scratch_bytes, hipStream_t st);
+
 // Per-row RMSNorm (+ optional RoPE) "prologue".
 //   x:   rows indexed (b, s, h) through `xs` (D contiguous), f32
 //   out: same indexing through `os`, f32 or bf16 (out_bf16)

@@ -1,0 +1,223 @@
+// Projection GEMM of the DiT attention: C[M,N] = A[M,K] . W[N,K]^T with f32
+// activations A, f32 output C and bf16 weights W, on bf16 MFMA.
+//
+// Replaces the reference's projection GEMM (anima_rt/vulkan/gemm_bf16.comp:25-57:
+// f32 A, bf16 W widened to f32, f32 FMA accumulation; CPU form
+// anima_rt/src/gemm_backend.cpp:140-173) as NumpyAttention.forward calls it for
+// q/k/v_proj and output_proj (anima_rt/scripts/numpy_dit.py:273-281, 294-296),
+// and for the text-context k/v_proj that feed the context K/V cache.
+//
+// W is bf16 already, so only A needs a representation the bf16 MFMA accepts.
+// split_kernel writes it as bf16 terms with rows padded to 8 elements:
+//   exact mode  A = hi + lo + r,  hi = bf16(A), lo = bf16(A - hi),
+//               |r| <= 2^-16 |A| per element; C = hi.W^T + lo.W^T
+//               (two products, f32 accumulation);
+//   bf16 mode   hi only (|A - hi| <= 2^-8 |A|).
+// The products are plain bf16 x bf16 -> f32 GEMMs and go to hipBLASLt.  A
+// shape without a hipBLASLt solution falls back to gemm_kernel (f32 MFMA
+// on the exact f32 values).
+#include "common.h"
+
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <memory>
+#include <mutex>
+#include <tuple>
+
+namespace anima_hip {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+size_t round_up256(size_t n) { return (n + 255) / 256 * 256; }
+int64_t padded_k(int K) { return (int64_t(K) + 7) / 8 * 8; }
+
+struct SplitArgs {
+    const float *a;
+    int64_t lda;
+    unsigned int *hi, *lo;  // [M][Kp] bf16, addressed as bf16 pairs
+    int64_t kp;             // padded row length (elements)
+    int M, K, vec;
+    int64_t total;          // M * Kp / 8 chunks
+};
+
+__device__ __forceinline__ unsigned int pack_pair(float x, float y)
+{
+    return __builtin_bit_cast(unsigned int, __builtin_convertvector(f32x2{x, y}, bf16x2));
+}
+
+__device__ __forceinline__ float bf16_lo_value(unsigned int w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi_value(unsigned int w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// One thread per 8 consecutive elements of a row: hi (and lo) as one
+// 16-byte store each; elements k >= K are written as zero.
+__global__ __launch_bounds__(256) void split_kernel(SplitArgs a)
+{
+    const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= a.total)
+        return;
+    const int64_t chunks = a.kp / 8;
+    const int64_t m = idx / chunks;
+    const int k0 = int(idx - m * chunks) * 8;
+    const float *row = a.a + m * a.lda;
+    float x[8];
+    if (a.vec && k0 + 8 <= a.K) {
+        const f32x4 u = *reinterpret_cast<const f32x4 *>(row + k0);
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(row + k0 + 4);
+        x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
+        x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            x[e] = k0 + e < a.K ? row[k0 + e] : 0.0f;
+    }
+    unsigned int h[4], l[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        h[e] = pack_pair(x[2 * e], x[2 * e + 1]);
+        // x - hi is exact in f32 (hi holds the leading bits of x).
+        l[e] = pack_pair(x[2 * e] - bf16_lo_value(h[e]), x[2 * e + 1] - bf16_hi_value(h[e]));
+    }
+    const int64_t off = (m * a.kp + k0) / 2;
+    *reinterpret_cast<uint4 *>(a.hi + off) = uint4{h[0], h[1], h[2], h[3]};
+    if (a.lo)
+        *reinterpret_cast<uint4 *>(a.lo + off) = uint4{l[0], l[1], l[2], l[3]};
+}
+
+// hipBLASLt plans per device and problem shape.  Row-major C[M,N] = A W^T is
+// the column-major product C^T[N,M] = op_T(W_cm[K,N]) . A_cm[K,M].
+struct LtPlan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t lw = nullptr, la = nullptr, lc = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    bool ok = false;
+};
+
+struct LtDevice {
+    hipblasLtHandle_t handle = nullptr;
+    std::map<std::tuple<int, int, int, int64_t, int64_t, int64_t>, std::unique_ptr<LtPlan>> plans;
+};
+
+std::mutex g_lt_mu;
+std::map<int, std::unique_ptr<LtDevice>> g_lt;
+
+LtPlan *lt_plan(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess)
+        return nullptr;
+    auto &slot = g_lt[dev];
+    if (!slot) {
+        slot.reset(new LtDevice);
+        if (hipblasLtCreate(&slot->handle) != HIPBLAS_STATUS_SUCCESS) {
+            slot->handle = nullptr;
+            return nullptr;
+        }
+    }
+    if (!slot->handle)
+        return nullptr;
+    auto &pp = slot->plans[std::make_tuple(M, N, K, lda, ldw, ldc)];
+    if (pp)
+        return pp->ok ? pp.get() : nullptr;
+    pp.reset(new LtPlan);
+    LtPlan &p = *pp;
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    uint64_t ws = 0;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int n = 0;
+    const bool built =
+        hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) ==
+            HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) ==
+            HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatrixLayoutCreate(&p.lw, HIP_R_16BF, K, N, ldw) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, M, lda) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                              sizeof(ws)) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulAlgoGetHeuristic(slot->handle, p.desc, p.lw, p.la, p.lc, p.lc, pref, 1, res,
+                                        &n) == HIPBLAS_STATUS_SUCCESS &&
+        n > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS;
+    if (pref)
+        hipblasLtMatmulPreferenceDestroy(pref);
+    if (built) {
+        p.algo = res[0].algo;
+        p.ok = true;
+    }
+    return p.ok ? &p : nullptr;
+}
+
+bool lt_matmul(LtPlan *p, const void *w, const void *a, float *c, float beta, hipStream_t st)
+{
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const float alpha = 1.0f;
+    const hipblasStatus_t s = hipblasLtMatmul(g_lt[dev]->handle, p->desc, &alpha, w, p->lw, a, p->la,
+                                              &beta, c, p->lc, c, p->lc, &p->algo, nullptr, 0, st);
+    if (s != HIPBLAS_STATUS_SUCCESS)
+        return fail("linear: hipblasLtMatmul failed with status " + std::to_string(int(s)));
+    return true;
+}
+
+}  // namespace
+
+size_t linear_scratch_bytes(int M, int K, bool exact)
+{
+    if (M <= 0 || K <= 0)
+        return 0;
+    return round_up256(size_t(M) * size_t(padded_k(K)) * 2) * (exact ? 2 : 1);
+}
+
+bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *c,
+                   int64_t ldc, int M, int N, int K, bool exact, void *scratch,
+                   size_t scratch_bytes, hipStream_t st)
+{
+    if (M < 0 || N < 0 || K < 0)
+        return fail("linear: negative dimension");
+    if (int64_t(M) * N == 0)
+        return true;
+    if (lda < K || ldw < K || ldc < N)
+        return fail("linear: leading dimension smaller than the row length");
+    const int64_t kp = padded_k(K);
+    LtPlan *plan = nullptr;
+    if (K > 0 && (ldw % 8) == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
+        (reinterpret_cast<uintptr_t>(c) & 15u) == 0 && (ldc % 4) == 0) {
+        std::lock_guard<std::mutex> g(g_lt_mu);
+        plan = lt_plan(M, N, K, kp, ldw, ldc);
+    }
+    if (!plan)  // exact f32 MFMA on the original values
+        return launch_gemm(a, lda, w, true, ldw, c, ldc, M, N, K, st);
+    if (!scratch || scratch_bytes < linear_scratch_bytes(M, K, exact) ||
+        (reinterpret_cast<uintptr_t>(scratch) & 15u) != 0)
+        return fail("linear: scratch smaller than linear_scratch_bytes() or not 16-byte aligned");
+    SplitArgs s;
+    s.a = a;
+    s.lda = lda;
+    s.hi = static_cast<unsigned int *>(scratch);
+    s.lo = exact ? reinterpret_cast<unsigned int *>(static_cast<char *>(scratch) +
+                                                    round_up256(size_t(M) * kp * 2))
+                 : nullptr;
+    s.kp = kp;
+    s.M = M;
+    s.K = K;
+    s.vec = (reinterpret_cast<uintptr_t>(a) & 15u) == 0 && lda % 4 == 0;
+    s.total = int64_t(M) * kp / 8;
+    const int64_t nblk = (s.total + 255) / 256;
+    if (nblk > INT32_MAX)
+        return fail("linear: problem too large for one launch");
+    hipLaunchKernelGGL(split_kernel, dim3(unsigned(nblk)), dim3(256), 0, st, s);
+    if (!hip_ok(hipGetLastError(), "split_kernel launch"))
+        return false;
+    std::lock_guard<std::mutex> g(g_lt_mu);
+    if (!lt_matmul(plan, w, s.hi, c, 0.0f, st))
+        return false;
+    return !exact || lt_matmul(plan, w, s.lo, c, 1.0f, st);
+}
+
+}  // namespace anima_hip

@@ -262,6 +262,8 @@ def other_configs(c, cpu_rate):
         c.torch.cuda.empty_cache()
 
         res["c4_denoise_step_28_blocks"] = denoise_step(c, mode)
+        res["proj_gemm_8192x2048x2048"] = projection_gemm(c, mode)
+        res["c4_denoise_step_28_blocks_with_projections"] = denoise_step_with_projections(c, mode)
         out[variant] = res
         log(f"[bench] configs {variant}: " + json.dumps(res))
     if cpu_rate:
@@ -315,6 +317,89 @@ def denoise_step(c, mode, blocks=28, B=2, S=4096, H=16, D=128):
             "flops_per_step": flops,
             "includes": "q/k RMSNorm+RoPE prologues, flash self-attention, q prologue + cached "
                         "cross-attention (context K/V built once per block, outside the step)"}
+
+
+class Linear:
+    """anima_hip_linear_dev (bf16-MFMA projection GEMM) with its scratch."""
+
+    def __init__(self, c, mode, M, K):
+        self.c, self.mode = c, mode
+        self.nbytes = c.lib.anima_hip_linear_scratch_bytes(M, K, mode)
+        self.scratch = c.torch.empty(max(self.nbytes, 256), dtype=c.torch.uint8, device=c.dev)
+
+    def __call__(self, x, w, y):
+        """y[M,N] = x[M,K] . w[N,K]^T (w bf16 bits, int16 tensor)."""
+        M, K = x.shape
+        N = w.shape[0]
+        c = self.c
+        c._lib.check(c.lib.anima_hip_linear_dev(x.data_ptr(), K, w.data_ptr(), K, y.data_ptr(), N,
+                                                M, N, K, self.mode, self.scratch.data_ptr(),
+                                                self.nbytes, c.stp), "linear_dev")
+
+
+def projection_gemm(c, mode, M=8192, N=2048, K=2048):
+    """One q/k/v/output projection of a block at 4096 tokens, B=2."""
+    x = c.randn((M, K), 7001)
+    w = c.bf16_bits(c.randn((N, K), 7002, 0.02))
+    y = c.torch.empty((M, N), device=c.dev)
+    lin = Linear(c, mode, M, K)
+    ms = c.time(lambda: lin(x, w, y), 20, 3)
+    return {"ms": round(ms, 4), "tflops": round(2.0 * M * N * K / ms / 1e9, 2),
+            "note": "algorithmic 2*M*N*K; the f32 mode issues two bf16 products (hi + lo terms)"}
+
+
+def denoise_step_with_projections(c, mode, blocks=28, B=2, S=4096, H=16, D=128):
+    """The denoise step's attention blocks with their projections, as
+    NumpyAttention.forward runs them (numpy_dit.py:268-297): per block
+    q/k/v_proj -> self-attention -> output_proj, then cross q_proj ->
+    cached cross-attention -> output_proj.  Seeded per-block bf16 weights
+    ~N(0,0.02) and per-block hidden states ~N(0,1); context K/V caches are
+    built once per block outside the step."""
+    torch, lib, _lib = c.torch, c.lib, c._lib
+    from anima_hip.rope import generate_rope_freqs
+    M, C = B * S, H * D
+    freqs = torch.from_numpy(generate_rope_freqs(64, 64)).to(c.dev)
+    ones = torch.ones(D, device=c.dev)
+    caches = [context_cache(c, mode, 2, 4000 + i) for i in range(blocks)]
+    xs = [c.randn((M, C), 20000 + i) for i in range(blocks)]
+    ws = [[c.bf16_bits(c.randn((C, C), 30000 + 6 * i + j, 0.02)) for j in range(6)]
+          for i in range(blocks)]
+    q, k, v, o, y = (torch.empty((M, C), device=c.dev) for _ in range(5))
+    lin = Linear(c, mode, M, C)
+    n_self = lib.anima_hip_attention_scratch_bytes(B, S, B, S, H, D, mode)
+    n_x = lib.anima_hip_cross_attention_scratch_bytes(caches[0].handle, B, S)
+    scratch = torch.empty(max(n_self, n_x), dtype=torch.uint8, device=c.dev)
+    eps = ct.c_float(1e-6)
+
+    def step():
+        for i in range(blocks):
+            x, (wq, wk, wv, wo, wqx, wox) = xs[i], ws[i]
+            lin(x, wq, q)
+            lin(x, wk, k)
+            lin(x, wv, v)
+            _lib.check(lib.anima_hip_attention_dev(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                                   ones.data_ptr(), ones.data_ptr(),
+                                                   freqs.data_ptr(), o.data_ptr(),
+                                                   scratch.data_ptr(), n_self, B, S, B, S, H, D,
+                                                   eps, mode, c.stp), "attention_dev")
+            lin(o, wo, y)
+            lin(x, wqx, q)
+            _lib.check(lib.anima_hip_cross_attention_dev(q.data_ptr(), ones.data_ptr(),
+                                                         caches[i].handle, o.data_ptr(),
+                                                         scratch.data_ptr(), n_x, B, S, eps,
+                                                         c.stp), "cross_attention_dev")
+            lin(o, wox, y)
+    ms = c.time(step, 3, 1)
+    attn = blocks * 4.0 * B * H * S * D * (S + 512)
+    proj = blocks * 6 * 2.0 * M * C * C
+    for cache in caches:
+        cache.close()
+    del xs, ws
+    torch.cuda.empty_cache()
+    return {"ms_per_step": round(ms, 3), "tflops": round((attn + proj) / ms / 1e9, 2),
+            "flops_per_step": attn + proj, "projection_flops_per_step": proj,
+            "includes": "per block: q/k/v_proj, q/k prologues, flash self-attention, output_proj; "
+                        "cross q_proj, q prologue, cached cross-attention, output_proj"}
 
 
 def cpu_baseline(qn, kn, v, B, H, S, D, heads):

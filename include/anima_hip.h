@@ -148,6 +148,22 @@ bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const 
 bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, int64_t ldw,
                         float *c, int64_t ldc, int M, int N, int K, void *stream);
 
+/* Projection GEMM of the attention block on bf16 MFMA: C[M,N] = A[M,K] . W[N,K]^T
+ * with f32 activations a, bf16 weights w (bit patterns, [out_features, in_features]
+ * like the reference) and f32 output c, on device memory.  Replaces the
+ * projections of NumpyAttention.forward (anima_rt/scripts/numpy_dit.py:273-281,
+ * 294-296), computed there by anima_rt/vulkan/gemm_bf16.comp:25-57.
+ *   mode ANIMA_HIP_F32:  a enters as two bf16 terms hi + lo (per-element
+ *                        representation error <= 2^-16 |a|), f32 accumulation;
+ *   mode ANIMA_HIP_BF16: a is rounded to bf16 (<= 2^-8 |a|).
+ * scratch: anima_hip_linear_scratch_bytes(M, K, mode) bytes of device memory,
+ * 16-byte aligned; nothing is allocated.  Shapes without a library solution
+ * (e.g. ldw not a multiple of 8) run the exact f32-MFMA kernel instead. */
+size_t anima_hip_linear_scratch_bytes(int M, int K, int mode);
+bool anima_hip_linear_dev(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *c,
+                          int64_t ldc, int M, int N, int K, int mode, void *scratch,
+                          size_t scratch_bytes, void *stream);
+
 /* Device scratch needed by anima_hip_attention_dev for these sizes (bytes). */
 size_t anima_hip_attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D,
                                          int mode);

@@ -1,0 +1,111 @@
+"""Projection GEMM on bf16 MFMA (anima_hip_linear_dev) against the oracle's
+anima_rt GEMM (f32 activations x bf16 weights, f32 accumulation).
+
+Stated accuracy, normwise (max|out - ref| / max|ref|):
+* mode F32  (activations as bf16 hi + lo terms): <= 2e-5;
+* mode BF16 (activations rounded to bf16):        <= 1e-2.
+The F32 mode must also be far closer than the BF16 mode on the same data,
+which fails if the lo term were dropped.
+"""
+import ctypes as ct
+
+import numpy as np
+import pytest
+
+import oracle
+from anima_hip import _lib, rt
+
+pytestmark = pytest.mark.gpu
+
+REL_F32 = 2e-5
+REL_BF16 = 1e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    rt.init()
+
+
+def rel_err(out, ref):
+    return float(np.abs(out - ref).max() / np.abs(ref).max())
+
+
+def run_linear(a, w_bits, mode, lda=None):
+    """C = A W^T through anima_hip_linear_dev; `lda` > K places the rows of A
+    in a wider buffer."""
+    from devmem import DevBuf
+    lib = _lib.load()
+    M, K = a.shape
+    N = w_bits.shape[0]
+    lda = lda or K
+    abuf = np.zeros((M, lda), np.float32)
+    abuf[:, :K] = a
+    da, dw, dc = DevBuf.of(abuf), DevBuf.of(w_bits), DevBuf(M * N * 4)
+    sb = lib.anima_hip_linear_scratch_bytes(M, K, mode)
+    scratch = DevBuf(max(sb, 256))
+    ok = lib.anima_hip_linear_dev(da.addr, lda, dw.addr, K, dc.addr, N, M, N, K, mode,
+                                  scratch.addr, sb, None)
+    _lib.check(ok, "linear_dev")
+    return dc.get((M, N))
+
+
+def _data(seed, M, N, K):
+    rng = np.random.default_rng(seed)
+    a = rng.standard_normal((M, K), dtype=np.float32)
+    w = oracle.f32_to_bf16_bits(rng.standard_normal((N, K), dtype=np.float32) * 0.02)
+    return a, w
+
+
+# (M, N, K, lda): ragged M/N, the text-context K/V projection (Bc=1 and 2),
+# the 256-token q projection, K not a multiple of 8 (no library solution:
+# exact f32-MFMA fallback), and A rows inside a wider buffer.
+CASES = [(300, 200, 136, None), (512, 2048, 1024, None), (1024, 2048, 1024, None),
+         (512, 2048, 2048, None), (37, 64, 77, None), (200, 256, 512, 520)]
+
+
+@pytest.mark.parametrize("M,N,K,lda", CASES)
+def test_linear_modes(M, N, K, lda):
+    a, w = _data(M + N + K, M, N, K)
+    ref = oracle.gemm_bf16(a, w)
+    print(f"linear M={M} N={N} K={K} lda={lda}", flush=True)
+    e32 = rel_err(run_linear(a, w, rt.F32, lda), ref)
+    e16 = rel_err(run_linear(a, w, rt.BF16, lda), ref)
+    print(f"  rel err f32-split {e32:.2e}  bf16 {e16:.2e}", flush=True)
+    assert e32 <= REL_F32
+    assert e16 <= REL_BF16
+    if K % 8 == 0:
+        assert e32 * 20 < e16
+
+
+def test_linear_projection_8192x2048x2048_sampled_rows():
+    """The per-block projection at 4096 tokens, B=2: [8192, 2048] x [2048, 2048]^T;
+    64 rows (first, last and random) are checked against the oracle."""
+    M, N, K = 8192, 2048, 2048
+    a, w = _data(8192, M, N, K)
+    rows = np.unique(np.concatenate([[0, 1, 4095, 4096, M - 1],
+                                     np.random.default_rng(5).integers(0, M, 59)]))
+    ref = oracle.gemm_bf16(a[rows], w)
+    for mode, tol in ((rt.F32, REL_F32), (rt.BF16, REL_BF16)):
+        out = run_linear(a, w, mode)
+        assert np.isfinite(out).all()
+        err = rel_err(out[rows], ref)
+        print(f"  mode {mode}: rel err {err:.2e} on {len(rows)} rows", flush=True)
+        assert err <= tol
+
+
+def test_linear_drop_in_gemm_bf16_is_split_path():
+    """anima_rt_run_gemm_bf16 (host drop-in) runs the F32 split mode on shapes
+    the library GEMM supports, within the drop-in's 1e-5 bound."""
+    a, w = _data(11, 256, 512, 1024)
+    ref = oracle.gemm_bf16(a, w)
+    out = rt.gemm_bf16(a, w)
+    assert np.abs(out - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+
+
+def test_linear_errors():
+    lib = _lib.load()
+    assert not lib.anima_hip_linear_dev(None, 8, None, 8, None, 8, 4, 4, 8, 7, None, 0, None)
+    assert "mode" in _lib.last_error()
+    assert lib.anima_hip_linear_scratch_bytes(0, 8, rt.F32) == 0
+    assert (lib.anima_hip_linear_scratch_bytes(10, 9, rt.F32)
+            == 2 * lib.anima_hip_linear_scratch_bytes(10, 9, rt.BF16))
