@@ -16,9 +16,11 @@
 //     through LDS, double-buffered, one barrier per tile; row pitches are
 //     padded by 16 bytes so the per-lane 16-byte reads are conflict-free;
 //   * software-pipelined per wave: the MFMAs computing the scores of tile
-//     j+1 are interleaved (sched_group_barrier) with the VALU softmax of
-//     tile j, then P.V of tile j follows, so the MFMA pipe and the VALU
-//     overlap inside every wave;
+//     j+1 are interleaved (sched_barrier) with the VALU softmax of tile j,
+//     then P.V of tile j follows, so the MFMA pipe and the VALU overlap
+//     inside every wave; LDS fragments are read two MFMA pairs ahead of use
+//     and the compute section runs at raised wave priority (s_setprio);
+//   * the row sum l accumulates the bf16-rounded P that the P.V MFMAs use;
 //   * the softmax scale is folded into the exponent: p = exp2(s*c - m) with
 //     c = scale*log2(e) > 0, so the tile max is taken on raw scores; the
 //     running max m is updated lazily (only when a tile max exceeds it by
@@ -73,6 +75,20 @@ __device__ __forceinline__ float row_pair_max(float v)
 }
 
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// Sum of the 16 bf16 values of two P operands, in f32 (v_dot2_f32_bf16 with
+// a vector of ones).
+__device__ __forceinline__ float row_sum16(const bf16x8 &p, const bf16x8 &q)
+{
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    float a = 0.0f, b = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        a = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{p[i], p[i + 1]}, one, a, false);
+        b = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{q[i], q[i + 1]}, one, b, false);
+    }
+    return a + b;
+}
 
 __device__ __forceinline__ bf16x8 pack8(const f32x16 &s, int base)
 {
@@ -275,62 +291,75 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
         }
         const float neg_m = (m == -INFINITY) ? 0.0f : -m;
 
-        // ---- Pipelined section, one basic block, hand-interleaved: each step
-        // issues the K reads of the next step, one score MFMA of tile j+1, two
+        // ---- Pipelined section, one basic block, hand-interleaved.  Step t
+        // issues the K reads of step t+2, one score MFMA of tile j+1, two
         // exponentials of tile j, the other score MFMA and two more
-        // exponentials.  sched_barrier keeps the steps in this order so the
-        // MFMA pipe and the VALU work side by side.  (On the last tile the next
-        // K buffer holds stale data; those scores are never used.)
+        // exponentials; the last two steps also read the V^T fragments of the
+        // first P.V block.  sched_barrier keeps the steps in this order so the
+        // MFMA pipe and the VALU work side by side and every LDS read has two
+        // MFMA pairs to land.  (On the last tile the next K buffer holds stale
+        // data; those scores are never used.)  The wave runs this section at
+        // raised priority, so a wave still storing tiles or waiting at the
+        // barrier yields issue slots to it.
         const u16 *kr0 = &Ks[buf ^ 1][col * kKPitch + 64 * half];
         const u16 *kr1 = kr0 + 32 * kKPitch;
+        const u16 *vr = &Vs[buf][col * kVPitch + 8 * half];
+        bf16x8 kf0[8], kf1[8], vf[4][4];
+        auto read_k = [&](int t) {
+            kf0[t] = *reinterpret_cast<const bf16x8 *>(kr0 + 8 * t);
+            kf1[t] = *reinterpret_cast<const bf16x8 *>(kr1 + 8 * t);
+        };
+        auto read_v = [&](int blk, int i) {  // d block blk, keys [16i, 16i+16)
+            vf[blk][i] = *reinterpret_cast<const bf16x8 *>(vr + 32 * blk * kVPitch + 16 * i);
+        };
+        __builtin_amdgcn_s_setprio(1);
         f32x16 sn0 = {}, sn1 = {};
-        float ps0 = 0.0f, ps1 = 0.0f;
-        bf16x8 k0 = *reinterpret_cast<const bf16x8 *>(kr0);
-        bf16x8 k1 = *reinterpret_cast<const bf16x8 *>(kr1);
+        read_k(0);
+        read_k(1);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            bf16x8 k0n = k0, k1n = k1;
-            if (t < 7) {
-                k0n = *reinterpret_cast<const bf16x8 *>(kr0 + 8 * (t + 1));
-                k1n = *reinterpret_cast<const bf16x8 *>(kr1 + 8 * (t + 1));
+            if (t < 6)
+                read_k(t + 2);
+            if (t >= 6) {
+                read_v(0, 2 * (t - 6));
+                read_v(0, 2 * (t - 6) + 1);
             }
-            sn0 = mfma_bf16(k0, qf[t], sn0);
+            sn0 = mfma_bf16(kf0[t], qf[t], sn0);
             sc0[2 * t] = __builtin_amdgcn_exp2f(fmaf(sc0[2 * t], a.c, neg_m));
             sc0[2 * t + 1] = __builtin_amdgcn_exp2f(fmaf(sc0[2 * t + 1], a.c, neg_m));
-            ps0 += sc0[2 * t] + sc0[2 * t + 1];
-            sn1 = mfma_bf16(k1, qf[t], sn1);
+            sn1 = mfma_bf16(kf1[t], qf[t], sn1);
             sc1[2 * t] = __builtin_amdgcn_exp2f(fmaf(sc1[2 * t], a.c, neg_m));
             sc1[2 * t + 1] = __builtin_amdgcn_exp2f(fmaf(sc1[2 * t + 1], a.c, neg_m));
-            ps1 += sc1[2 * t] + sc1[2 * t + 1];
             __builtin_amdgcn_sched_barrier(0);
-            k0 = k0n;
-            k1 = k1n;
         }
-        l += ps0 + ps1;
         const bf16x8 p00 = pack8(sc0, 0), p01 = pack8(sc0, 8);
         const bf16x8 p10 = pack8(sc1, 0), p11 = pack8(sc1, 8);
+        // Row sum of the bf16 probabilities the P.V MFMAs consume, two per
+        // v_dot2_f32_bf16.
+        l += row_sum16(p00, p01) + row_sum16(p10, p11);
 
-        // P.V of tile j; meanwhile the VALU takes the max of tile j+1.
-        const u16 *vr = &Vs[buf][col * kVPitch + 8 * half];
+        // P.V of tile j, reading the V^T fragments of block blk+1 ahead;
+        // meanwhile the VALU takes the max of tile j+1.
         float a0 = -INFINITY, a1 = -INFINITY;
 #pragma unroll
         for (int blk = 0; blk < 4; ++blk) {
-            const u16 *vrow = vr + 32 * blk * kVPitch;
-            const bf16x8 v00 = *reinterpret_cast<const bf16x8 *>(vrow + 0);
-            const bf16x8 v01 = *reinterpret_cast<const bf16x8 *>(vrow + 16);
-            const bf16x8 v10 = *reinterpret_cast<const bf16x8 *>(vrow + 32);
-            const bf16x8 v11 = *reinterpret_cast<const bf16x8 *>(vrow + 48);
+            if (blk < 3) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    read_v(blk + 1, i);
+            }
             f32x16 &ob = blk == 0 ? o0 : blk == 1 ? o1 : blk == 2 ? o2 : o3;
-            ob = mfma_bf16(v00, p00, ob);
+            ob = mfma_bf16(vf[blk][0], p00, ob);
             a0 = fmaxf(a0, fmaxf(sn0[4 * blk], sn0[4 * blk + 1]));
-            ob = mfma_bf16(v01, p01, ob);
+            ob = mfma_bf16(vf[blk][1], p01, ob);
             a0 = fmaxf(a0, fmaxf(sn0[4 * blk + 2], sn0[4 * blk + 3]));
-            ob = mfma_bf16(v10, p10, ob);
+            ob = mfma_bf16(vf[blk][2], p10, ob);
             a1 = fmaxf(a1, fmaxf(sn1[4 * blk], sn1[4 * blk + 1]));
-            ob = mfma_bf16(v11, p11, ob);
+            ob = mfma_bf16(vf[blk][3], p11, ob);
             a1 = fmaxf(a1, fmaxf(sn1[4 * blk + 2], sn1[4 * blk + 3]));
             __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_s_setprio(0);
         mx_next = row_pair_max(fmaxf(a0, a1));
 
         if (has2)
