@@ -42,8 +42,8 @@ typedef unsigned short u16;
 
 constexpr int kD = 128;
 constexpr int kBN = 64;          // keys per tile (== kVtTile)
-constexpr int kKPitch = kD + 8;  // bf16 per LDS K row (272 bytes)
-constexpr int kVPitch = kBN + 8; // bf16 per LDS V^T row (144 bytes)
+constexpr int kStages = 3;          // depth of the K and V^T LDS rings
+constexpr int kTileElems = kBN * kD; // bf16 per K or V^T tile (16 KiB)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15)
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold: p <= 2^8
@@ -58,6 +58,47 @@ struct Bf16Args {
     int causal;
     FlashSplitArgs split;  // n == 1: write O; n > 1: write this split's partial
 };
+
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane i
+// of the wave writes bytes [16i, 16i + 16) of the wave-uniform 1 KiB LDS
+// window `lds` (through M0); no VGPRs hold the data.  Completion is counted
+// by vmcnt and waited for explicitly (wait_vmcnt).  Issued from inline asm so
+// that the compiler, which cannot tell the ring stages apart, does not put a
+// vmcnt(0) in front of every LDS read of another stage.
+// M0 is declared clobbered; nothing else in these kernels keeps a value in
+// M0 (checked in the generated assembly), so the reserved-register warning
+// does not apply.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const u16 *src, u16 *lds)
+{
+    const unsigned m0 = static_cast<unsigned>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)lds));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(m0), "v"(src)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 16, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+// Workgroup barrier for the LDS rings: this wave's LDS reads are complete
+// (lgkmcnt(0)), copies still in flight stay in flight (no vmcnt wait, unlike
+// __syncthreads), and the compiler moves no memory access across it.
+__device__ __forceinline__ void ring_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c)
 {
@@ -107,17 +148,15 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
 {
     constexpr int NT = NW * 64;
     constexpr int BM = NW * 32;
-    constexpr int KCH = kBN * kD / 8;  // 16-byte chunks per K tile
-    constexpr int VCH = kD * kBN / 8;  // 16-byte chunks per V^T tile
-    constexpr int LK = KCH / NT, LV = VCH / NT;
-    static_assert(KCH % NT == 0 && VCH % NT == 0, "tiles must split evenly");
+    constexpr int DMA = kTileElems / 8 / NT;  // 16-byte copies per thread per tile
+    static_assert(kTileElems / 8 % NT == 0, "tiles must split evenly");
 
-    __shared__ __attribute__((aligned(16))) u16 Ks[2][kBN * kKPitch];
-    __shared__ __attribute__((aligned(16))) u16 Vs[2][kD * kVPitch];
+    __shared__ __attribute__((aligned(16))) u16 Ks[kStages][kTileElems];
+    __shared__ __attribute__((aligned(16))) u16 Vs[kStages][kTileElems];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31;
     const int half = lane >> 5;
 
@@ -157,56 +196,51 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     const int j0 = sp * a.split.tiles;
     const int ntiles = max(0, min((kv_end + kBN - 1) / kBN - j0, a.split.tiles));
 
-    // K is fetched two tiles ahead and V one tile ahead: iteration j reads
-    // K(j+1) (scores of the next tile) and V(j) (P.V of this tile) while
-    // K(j+2) and V(j+1) travel from HBM through registers into the buffers
-    // that K(j) and V(j-1) used.  One barrier per tile keeps this safe.
-    f32x4 kst[LK], vst[LV];
-    auto gload_k = [&](int key0) {
+    // K and V^T tiles reach LDS by DMA through rings of kStages buffers:
+    // tile t lives in stage t % 3.  Iteration j reads K(j+1) (scores of the
+    // next tile) and V^T(j) (P.V of this tile) and starts the copies of
+    // K(j+3) and V^T(j+2), which have two iterations to land.
+    // Layouts, unpadded, XOR-swizzled so every 16-lane group of a fragment
+    // read hits distinct banks:
+    //   K   [64 keys][128 d]: 16-byte chunk c of key row r at chunk c ^ (r & 15);
+    //   V^T [128 d][64 keys]: chunk c of d row r at chunk c ^ ((r >> 1) & 7).
+    // Keys past S_kv copy row S_kv - 1 (their scores are masked); V^T is
+    // zero-padded in HBM to whole tiles.
+    auto dma_k = [&](int t, int stage) {
+        const int key0 = (j0 + t) * kBN;
 #pragma unroll
-        for (int i = 0; i < LK; ++i) {
-            const int f = tid + i * NT;
-            const int r = f >> 4, c = f & 15;
-            const int key = key0 + r;
-            kst[i] = key < a.S_kv ? *reinterpret_cast<const f32x4 *>(kp + key * a.ks + 8 * c)
-                                  : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < DMA; ++i) {
+            const int w = wave * DMA + i;  // 1 KiB window of the tile
+            const int f = w * 64 + lane;   // 16-byte chunk slot
+            const int r = f >> 4, c = (f & 15) ^ (r & 15);
+            const int key = min(key0 + r, a.S_kv - 1);
+            dma16(kp + key * a.ks + 8 * c, &Ks[stage][w * 512]);
         }
     };
-    auto gload_v = [&](int key0) {
+    auto dma_v = [&](int t, int stage) {
+        const int key0 = (j0 + t) * kBN;
 #pragma unroll
-        for (int i = 0; i < LV; ++i) {
-            const int f = tid + i * NT;
-            const int d = f >> 3, c = f & 7;
-            vst[i] = *reinterpret_cast<const f32x4 *>(vp + d * a.vd + key0 + 8 * c);
+        for (int i = 0; i < DMA; ++i) {
+            const int w = wave * DMA + i;
+            const int f = w * 64 + lane;
+            const int r = f >> 3, c = (f & 7) ^ ((r >> 1) & 7);
+            dma16(vp + r * a.vd + key0 + 8 * c, &Vs[stage][w * 512]);
         }
     };
-    auto lstore_k = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < LK; ++i) {
-            const int f = tid + i * NT;
-            const int r = f >> 4, c = f & 15;
-            *reinterpret_cast<f32x4 *>(&Ks[buf][r * kKPitch + 8 * c]) = kst[i];
-        }
-    };
-    auto lstore_v = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < LV; ++i) {
-            const int f = tid + i * NT;
-            const int d = f >> 3, c = f & 7;
-            *reinterpret_cast<f32x4 *>(&Vs[buf][d * kVPitch + 8 * c]) = vst[i];
-        }
-    };
-    // S^T of one 64-key tile from the K buffer `buf`: keys [0,32) in s0,
+    // Element offsets of this lane's fragments inside a stage: K rows col and
+    // col + 32, chunk 8*half + t; V^T rows col + 32*blk, chunk half + 2i.
+    const int ksw = col & 15, vsw = (col >> 1) & 7;
+    auto koff = [&](int t) { return col * kD + 8 * (((half << 3) | t) ^ ksw); };
+    auto voff = [&](int i) { return col * kBN + 8 * ((half + 2 * i) ^ vsw); };
+    // S^T of one 64-key tile from K stage `stage`: keys [0,32) in s0,
     // [32,64) in s1.
-    auto scores = [&](int buf, f32x16 &s0, f32x16 &s1) {
-        const u16 *kr0 = &Ks[buf][col * kKPitch + 64 * half];
-        const u16 *kr1 = kr0 + 32 * kKPitch;
+    auto scores = [&](int stage, f32x16 &s0, f32x16 &s1) {
         s0 = f32x16{};
         s1 = f32x16{};
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const bf16x8 k0 = *reinterpret_cast<const bf16x8 *>(kr0 + 8 * t);
-            const bf16x8 k1 = *reinterpret_cast<const bf16x8 *>(kr1 + 8 * t);
+            const bf16x8 k0 = *reinterpret_cast<const bf16x8 *>(&Ks[stage][koff(t)]);
+            const bf16x8 k1 = *reinterpret_cast<const bf16x8 *>(&Ks[stage][koff(t) + 32 * kD]);
             s0 = mfma_bf16(k0, qf[t], s0);
             s1 = mfma_bf16(k1, qf[t], s1);
         }
@@ -215,22 +249,26 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     f32x16 o0 = {}, o1 = {}, o2 = {}, o3 = {};
     float m = -INFINITY;
     float l = 0.0f;
-    f32x16 sc0 = {}, sc1 = {};  // scores of the tile being consumed
+    // Scores of two consecutive tiles; the loop below is unrolled by two so
+    // the pair being consumed and the pair being produced swap roles without
+    // register copies.
+    f32x16 sa0 = {}, sa1 = {}, sb0 = {}, sb1 = {};
 
     if (ntiles > 0) {
-        gload_k(j0 * kBN);
-        gload_v(j0 * kBN);
-        lstore_k(0);
-        lstore_v(0);
-        if (ntiles > 1) {
-            gload_k((j0 + 1) * kBN);
-            lstore_k(1);
-        }
+        dma_k(0, 0);
+        if (ntiles > 1)
+            dma_k(1, 1);
+        dma_v(0, 0);
     }
-    __syncthreads();
+    wait_vmcnt<0>();
+    ring_barrier();
     if (ntiles > 0)
-        scores(0, sc0, sc1);
-    __syncthreads();  // K buffer 0 is rewritten in the first iteration
+        scores(0, sa0, sa1);
+    if (ntiles > 2)
+        dma_k(2, 2);
+    if (ntiles > 1)
+        dma_v(1, 1);
+    ring_barrier();  // K stage 0 is rewritten in the first iteration
 
     // Raw-score tile max over a lane's 32 scores, combined across the two
     // lanes of the row (c > 0, so the max commutes with the scaling).
@@ -245,15 +283,17 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     };
     // Max of the unmasked scores of the tile consumed next; the pipelined
     // section computes it for tile j+1 while the P.V MFMAs of tile j run.
-    float mx_next = ntiles > 0 ? tile_max(sc0, sc1) : -INFINITY;
+    float mx_next = ntiles > 0 ? tile_max(sa0, sa1) : -INFINITY;
 
-    for (int j = 0; j < ntiles; ++j) {
-        const int buf = j & 1;
-        const bool has1 = j + 1 < ntiles, has2 = j + 2 < ntiles;
-        if (has2)
-            gload_k((j0 + j + 2) * kBN);
-        if (has1)
-            gload_v((j0 + j + 1) * kBN);
+    // Tile j: consumes the scores sc0/sc1 of tile j, produces sn0/sn1 of
+    // tile j+1.
+    auto tile = [&](const int j, f32x16 &sc0, f32x16 &sc1, f32x16 &sn0, f32x16 &sn1) {
+        const int sv = j % kStages, sk = (j + 1) % kStages;  // stages of V^T(j), K(j+1)
+        const bool dk = j + 3 < ntiles, dv = j + 2 < ntiles;
+        if (dk)
+            dma_k(j + 3, sv);
+        if (dv)
+            dma_v(j + 2, (j + 2) % kStages);
 
         float mx = mx_next;
         const int key0 = (j0 + j) * kBN;
@@ -301,19 +341,19 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
         // data; those scores are never used.)  The wave runs this section at
         // raised priority, so a wave still storing tiles or waiting at the
         // barrier yields issue slots to it.
-        const u16 *kr0 = &Ks[buf ^ 1][col * kKPitch + 64 * half];
-        const u16 *kr1 = kr0 + 32 * kKPitch;
-        const u16 *vr = &Vs[buf][col * kVPitch + 8 * half];
+        const u16 *kst = Ks[sk];
+        const u16 *vst = Vs[sv];
         bf16x8 kf0[8], kf1[8], vf[4][4];
         auto read_k = [&](int t) {
-            kf0[t] = *reinterpret_cast<const bf16x8 *>(kr0 + 8 * t);
-            kf1[t] = *reinterpret_cast<const bf16x8 *>(kr1 + 8 * t);
+            kf0[t] = *reinterpret_cast<const bf16x8 *>(kst + koff(t));
+            kf1[t] = *reinterpret_cast<const bf16x8 *>(kst + koff(t) + 32 * kD);
         };
         auto read_v = [&](int blk, int i) {  // d block blk, keys [16i, 16i+16)
-            vf[blk][i] = *reinterpret_cast<const bf16x8 *>(vr + 32 * blk * kVPitch + 16 * i);
+            vf[blk][i] = *reinterpret_cast<const bf16x8 *>(vst + voff(i) + 32 * blk * kBN);
         };
         __builtin_amdgcn_s_setprio(1);
-        f32x16 sn0 = {}, sn1 = {};
+        sn0 = f32x16{};
+        sn1 = f32x16{};
         read_k(0);
         read_k(1);
 #pragma unroll
@@ -362,14 +402,24 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
         __builtin_amdgcn_s_setprio(0);
         mx_next = row_pair_max(fmaxf(a0, a1));
 
-        if (has2)
-            lstore_k(buf);
-        if (has1)
-            lstore_v(buf ^ 1);
-        __syncthreads();
-        sc0 = sn0;
-        sc1 = sn1;
+        // K(j+2) and V^T(j+1) were started one iteration ago: wait until only
+        // this iteration's copies are outstanding, then let every wave see them.
+        const int inflight = DMA * (int(dk) + int(dv));
+        if (inflight == 2 * DMA)
+            wait_vmcnt<2 * DMA>();
+        else if (inflight == DMA)
+            wait_vmcnt<DMA>();
+        else
+            wait_vmcnt<0>();
+        ring_barrier();
+    };
+    int j = 0;
+    for (; j + 1 < ntiles; j += 2) {
+        tile(j, sa0, sa1, sb0, sb1);
+        tile(j + 1, sb0, sb1, sa0, sa1);
     }
+    if (j < ntiles)
+        tile(j, sa0, sa1, sb0, sb1);
 
     l += __shfl_xor(l, 32);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
