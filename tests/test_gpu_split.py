@@ -115,3 +115,21 @@ def test_device_entries_without_scratch():
                                       None, vts, None, scale, False, None)
     _lib.check(ok, "flash_bf16_dev")
     assert rel_err(o2.get(q.shape), ref) <= REL
+
+
+@pytest.mark.parametrize("mode", [rt.F32, rt.BF16])
+def test_empty_key_set_and_zero_sizes(mode):
+    """S_kv = 0 gives O = 0 (no visible key; anima_rt's flash_attention divides
+    by zero computing its key-slice count there, flash_attention.h:66-70, so the
+    oracle is not called), and zero-size problems are no-ops."""
+    q = np.ones((2, 5, 128), np.float32)
+    empty = np.zeros((2, 0, 128), np.float32)
+    out = np.full((2, 5, 128), np.nan, np.float32)  # must be overwritten with zeros
+    ok = _lib.load().anima_hip_sdpa(q.ctypes.data, empty.ctypes.data, empty.ctypes.data,
+                                    out.ctypes.data, 2, 5, 0, 128, ct.c_float(128 ** -0.5), False,
+                                    int(mode))
+    _lib.check(ok, "anima_hip_sdpa")
+    assert not np.isnan(out).any() and not out.any()
+    assert rt.sdpa(np.zeros((2, 0, 128), np.float32), q, q, mode=mode).shape == (2, 0, 128)
+    none = np.zeros((0, 5, 128), np.float32)
+    assert rt.sdpa(none, empty[:0], empty[:0], mode=mode).shape == (0, 5, 128)
