@@ -133,3 +133,22 @@ def test_empty_key_set_and_zero_sizes(mode):
     assert rt.sdpa(np.zeros((2, 0, 128), np.float32), q, q, mode=mode).shape == (2, 0, 128)
     none = np.zeros((0, 5, 128), np.float32)
     assert rt.sdpa(none, empty[:0], empty[:0], mode=mode).shape == (0, 5, 128)
+
+
+@pytest.mark.parametrize("mode", [rt.F32, rt.BF16])
+def test_long_sequence_32768_sampled_rows(mode):
+    """S_q = S_kv = 32768 (8x the 1024x1024 latent), two heads: 64 query rows
+    (first, last, random) against the oracle over all 32768 keys; query rows
+    are independent, so the oracle runs on the sampled rows only."""
+    rng = np.random.default_rng(32768 + mode)
+    bh, S = 2, 32768
+    q, k, v = randn(rng, bh, S, 128), randn(rng, bh, S, 128), randn(rng, bh, S, 128)
+    print(f"long sequence mode={mode} S={S}", flush=True)
+    out = rt.sdpa(q, k, v, mode=mode)
+    assert np.isfinite(out).all()
+    rows = np.unique(np.concatenate([[0, 1, S - 2, S - 1], rng.integers(0, S, 60)]))
+    ref = oracle.flash_sdpa(np.ascontiguousarray(q[:, rows]), k, v, threads=2)
+    if mode == rt.F32:
+        assert np.abs(out[:, rows] - ref).max() <= TOL
+    else:
+        assert rel_err(out[:, rows], ref) <= REL
