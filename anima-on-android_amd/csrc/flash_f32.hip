@@ -17,7 +17,9 @@
 //   * the output is accumulated transposed, O^T += V^T P^T: the B operand of
 //     that MFMA is exactly the S^T accumulator (after exp2), so P never moves
 //     between lanes, and the per-row rescale factor is lane-local too;
-//   * exp is evaluated as exp2(s * scale*log2(e) - m) on v_exp_f32.
+//   * exp is evaluated as exp2(s * scale*log2(e) - m) on v_exp_f32, with the
+//     running max m updated lazily (only when a tile max exceeds it by more
+//     than 8 in log2 units), so the O rescale is almost never executed.
 // The contraction index d is permuted (lane half h walks d = 64h + t) so each
 // lane reads K and Q as contiguous float4s; the permutation is applied to Q
 // and K alike, so the dot products are unchanged.
@@ -37,6 +39,7 @@ constexpr int kKStride = kD + 4; // LDS row pitch of K (floats): 16-byte skew pe
 constexpr int kVStride = kD;     // LDS row pitch of V: rows are read whole
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15)
+constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold: p <= 2^8
 
 struct F32Args {
     const float *q, *k, *v;
@@ -212,10 +215,22 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_f32_d128(F32Args a)
             mx = fmaxf(mx, fmaxf(x0, x1));
         }
         mx = row_pair_max(mx);
-        const float m_new = fmaxf(m, mx);
-        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-        m = m_new;
+        // Lazy rescale: the reference max m (log2 domain) moves only when some
+        // row of the wave sees a tile max above m + kRescaleLog2, and then for
+        // the whole wave at once; otherwise the exponentials stay <= 2^8 and
+        // O, l keep accumulating against the same m (exact, since the final
+        // O / l shares it).  The O rescale is therefore almost never run.
+        if (__any(mx > m + kRescaleLog2)) {
+            const float m_new = fmaxf(m, mx);
+            const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+            m = m_new;
+            l *= alpha;
+            o0 *= alpha;
+            o1 *= alpha;
+            o2 *= alpha;
+            o3 *= alpha;
+        }
+        const float m_use = (m == -INFINITY) ? 0.0f : m;
 
         float psum = 0.0f;
 #pragma unroll
@@ -224,17 +239,13 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_f32_d128(F32Args a)
             s1[r] = __builtin_amdgcn_exp2f(s1[r] - m_use);
             psum += s0[r] + s1[r];
         }
-        l = l * alpha + psum;
+        l += psum;
         // V of the next tile goes to the other buffer (last read before the
         // previous barrier), then K of the next tile is fetched.
         if (more) {
             lstore(Vs[buf ^ 1], kVStride);
             gload(kp, a.ks, (j + 1) * kBN);
         }
-        o0 *= alpha;
-        o1 *= alpha;
-        o2 *= alpha;
-        o3 *= alpha;
 
         // O^T[d][q] += V^T P^T.  Output block c holds d = 4*i + c, so one
         // float4 read of a V row feeds the four blocks.
