@@ -24,6 +24,12 @@
  *       the D=4 known-answer test of scripts/test_rope_debug.py:17-34;
  *       norm preservation per rotated pair.
  *   oracle_gemm_bf16        -- fp64 GEMM on the bf16-decoded weights.
+ *   oracle_layernorm        -- bit-identical to oracle/_ref anima_rt_run_layernorm;
+ *       fp64 two-pass mean/variance.
+ *   oracle_silu             -- bit-identical to oracle/_ref anima_rt_run_silu;
+ *       fp64 x / (1 + exp(-x)).
+ *   oracle_modulate, oracle_gate_residual -- numpy float32 evaluation of the
+ *       same expressions (each operation rounded to float32).
  */
 #include <math.h>
 #include <stdint.h>
@@ -356,4 +362,68 @@ void oracle_gemm_bf16(const float *A, const uint16_t *W, float *C, int M, int N,
             }
             C[(int64_t)i * N + j] = acc;
         }
+}
+
+/* LayerNorm without affine parameters, as anima_rt_run_layernorm calls it
+ * (anima_rt/src/anima_rt.cpp:36-43 -> layernorm_kernel,
+ * anima_rt/include/cpu/layernorm_kernel.h:13-33): Welford moments
+ * (anima_rt/include/cpu/welford.h:15-31, one correctly rounded divide per
+ * step), population variance, rstd = 1/sqrt(var + eps), y = (x - mean)*rstd. */
+void oracle_layernorm(const float *X, float *Y, int64_t M, int64_t D, float eps)
+{
+    for (int64_t r = 0; r < M; r++) {
+        const float *x = X + r * D;
+        float *y = Y + r * D;
+        float mean = 0.0f, m2 = 0.0f;
+        int64_t count = 0;
+        for (int64_t i = 0; i < D; i++) {
+            const float v = x[i];
+            count++;
+            const float delta = v - mean;
+            mean += delta / (float)count;
+            const float delta2 = v - mean;
+            m2 += delta * delta2;
+        }
+        const float var = count > 0 ? m2 / (float)count : 0.0f;
+        const float rstd = 1.0f / sqrtf(var + eps);
+        for (int64_t j = 0; j < D; j++)
+            y[j] = (x[j] - mean) * rstd;
+    }
+}
+
+/* SiLU (anima_rt/include/cpu/silu_kernel.h:11-20): x / (1 + exp(-x)). */
+void oracle_silu(const float *x, float *y, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++)
+        y[i] = x[i] / (1.0f + expf(-x[i]));
+}
+
+/* AdaLN modulation of NumpyBlock.forward (anima_rt/scripts/numpy_dit.py:238,
+ * 244, 250), x_m = x_n*(1.0 + scale) + shift in float32, with per-batch
+ * vectors: x_n [B, S, D], scale/shift [B, D]. */
+void oracle_modulate(const float *xn, const float *scale, const float *shift, float *y,
+                     int B, int64_t S, int64_t D)
+{
+    for (int b = 0; b < B; b++)
+        for (int64_t s = 0; s < S; s++)
+            for (int64_t d = 0; d < D; d++) {
+                const int64_t i = ((int64_t)b * S + s) * D + d;
+                const float t = 1.0f + scale[(int64_t)b * D + d];
+                const float m = xn[i] * t;
+                y[i] = m + shift[(int64_t)b * D + d];
+            }
+}
+
+/* Gated residual of NumpyBlock.forward (numpy_dit.py:240, 246, 252),
+ * x = x + gate*out in float32, per-batch gate [B, D]; x updated in place. */
+void oracle_gate_residual(float *x, const float *gate, const float *out, int B, int64_t S,
+                          int64_t D)
+{
+    for (int b = 0; b < B; b++)
+        for (int64_t s = 0; s < S; s++)
+            for (int64_t d = 0; d < D; d++) {
+                const int64_t i = ((int64_t)b * S + s) * D + d;
+                const float g = gate[(int64_t)b * D + d] * out[i];
+                x[i] = x[i] + g;
+            }
 }

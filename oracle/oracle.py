@@ -7,8 +7,9 @@ and has no CPU fallback.
 
 Contents
   * ctypes wrappers over ``liboracle.so`` (``anima_oracle.c``): the plain-C
-    restatement of anima_rt's flash SDPA, math SDPA, RMSNorm, RoPE and bf16
-    GEMM, bit-identical to the reference runtime.
+    restatement of anima_rt's flash SDPA, math SDPA, RMSNorm, RoPE, bf16
+    GEMM, LayerNorm and SiLU, bit-identical to the reference runtime, and the
+    float32 AdaLN modulate / gated residual of NumpyBlock.forward.
   * ctypes wrappers over ``_ref/libanima_rt_ref.so``: the reference runtime
     itself, compiled from its sources (present only where it was built).
   * numpy restatements of the NumpyDiT host pieces: the 3D RoPE table
@@ -26,6 +27,11 @@ Pinning status (each function is checked by something other than itself):
       numpy_dit.py's float32 rounding is "parity unpinned" (would need an
       import of the reference) and is covered only to 1 ulp-level tolerance.
   numpy_rope -- same arithmetic as rope (checked bit-identical against it).
+  layernorm, silu -- bit-identical to the compiled reference and the golden
+      vectors it wrote; fp64 two-pass moments / fp64 x/(1+exp(-x)).
+  modulate, gate_residual -- fp64 evaluation within float32 rounding, and
+      closed cases (scale = shift = 0 is identity, gate = 0 keeps x).
+  attention_block -- composition of the pinned pieces above.
 """
 from __future__ import annotations
 
@@ -78,6 +84,14 @@ def oracle_lib():
         lib.oracle_gemm_bf16.restype = None
         lib.oracle_f32_to_bf16.argtypes = [_F]
         lib.oracle_f32_to_bf16.restype = _ct.c_uint16
+        lib.oracle_layernorm.argtypes = [_P, _P, _ct.c_int64, _ct.c_int64, _F]
+        lib.oracle_layernorm.restype = None
+        lib.oracle_silu.argtypes = [_P, _P, _ct.c_int64]
+        lib.oracle_silu.restype = None
+        lib.oracle_modulate.argtypes = [_P, _P, _P, _P, _I, _ct.c_int64, _ct.c_int64]
+        lib.oracle_modulate.restype = None
+        lib.oracle_gate_residual.argtypes = [_P, _P, _P, _I, _ct.c_int64, _ct.c_int64]
+        lib.oracle_gate_residual.restype = None
         _oracle_lib = lib
     return _oracle_lib
 
@@ -103,6 +117,10 @@ def ref_lib():
         lib.anima_rt_run_rope.restype = _ct.c_bool
         lib.anima_rt_run_gemm_bf16.argtypes = [_P, _P, _P, _I, _I, _I]
         lib.anima_rt_run_gemm_bf16.restype = _ct.c_bool
+        lib.anima_rt_run_layernorm.argtypes = [_P, _P, _I, _I, _F]
+        lib.anima_rt_run_layernorm.restype = _ct.c_bool
+        lib.anima_rt_run_silu.argtypes = [_P, _P, _I]
+        lib.anima_rt_run_silu.restype = _ct.c_bool
         if not lib.anima_rt_init():
             raise RuntimeError("reference anima_rt_init failed")
         _ref_lib = lib
@@ -159,6 +177,73 @@ def rmsnorm(x, w=None, eps=1e-6):
         wp = _ptr(w)
     oracle_lib().oracle_rmsnorm(_ptr(x), wp, _ptr(y), M, D, eps)
     return y
+
+
+def layernorm(x, eps=1e-6):
+    """LayerNorm without affine over the last axis restated
+    (anima_rt_run_layernorm -> layernorm_kernel.h:13-33, welford.h:15-31)."""
+    x = _f32c(x)
+    D = x.shape[-1]
+    y = np.empty_like(x)
+    oracle_lib().oracle_layernorm(_ptr(x), _ptr(y), x.size // D, D, eps)
+    return y
+
+
+def silu(x):
+    """SiLU restated (silu_kernel.h:11-20)."""
+    x = _f32c(x)
+    y = np.empty_like(x)
+    oracle_lib().oracle_silu(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def modulate(xn, scale, shift):
+    """x_n*(1.0 + scale) + shift in float32 (numpy_dit.py:238); xn [B,S,D],
+    scale/shift [B,D]."""
+    xn, scale, shift = _f32c(xn), _f32c(scale), _f32c(shift)
+    B, S, D = xn.shape
+    y = np.empty_like(xn)
+    oracle_lib().oracle_modulate(_ptr(xn), _ptr(scale), _ptr(shift), _ptr(y), B, S, D)
+    return y
+
+
+def gate_residual(x, gate, out):
+    """x + gate*out in float32 (numpy_dit.py:240); x/out [B,S,D], gate [B,D]."""
+    x = _f32c(x).copy()
+    gate, out = _f32c(gate), _f32c(out)
+    B, S, D = x.shape
+    oracle_lib().oracle_gate_residual(_ptr(x), _ptr(gate), _ptr(out), B, S, D)
+    return x
+
+
+def attention_block(x, mod, wq, wk, wv, wo, q_norm_w, k_norm_w, freqs=None, ctx=None,
+                    heads=16, head_dim=128, eps=1e-6, sdpa=None):
+    """One attention sub-block of NumpyBlock.forward (numpy_dit.py:236-247):
+    x + gate * output_proj(attention(layernorm(x)*(1+scale) + shift)).
+    x [B,S,Dm]; mod [B,3,Dm] = (shift, scale, gate); w* bf16 bit patterns
+    [out, in]; self-attention when ctx is None (K/V from the modulated x,
+    RoPE with freqs), else cross-attention with K/V projected from ctx
+    [Bc,Sk,C] (Bc 1 broadcasts over the batch) and no RoPE."""
+    x = _f32c(x)
+    B, S, Dm = x.shape
+    shift, scale, gate = (np.ascontiguousarray(mod[:, i]) for i in range(3))
+    xm = modulate(layernorm(x, eps), scale, shift)
+    HD = heads * head_dim
+    q = gemm_bf16(xm.reshape(B * S, Dm), wq).reshape(B, S, heads, head_dim)
+    if ctx is None:
+        k = gemm_bf16(xm.reshape(B * S, Dm), wk).reshape(B, S, heads, head_dim)
+        v = gemm_bf16(xm.reshape(B * S, Dm), wv).reshape(B, S, heads, head_dim)
+    else:
+        ctx = _f32c(ctx)
+        Bc, Sk, C = ctx.shape
+        k = np.stack([gemm_bf16(ctx[b], wk) for b in range(Bc)]).reshape(Bc, Sk, heads, head_dim)
+        v = np.stack([gemm_bf16(ctx[b], wv) for b in range(Bc)]).reshape(Bc, Sk, heads, head_dim)
+        k = np.broadcast_to(k, (B, Sk, heads, head_dim))
+        v = np.broadcast_to(v, (B, Sk, heads, head_dim))
+    attn = attention_dataflow(q, k, v, q_norm_w, k_norm_w, freqs if ctx is None else None,
+                              eps, sdpa)
+    out = gemm_bf16(attn.reshape(B * S, HD), wo).reshape(B, S, Dm)
+    return gate_residual(x, gate, out)
 
 
 def rope(t, freqs):
@@ -219,6 +304,21 @@ def ref_math_sdpa(q, k, v, scale=None, is_causal=False):
     assert ref_lib().anima_rt_run_sdpa(_ptr(q), _ptr(k), _ptr(v), _ptr(o), BH, Sq, Sk, D,
                                        scale, bool(is_causal))
     return o
+
+
+def ref_layernorm(x, eps=1e-6):
+    x = _f32c(x)
+    D = x.shape[-1]
+    y = np.zeros_like(x)
+    assert ref_lib().anima_rt_run_layernorm(_ptr(x), _ptr(y), x.size // D, D, eps)
+    return y
+
+
+def ref_silu(x):
+    x = _f32c(x)
+    y = np.zeros_like(x)
+    assert ref_lib().anima_rt_run_silu(_ptr(x), _ptr(y), x.size)
+    return y
 
 
 def ref_rmsnorm(x, w=None, eps=1e-6):

@@ -87,6 +87,17 @@ def main():
     vec["gemm_a"], vec["gemm_w_bf16"] = a, wb
     vec["gemm_out"] = oracle.ref_gemm_bf16(a, wb)
 
+    # LayerNorm (no affine, eps 1e-6 as NumpyRT calls it) on DiT-width rows
+    # with an offset mean, and SiLU over a range that includes large |x|.
+    ln_x = normal(rng, 6, 2048, sigma=2.0) + np.float32(0.75)
+    vec["ln_x"] = ln_x
+    vec["ln_out"] = oracle.ref_layernorm(ln_x, 1e-6)
+    silu_x = np.concatenate([normal(rng, 1000, sigma=4.0),
+                             np.array([0.0, -0.0, 1e-8, -1e-8, 30.0, -30.0, 88.0, -88.0,
+                                       -100.0], np.float32)]).astype(np.float32)
+    vec["silu_x"] = silu_x
+    vec["silu_out"] = oracle.ref_silu(silu_x)
+
     np.savez_compressed(OUT, **vec)
     print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes, {len(vec)} arrays)")
 

@@ -197,3 +197,90 @@ def test_attention_dataflow_vs_fp64():
     vt = v.transpose(0, 2, 1, 3).reshape(B * H, S, D)
     ref = oracle.sdpa_fp64(qt, kt, vt).reshape(B, H, S, D).transpose(0, 2, 1, 3)
     assert np.abs(out - ref).max() < 5e-6
+
+
+# ---------------------------------------------------- block-level pieces
+
+def test_layernorm_and_silu_match_reference_vectors(gold):
+    np.testing.assert_array_equal(oracle.layernorm(gold["ln_x"], 1e-6), gold["ln_out"])
+    np.testing.assert_array_equal(oracle.silu(gold["silu_x"]), gold["silu_out"])
+
+
+def test_layernorm_vs_fp64_two_pass():
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal((16, 2048)) * 3 + 1.5).astype(np.float32)
+    xd = x.astype(np.float64)
+    mu = xd.mean(-1, keepdims=True)
+    ref = (xd - mu) / np.sqrt(((xd - mu) ** 2).mean(-1, keepdims=True) + 1e-6)
+    assert np.abs(oracle.layernorm(x) - ref).max() < 2e-5
+    # A constant row has zero variance: y = 0 exactly.
+    np.testing.assert_array_equal(oracle.layernorm(np.full((1, 64), 3.25, np.float32)), 0.0)
+
+
+def test_silu_vs_fp64():
+    x = np.linspace(-40, 40, 4001, dtype=np.float32)
+    ref = x.astype(np.float64) / (1.0 + np.exp(-x.astype(np.float64)))
+    assert np.abs(oracle.silu(x) - ref).max() <= 4 * np.spacing(np.abs(ref).astype(np.float32)).max()
+
+
+def test_modulate_and_gate_residual():
+    rng = np.random.default_rng(22)
+    xn = rng.standard_normal((2, 5, 64), dtype=np.float32)
+    sc, sh, g = (rng.standard_normal((2, 64), dtype=np.float32) for _ in range(3))
+    out = rng.standard_normal((2, 5, 64), dtype=np.float32)
+    # Closed cases: zero scale/shift is the identity, zero gate keeps x.
+    z = np.zeros((2, 64), np.float32)
+    np.testing.assert_array_equal(oracle.modulate(xn, z, z), xn)
+    np.testing.assert_array_equal(oracle.gate_residual(xn, z, out), xn)
+    # Each operation rounds to float32 once: matches fp64 to a few ulps.
+    m = oracle.modulate(xn, sc, sh)
+    md = xn.astype(np.float64) * (1.0 + sc[:, None].astype(np.float64)) + sh[:, None]
+    assert np.abs(m - md).max() <= 4 * np.spacing(np.abs(md).max().astype(np.float32))
+    r = oracle.gate_residual(xn, g, out)
+    rd = xn.astype(np.float64) + g[:, None].astype(np.float64) * out
+    assert np.abs(r - rd).max() <= 4 * np.spacing(np.abs(rd).max().astype(np.float32))
+    # And the float32 order is the numpy one: (x_n * (1 + scale)) + shift.
+    np.testing.assert_array_equal(m, xn * (np.float32(1.0) + sc[:, None]) + sh[:, None])
+    np.testing.assert_array_equal(r, xn + g[:, None] * out)
+
+
+@pytest.mark.parametrize("cross", [False, True])
+def test_attention_block_vs_fp64(cross):
+    """The composed sub-block against the same dataflow in float64: LayerNorm,
+    modulate, bf16-weight projections, per-head RMSNorm, RoPE (self only),
+    softmax attention, output projection, gated residual."""
+    rng = np.random.default_rng(23 + cross)
+    B, S, Dm, H, D, Sk, C = 2, 16, 256, 2, 128, 24, 64
+    x = rng.standard_normal((B, S, Dm), dtype=np.float32)
+    mod = (rng.standard_normal((B, 3, Dm)) * 0.5).astype(np.float32)
+    ctx = rng.standard_normal((1, Sk, C), dtype=np.float32) if cross else None
+    kin = C if cross else Dm
+    wq, wk, wv = (oracle.f32_to_bf16_bits(rng.standard_normal((H * D, n), dtype=np.float32)
+                                          * 0.05) for n in (Dm, kin, kin))
+    wo = oracle.f32_to_bf16_bits(rng.standard_normal((Dm, H * D), dtype=np.float32) * 0.05)
+    qw, kw = (rng.uniform(0.5, 1.5, D).astype(np.float32) for _ in range(2))
+    f = None if cross else generate_rope_freqs(4, 4)
+    got = oracle.attention_block(x, mod, wq, wk, wv, wo, qw, kw, f, ctx, heads=H, head_dim=D)
+
+    d64 = lambda a: np.asarray(a, np.float64)
+    wf = lambda bits: d64(oracle.bf16_bits_to_f32(bits))
+    xd = d64(x)
+    mu = xd.mean(-1, keepdims=True)
+    xn = (xd - mu) / np.sqrt(((xd - mu) ** 2).mean(-1, keepdims=True) + 1e-6)
+    xm = xn * (1 + d64(mod[:, 1])[:, None]) + d64(mod[:, 0])[:, None]
+    src = np.broadcast_to(d64(ctx), (B, Sk, C)) if cross else xm
+    q = (xm @ wf(wq).T).reshape(B, S, H, D)
+    k = (src @ wf(wk).T).reshape(B, -1, H, D)
+    v = (src @ wf(wv).T).reshape(B, -1, H, D)
+    q, k = oracle.rmsnorm_fp64(q, qw), oracle.rmsnorm_fp64(k, kw)
+    if not cross:
+        fd = d64(f).reshape(S, D // 2, 2, 2)
+        rot = lambda t: np.concatenate(
+            [fd[None, :, None, :, 0, 0] * t[..., :D // 2] + fd[None, :, None, :, 0, 1] * t[..., D // 2:],
+             fd[None, :, None, :, 1, 0] * t[..., :D // 2] + fd[None, :, None, :, 1, 1] * t[..., D // 2:]],
+            axis=-1)
+        q, k = rot(q), rot(k)
+    qt, kt, vt = (t.transpose(0, 2, 1, 3).reshape(B * H, -1, D) for t in (q, k, v))
+    o = oracle.sdpa_fp64(qt, kt, vt).reshape(B, H, S, D).transpose(0, 2, 1, 3).reshape(B, S, H * D)
+    ref = xd + d64(mod[:, 2])[:, None] * (o @ wf(wo).T)
+    assert np.abs(got - ref).max() < 2e-5 * max(1.0, np.abs(ref).max())

@@ -53,3 +53,11 @@ def test_rmsnorm_rope_gemm_bitwise_vs_reference():
     a = rng.standard_normal((5, 64)).astype(np.float32)
     wb = oracle.f32_to_bf16_bits(rng.standard_normal((9, 64)).astype(np.float32))
     np.testing.assert_array_equal(oracle.gemm_bf16(a, wb), oracle.ref_gemm_bf16(a, wb))
+
+
+def test_layernorm_silu_bitwise_vs_reference():
+    rng = np.random.default_rng(44)
+    x = (rng.standard_normal((33, 2048)) * 5 - 2).astype(np.float32)
+    np.testing.assert_array_equal(oracle.layernorm(x), oracle.ref_layernorm(x))
+    np.testing.assert_array_equal(oracle.layernorm(x[:, :77], 1e-5), oracle.ref_layernorm(x[:, :77], 1e-5))
+    np.testing.assert_array_equal(oracle.silu(x), oracle.ref_silu(x))
