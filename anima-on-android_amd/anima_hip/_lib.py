@@ -37,6 +37,8 @@ SIGNATURES = {
     "anima_hip_attention": (_B, [_P] * 7 + [_I] * 5 + [_F, _I]),
     "anima_hip_gemm_dev": (_B, [_P, ct.c_int64, _P, _I, ct.c_int64, _P, ct.c_int64] + [_I] * 3
                            + [_P]),
+    "anima_hip_attention_block_scratch_bytes": (ct.c_size_t, [_P] + [_I] * 6),
+    "anima_hip_attention_block_dev": (_B, [_P] * 10 + [_I] * 5 + [_F, _I, _P, ct.c_size_t, _P]),
     "anima_hip_linear_scratch_bytes": (ct.c_size_t, [_I, _I, _I]),
     "anima_hip_linear_dev": (_B, [_P, ct.c_int64, _P, ct.c_int64, _P, ct.c_int64] + [_I] * 4
                              + [_P, ct.c_size_t, _P]),

@@ -754,6 +754,67 @@ void anima_hip_ctx_kv_destroy(anima_hip_ctx_kv *kv)
     delete kv;
 }
 
+size_t anima_hip_attention_block_scratch_bytes(const anima_hip_ctx_kv *kv, int B, int S, int Dm,
+                                               int H, int D, int mode)
+{
+    if (B < 0 || S < 0 || Dm < 0 || H < 0 || D < 0)
+        return 0;
+    if (kv)
+        return attention_block_scratch_bytes(B, S, Dm, kv->H, kv->D, kv->Bc, kv->S_kv,
+                                             kv->mode == ANIMA_HIP_BF16, true);
+    return attention_block_scratch_bytes(B, S, Dm, H, D, B, S, mode == ANIMA_HIP_BF16, false);
+}
+
+bool anima_hip_attention_block_dev(float *x, const float *mod, const uint16_t *wq,
+                                   const uint16_t *wk, const uint16_t *wv, const uint16_t *wo,
+                                   const float *q_norm_w, const float *k_norm_w,
+                                   const float *freqs, const anima_hip_ctx_kv *kv, int B, int S,
+                                   int Dm, int H, int D, float eps, int mode, void *scratch,
+                                   size_t scratch_bytes, void *stream)
+{
+    if (!ready_for_device_call())
+        return false;
+    if (!check_dims(B, H, S, S, D) || Dm < 0)
+        return fail("attention_block_dev: negative dimension");
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16)
+        return fail("attention_block_dev: unknown mode " + std::to_string(mode));
+    BlockProblem p;
+    p.x = x;
+    p.mod = mod;
+    p.wq = wq;
+    p.wk = wk;
+    p.wv = wv;
+    p.wo = wo;
+    p.q_norm_w = q_norm_w;
+    p.k_norm_w = k_norm_w;
+    p.freqs = freqs;
+    p.B = B;
+    p.S = S;
+    p.Dm = Dm;
+    p.H = H;
+    p.D = D;
+    p.eps = eps;
+    p.bf16 = mode == ANIMA_HIP_BF16;
+    if (kv) {
+        int dev = 0;
+        if (!hip_ok(hipGetDevice(&dev), "hipGetDevice"))
+            return false;
+        if (dev != kv->device)
+            return fail("attention_block_dev: the context cache lives on another device");
+        if (kv->H != H || kv->D != D || kv->mode != mode)
+            return fail("attention_block_dev: heads, head dim and mode must match the context cache");
+        if (kv->Bc != 1 && kv->Bc != B)
+            return fail("attention_block_dev: the context batch must be 1 or B");
+        p.k_prep = kv->k;
+        p.v_prep = kv->v;
+        p.Bk = kv->Bc;
+        p.S_kv = kv->S_kv;
+    } else if (freqs && !S) {
+        return true;
+    }
+    return run_attention_block(p, scratch, scratch_bytes, pick_stream(stream));
+}
+
 size_t anima_hip_cross_attention_scratch_bytes(const anima_hip_ctx_kv *kv, int B, int S_q)
 {
     if (!kv || B < 0 || S_q < 0)

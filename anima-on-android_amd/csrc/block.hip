@@ -1,0 +1,305 @@
+// One attention sub-block of a DiT block on the device-resident residual
+// stream, NumpyBlock.forward (anima_rt/scripts/numpy_dit.py:236-247):
+//   x_n = layernorm(x)                       (anima_rt_run_layernorm, eps 1e-6)
+//   x_m = x_n * (1 + scale[b]) + shift[b]    (AdaLN modulation)
+//   a   = NumpyAttention(x_m [, ctx])        (projections, q/k RMSNorm, RoPE, SDPA)
+//   x   = x + gate[b] * output_proj(a)
+// with (shift, scale, gate) the three chunks of the block's AdaLN output
+// (numpy_dit.py:218-228).  x stays in HBM across calls: the host sees
+// nothing between the blocks of a denoise step.
+//
+// Kernels here:
+//   ln_modulate_kernel  one wave per row: mean and variance by wave
+//                       reductions (two passes over registers), then the
+//                       modulated row written directly as the bf16 terms
+//                       (hi, and lo in f32 mode) that the projection GEMM
+//                       consumes, so no separate split pass runs;
+//   gate_residual_kernel x += gate[b] * y, float4 per thread.
+// The LayerNorm statistics are summed in a different order than the
+// reference's serial Welford pass (layernorm_kernel.h:13-33), so x_n agrees
+// to float32 rounding (~1e-7 relative), not bit for bit; the products
+// and sums after it round like numpy's float32 expressions.
+#include "common.h"
+
+#include <cmath>
+
+#pragma clang fp contract(off)
+
+namespace anima_hip {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+size_t round_up256(size_t n) { return (n + 255) / 256 * 256; }
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        v += __shfl_xor(v, off);
+    return v;
+}
+
+__device__ __forceinline__ unsigned int pack_pair(float x, float y)
+{
+    return __builtin_bit_cast(unsigned int, __builtin_convertvector(f32x2{x, y}, bf16x2));
+}
+
+struct LnArgs {
+    const float *x;
+    int64_t ldx;
+    const float *mod;  // [B][3][Dm]: shift, scale, gate
+    unsigned int *hi, *lo;  // [M][kp] bf16 (addressed as pairs); lo may be null
+    int64_t kp;
+    int64_t M;
+    int S, Dm;
+    float eps;
+};
+
+// Row r of batch entry r / S.  VPL float4 per lane cover Dm <= 256 * VPL.
+template <int VPL>
+__global__ __launch_bounds__(256) void ln_modulate_kernel(LnArgs a)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = int64_t(blockIdx.x) * 4 + wave;
+    if (row >= a.M)
+        return;  // whole wave
+    const int b = int(row / a.S);
+    const float *x = a.x + row * a.ldx;
+    const int n4 = a.Dm >> 2;
+    f32x4 v[VPL];
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int c = lane + 64 * i;
+        v[i] = c < n4 ? *reinterpret_cast<const f32x4 *>(x + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+        sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    const float mean = wave_sum(sum) / float(a.Dm);
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        if (lane + 64 * i < n4) {
+            const f32x4 d = v[i] - mean;
+            sq += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+        }
+    }
+    const float rstd = 1.0f / sqrtf(wave_sum(sq) / float(a.Dm) + a.eps);
+    const float *shift = a.mod + int64_t(b) * 3 * a.Dm;
+    const float *scale = shift + a.Dm;
+    unsigned int *hrow = a.hi + row * (a.kp >> 1);
+    unsigned int *lrow = a.lo ? a.lo + row * (a.kp >> 1) : nullptr;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int c = lane + 64 * i;
+        if (c < n4) {
+            const f32x4 sc = *reinterpret_cast<const f32x4 *>(scale + 4 * c);
+            const f32x4 sh = *reinterpret_cast<const f32x4 *>(shift + 4 * c);
+            const f32x4 xn = (v[i] - mean) * rstd;
+            const f32x4 y = xn * (1.0f + sc) + sh;
+            const unsigned int h0 = pack_pair(y.x, y.y), h1 = pack_pair(y.z, y.w);
+            *reinterpret_cast<uint2 *>(hrow + 2 * c) = uint2{h0, h1};
+            if (lrow) {
+                // y - hi is exact in f32 (hi holds the leading bits of y).
+                const float r0 = y.x - __uint_as_float(h0 << 16);
+                const float r1 = y.y - __uint_as_float(h0 & 0xFFFF0000u);
+                const float r2 = y.z - __uint_as_float(h1 << 16);
+                const float r3 = y.w - __uint_as_float(h1 & 0xFFFF0000u);
+                *reinterpret_cast<uint2 *>(lrow + 2 * c) = uint2{pack_pair(r0, r1), pack_pair(r2, r3)};
+            }
+        }
+    }
+    // Dm % 8 == 4: the last four elements of the padded row are zero.
+    if ((a.Dm & 7) == 4 && lane == 0) {
+        *reinterpret_cast<uint2 *>(hrow + 2 * n4) = uint2{0u, 0u};
+        if (lrow)
+            *reinterpret_cast<uint2 *>(lrow + 2 * n4) = uint2{0u, 0u};
+    }
+}
+
+struct ResidualArgs {
+    float *x;
+    const float *y;
+    const float *mod;
+    int64_t n4;  // M * Dm / 4
+    int S, Dm;
+};
+
+__global__ __launch_bounds__(256) void gate_residual_kernel(ResidualArgs a)
+{
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= a.n4)
+        return;
+    const int64_t e = 4 * i;
+    const int64_t row = e / a.Dm;
+    const int d = int(e - row * a.Dm);
+    const int b = int(row / a.S);
+    const f32x4 g = *reinterpret_cast<const f32x4 *>(a.mod + (int64_t(b) * 3 + 2) * a.Dm + d);
+    const f32x4 y = *reinterpret_cast<const f32x4 *>(a.y + e);
+    f32x4 &x = *reinterpret_cast<f32x4 *>(a.x + e);
+    x = x + g * y;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Scratch regions of one sub-block, 256-byte aligned, in order.
+struct BlockScratch {
+    size_t terms, q, k, v, o, y, attn, lin, total;
+};
+
+BlockScratch block_scratch(int B, int S, int Dm, int H, int D, int Bk, int S_kv, bool bf16,
+                           bool cross)
+{
+    const size_t M = size_t(B) * S, HD = size_t(H) * D;
+    BlockScratch s{};
+    s.terms = round_up256(M * size_t(linear_terms_ld(Dm)) * 2) * (bf16 ? 1 : 2);
+    s.q = round_up256(M * HD * 4);
+    s.k = cross ? 0 : s.q;
+    s.v = cross ? 0 : s.q;
+    s.o = s.q;
+    s.y = round_up256(M * size_t(Dm) * 4);
+    s.attn = round_up256(attention_scratch_bytes(B, S, Bk, S_kv, H, D, bf16, cross));
+    s.lin = round_up256(linear_scratch_bytes(int(M), int(HD), !bf16));
+    s.total = s.terms + s.q + s.k + s.v + s.o + s.y + s.attn + s.lin;
+    return s;
+}
+
+}  // namespace
+
+size_t attention_block_scratch_bytes(int B, int S, int Dm, int H, int D, int Bk, int S_kv,
+                                     bool bf16, bool cross)
+{
+    return block_scratch(B, S, Dm, H, D, Bk, S_kv, bf16, cross).total;
+}
+
+bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, uint16_t *hi, uint16_t *lo,
+                        int64_t M, int S, int Dm, float eps, hipStream_t st)
+{
+    if (M == 0)
+        return true;
+    if (Dm <= 0 || Dm % 4 || Dm > 256 * 16 || S <= 0)
+        return fail("ln_modulate: the model width must be a positive multiple of 4, at most 4096");
+    if (!aligned16(x) || ldx % 4 || !aligned16(mod) || !aligned16(hi) || !aligned16(lo))
+        return fail("ln_modulate: operands must be 16-byte aligned");
+    LnArgs a;
+    a.x = x;
+    a.ldx = ldx;
+    a.mod = mod;
+    a.hi = reinterpret_cast<unsigned int *>(hi);
+    a.lo = reinterpret_cast<unsigned int *>(lo);
+    a.kp = linear_terms_ld(Dm);
+    a.M = M;
+    a.S = S;
+    a.Dm = Dm;
+    a.eps = eps;
+    const int64_t nblk = (M + 3) / 4;
+    if (nblk > INT32_MAX)
+        return fail("ln_modulate: too many rows");
+    const int vpl = (Dm + 255) / 256;
+    if (vpl <= 1)
+        hipLaunchKernelGGL(ln_modulate_kernel<1>, dim3(unsigned(nblk)), dim3(256), 0, st, a);
+    else if (vpl <= 2)
+        hipLaunchKernelGGL(ln_modulate_kernel<2>, dim3(unsigned(nblk)), dim3(256), 0, st, a);
+    else if (vpl <= 4)
+        hipLaunchKernelGGL(ln_modulate_kernel<4>, dim3(unsigned(nblk)), dim3(256), 0, st, a);
+    else if (vpl <= 8)
+        hipLaunchKernelGGL(ln_modulate_kernel<8>, dim3(unsigned(nblk)), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL(ln_modulate_kernel<16>, dim3(unsigned(nblk)), dim3(256), 0, st, a);
+    return hip_ok(hipGetLastError(), "ln_modulate_kernel launch");
+}
+
+bool launch_gate_residual(float *x, const float *y, const float *mod, int64_t M, int S, int Dm,
+                          hipStream_t st)
+{
+    if (M == 0)
+        return true;
+    if (Dm % 4 || !aligned16(x) || !aligned16(y) || !aligned16(mod))
+        return fail("gate_residual: rows must be 16-byte aligned multiples of 4");
+    ResidualArgs a;
+    a.x = x;
+    a.y = y;
+    a.mod = mod;
+    a.n4 = M * Dm / 4;
+    a.S = S;
+    a.Dm = Dm;
+    const int64_t nblk = (a.n4 + 255) / 256;
+    if (nblk > INT32_MAX)
+        return fail("gate_residual: too many elements");
+    hipLaunchKernelGGL(gate_residual_kernel, dim3(unsigned(nblk)), dim3(256), 0, st, a);
+    return hip_ok(hipGetLastError(), "gate_residual_kernel launch");
+}
+
+bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_bytes, hipStream_t st)
+{
+    const int B = p.B, S = p.S, Dm = p.Dm, H = p.H, D = p.D;
+    const bool cross = p.k_prep != nullptr;
+    const int64_t M = int64_t(B) * S;
+    const int HD = H * D;
+    if (M == 0)
+        return true;
+    if (Dm % 8 || HD % 8)
+        return fail("attention_block: the model width and H*D must be multiples of 8");
+    if (!p.x || !p.mod || !p.wq || !p.wo || (!cross && (!p.wk || !p.wv)))
+        return fail("attention_block: null pointer");
+    const BlockScratch s = block_scratch(B, S, Dm, H, D, cross ? p.Bk : B, cross ? p.S_kv : S,
+                                         p.bf16, cross);
+    if (!scratch || scratch_bytes < s.total || !aligned16(scratch))
+        return fail("attention_block: scratch smaller than the size query or not 16-byte aligned");
+    char *cur = static_cast<char *>(scratch);
+    auto take = [&](size_t n) {
+        char *r = cur;
+        cur += n;
+        return r;
+    };
+    uint16_t *hi = reinterpret_cast<uint16_t *>(take(s.terms));
+    uint16_t *lo = p.bf16 ? nullptr : hi + (s.terms / 2) / sizeof(uint16_t);
+    float *q = reinterpret_cast<float *>(take(s.q));
+    float *k = reinterpret_cast<float *>(take(s.k));
+    float *v = reinterpret_cast<float *>(take(s.v));
+    float *o = reinterpret_cast<float *>(take(s.o));
+    float *y = reinterpret_cast<float *>(take(s.y));
+    void *attn = take(s.attn);
+    void *lin = take(s.lin);
+
+    // x_m as bf16 terms, then the projections of NumpyAttention.forward
+    // (numpy_dit.py:273-281): q from x_m, and k/v from x_m (self) or the
+    // cached context projections (cross).
+    if (!launch_ln_modulate(p.x, Dm, p.mod, hi, lo, M, S, Dm, p.eps, st))
+        return false;
+    if (!launch_linear_terms(hi, lo, p.wq, Dm, q, HD, int(M), HD, Dm, st))
+        return false;
+    if (!cross && (!launch_linear_terms(hi, lo, p.wk, Dm, k, HD, int(M), HD, Dm, st) ||
+                   !launch_linear_terms(hi, lo, p.wv, Dm, v, HD, int(M), HD, Dm, st)))
+        return false;
+
+    AttnInputs in;
+    in.q = q;
+    in.q_norm_w = p.q_norm_w;
+    in.freqs = cross ? nullptr : p.freqs;
+    in.k = k;
+    in.v = v;
+    in.k_norm_w = p.k_norm_w;
+    in.k_prep = p.k_prep;
+    in.v_prep = p.v_prep;
+    in.out = o;
+    in.B = B;
+    in.Bk = cross ? p.Bk : B;
+    in.S_q = S;
+    in.S_kv = cross ? p.S_kv : S;
+    in.H = H;
+    in.D = D;
+    in.eps = p.eps;
+    in.bf16 = p.bf16;
+    if (!run_attention(in, attn, st))
+        return false;
+
+    // output_proj (numpy_dit.py:294-296) and the gated residual.
+    if (!launch_linear(o, HD, p.wo, HD, y, Dm, int(M), Dm, HD, !p.bf16, lin, s.lin, st))
+        return false;
+    return launch_gate_residual(p.x, y, p.mod, M, S, Dm, st);
+}
+
+}  // namespace anima_hip

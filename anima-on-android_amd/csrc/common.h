@@ -109,6 +109,14 @@ bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, 
                    int64_t ldc, int M, int N, int K, bool exact, void *scratch,
                    size_t scratch_bytes, hipStream_t st);
 
+// The same product on A already split into bf16 terms hi (and lo, or null for
+// one term), rows of linear_terms_ld(K) elements zero-padded past K.
+int64_t linear_terms_ld(int K);
+bool linear_terms_supported(int M, int N, int K, const void *w, int64_t ldw, const float *c,
+                            int64_t ldc);
+bool launch_linear_terms(const uint16_t *hi, const uint16_t *lo, const uint16_t *w, int64_t ldw,
+                         float *c, int64_t ldc, int M, int N, int K, hipStream_t st);
+
 // Per-row RMSNorm (+ optional RoPE) "prologue".
 //   x:   rows indexed (b, s, h) through `xs` (D contiguous), f32
 //   out: same indexing through `os`, f32 or bf16 (out_bf16)
@@ -152,5 +160,32 @@ bool prepare_kv(const float *k, const float *v, const float *k_norm_w, const flo
                 void *k_out, void *v_out, int Bk, int S_kv, int H, int D, float eps, bool bf16,
                 hipStream_t st);
 bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st);
+
+// ---- Attention sub-block of a DiT block on the resident residual stream
+// (block.hip): x += gate[b] * output_proj(attention(LN(x)*(1+scale[b]) +
+// shift[b])).  mod is [B][3][Dm] = (shift, scale, gate).  Self-attention when
+// k_prep is null (q/k/v projections of the modulated x, RoPE with freqs);
+// cross-attention over a prepared context cache otherwise (wk/wv unused).
+struct BlockProblem {
+    float *x = nullptr;         // [B*S, Dm] f32, updated in place
+    const float *mod = nullptr;
+    const uint16_t *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;  // bf16 [out, in]
+    const float *q_norm_w = nullptr, *k_norm_w = nullptr, *freqs = nullptr;
+    const void *k_prep = nullptr, *v_prep = nullptr;  // context cache (cross-attention)
+    int Bk = 0, S_kv = 0;
+    int B = 0, S = 0, Dm = 0, H = 0, D = 0;
+    float eps = 1e-6f;
+    bool bf16 = false;
+};
+size_t attention_block_scratch_bytes(int B, int S, int Dm, int H, int D, int Bk, int S_kv,
+                                     bool bf16, bool cross);
+bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_bytes, hipStream_t st);
+// LayerNorm (no affine) + AdaLN modulation of rows of x, written as the bf16
+// terms (hi, and lo unless null) of the projection GEMM's input.
+bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, uint16_t *hi, uint16_t *lo,
+                        int64_t M, int S, int Dm, float eps, hipStream_t st);
+// x += gate[b] * y for rows of S per batch entry.
+bool launch_gate_residual(float *x, const float *y, const float *mod, int64_t M, int S, int Dm,
+                          hipStream_t st);
 
 }  // namespace anima_hip

@@ -167,6 +167,32 @@ bool lt_matmul(LtPlan *p, const void *w, const void *a, float *c, float beta, hi
 
 }  // namespace
 
+int64_t linear_terms_ld(int K) { return padded_k(K); }
+
+bool linear_terms_supported(int M, int N, int K, const void *w, int64_t ldw, const float *c,
+                            int64_t ldc)
+{
+    if (M <= 0 || N <= 0 || K <= 0 || ldw < K || ldc < N || (ldw % 8) != 0 || (ldc % 4) != 0 ||
+        (reinterpret_cast<uintptr_t>(w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(c) & 15u) != 0)
+        return false;
+    std::lock_guard<std::mutex> g(g_lt_mu);
+    return lt_plan(M, N, K, padded_k(K), ldw, ldc) != nullptr;
+}
+
+bool launch_linear_terms(const uint16_t *hi, const uint16_t *lo, const uint16_t *w, int64_t ldw,
+                         float *c, int64_t ldc, int M, int N, int K, hipStream_t st)
+{
+    if (!linear_terms_supported(M, N, K, w, ldw, c, ldc))
+        return fail("linear: no bf16 GEMM for this shape");
+    if ((reinterpret_cast<uintptr_t>(hi) & 15u) != 0 || (reinterpret_cast<uintptr_t>(lo) & 15u) != 0)
+        return fail("linear: bf16 terms must be 16-byte aligned");
+    std::lock_guard<std::mutex> g(g_lt_mu);
+    LtPlan *plan = lt_plan(M, N, K, padded_k(K), ldw, ldc);
+    if (!lt_matmul(plan, w, hi, c, 0.0f, st))
+        return false;
+    return !lo || lt_matmul(plan, w, lo, c, 1.0f, st);
+}
+
 size_t linear_scratch_bytes(int M, int K, bool exact)
 {
     if (M <= 0 || K <= 0)

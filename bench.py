@@ -272,7 +272,7 @@ def other_configs(c, cpu_rate):
 
         res["c4_denoise_step_28_blocks"] = denoise_step(c, mode)
         res["proj_gemm_8192x2048x2048"] = projection_gemm(c, mode)
-        res["c4_denoise_step_28_blocks_with_projections"] = denoise_step_with_projections(c, mode)
+        res["c4_denoise_step_28_blocks_attention_sublayers"] = denoise_step_blocks(c, mode)
         out[variant] = res
         log(f"[bench] configs {variant}: " + json.dumps(res))
     if cpu_rate:
@@ -357,58 +357,55 @@ def projection_gemm(c, mode, M=8192, N=2048, K=2048):
             "note": "algorithmic 2*M*N*K; the f32 mode issues two bf16 products (hi + lo terms)"}
 
 
-def denoise_step_with_projections(c, mode, blocks=28, B=2, S=4096, H=16, D=128):
-    """The denoise step's attention blocks with their projections, as
-    NumpyAttention.forward runs them (numpy_dit.py:268-297): per block
-    q/k/v_proj -> self-attention -> output_proj, then cross q_proj ->
-    cached cross-attention -> output_proj.  Seeded per-block bf16 weights
-    ~N(0,0.02) and per-block hidden states ~N(0,1); context K/V caches are
-    built once per block outside the step."""
+def denoise_step_blocks(c, mode, blocks=28, B=2, S=4096, H=16, D=128, Dm=2048):
+    """The attention sub-layers of one denoise step, as NumpyBlock.forward
+    runs them (numpy_dit.py:236-247), on one device-resident residual stream
+    x [B*S, Dm]: per block a self-attention sub-block and a cross-attention
+    sub-block, each LayerNorm -> AdaLN modulate -> projections -> attention
+    -> output_proj -> gated residual (anima_hip_attention_block_dev).
+    Seeded per-block bf16 weights ~N(0,0.02) and modulation vectors; the
+    per-block context K/V caches are built once, outside the step."""
     torch, lib, _lib = c.torch, c.lib, c._lib
     from anima_hip.rope import generate_rope_freqs
-    M, C = B * S, H * D
+    M, HD = B * S, H * D
     freqs = torch.from_numpy(generate_rope_freqs(64, 64)).to(c.dev)
     ones = torch.ones(D, device=c.dev)
     caches = [context_cache(c, mode, 2, 4000 + i) for i in range(blocks)]
-    xs = [c.randn((M, C), 20000 + i) for i in range(blocks)]
-    ws = [[c.bf16_bits(c.randn((C, C), 30000 + 6 * i + j, 0.02)) for j in range(6)]
-          for i in range(blocks)]
-    q, k, v, o, y = (torch.empty((M, C), device=c.dev) for _ in range(5))
-    lin = Linear(c, mode, M, C)
-    n_self = lib.anima_hip_attention_scratch_bytes(B, S, B, S, H, D, mode)
-    n_x = lib.anima_hip_cross_attention_scratch_bytes(caches[0].handle, B, S)
+    x = c.randn((M, Dm), 20000)
+    mods = [[c.randn((B, 3, Dm), 21000 + 2 * i + j, 0.5) for j in range(2)] for i in range(blocks)]
+    ws = [[c.bf16_bits(c.randn((HD, Dm) if j < 4 else (Dm, HD), 30000 + 6 * i + j, 0.02))
+           for j in range(6)] for i in range(blocks)]
+    n_self = lib.anima_hip_attention_block_scratch_bytes(None, B, S, Dm, H, D, mode)
+    n_x = lib.anima_hip_attention_block_scratch_bytes(caches[0].handle, B, S, Dm, H, D, mode)
     scratch = torch.empty(max(n_self, n_x), dtype=torch.uint8, device=c.dev)
     eps = ct.c_float(1e-6)
 
     def step():
         for i in range(blocks):
-            x, (wq, wk, wv, wo, wqx, wox) = xs[i], ws[i]
-            lin(x, wq, q)
-            lin(x, wk, k)
-            lin(x, wv, v)
-            _lib.check(lib.anima_hip_attention_dev(q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                                   ones.data_ptr(), ones.data_ptr(),
-                                                   freqs.data_ptr(), o.data_ptr(),
-                                                   scratch.data_ptr(), n_self, B, S, B, S, H, D,
-                                                   eps, mode, c.stp), "attention_dev")
-            lin(o, wo, y)
-            lin(x, wqx, q)
-            _lib.check(lib.anima_hip_cross_attention_dev(q.data_ptr(), ones.data_ptr(),
-                                                         caches[i].handle, o.data_ptr(),
-                                                         scratch.data_ptr(), n_x, B, S, eps,
-                                                         c.stp), "cross_attention_dev")
-            lin(o, wox, y)
-    ms = c.time(step, 3, 1)
+            (wq, wk, wv, wqx, wo, wox), (ms, mx) = ws[i], mods[i]
+            _lib.check(lib.anima_hip_attention_block_dev(
+                x.data_ptr(), ms.data_ptr(), wq.data_ptr(), wk.data_ptr(), wv.data_ptr(),
+                wo.data_ptr(), ones.data_ptr(), ones.data_ptr(), freqs.data_ptr(), None, B, S, Dm,
+                H, D, eps, mode, scratch.data_ptr(), n_self, c.stp), "attention_block_dev")
+            _lib.check(lib.anima_hip_attention_block_dev(
+                x.data_ptr(), mx.data_ptr(), wqx.data_ptr(), None, None, wox.data_ptr(),
+                ones.data_ptr(), ones.data_ptr(), None, caches[i].handle, B, S, Dm, H, D, eps,
+                mode, scratch.data_ptr(), n_x, c.stp), "attention_block_dev (cross)")
+    ms_step = c.time(step, 3, 1)
+    if not torch.isfinite(x).all():
+        raise RuntimeError("non-finite residual stream")
     attn = blocks * 4.0 * B * H * S * D * (S + 512)
-    proj = blocks * 6 * 2.0 * M * C * C
+    proj = blocks * 6 * 2.0 * M * Dm * HD
     for cache in caches:
         cache.close()
-    del xs, ws
+    del ws, mods
     torch.cuda.empty_cache()
-    return {"ms_per_step": round(ms, 3), "tflops": round((attn + proj) / ms / 1e9, 2),
+    return {"ms_per_step": round(ms_step, 3), "tflops": round((attn + proj) / ms_step / 1e9, 2),
             "flops_per_step": attn + proj, "projection_flops_per_step": proj,
-            "includes": "per block: q/k/v_proj, q/k prologues, flash self-attention, output_proj; "
-                        "cross q_proj, q prologue, cached cross-attention, output_proj"}
+            "includes": "per block, self and cross: LayerNorm + AdaLN modulate (written as the "
+                        "projection's bf16 terms), q(/k/v)_proj, q/k RMSNorm+RoPE, flash attention "
+                        "(cross: cached context K/V), output_proj, gated residual into the "
+                        "resident stream"}
 
 
 def cpu_baseline(qn, kn, v, B, H, S, D, heads):

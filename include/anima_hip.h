@@ -222,6 +222,31 @@ bool anima_hip_cross_attention_dev(const float *q, const float *q_norm_w,
                                    const anima_hip_ctx_kv *kv, float *out, void *scratch,
                                    size_t scratch_bytes, int B, int S_q, float eps, void *stream);
 
+/* One attention sub-block of a DiT block on the device-resident residual
+ * stream (NumpyBlock.forward, anima_rt/scripts/numpy_dit.py:236-247):
+ *   x += gate[b] * output_proj(attention(layernorm(x) * (1 + scale[b]) + shift[b]))
+ * x: [B*S, Dm] f32, updated in place; mod: [B][3][Dm] f32 = (shift, scale,
+ * gate), the three chunks of the block's AdaLN output (numpy_dit.py:218-228);
+ * wq/wk/wv: [H*D, Dm], wo: [Dm, H*D] bf16 bit patterns like the reference's
+ * weights.  kv == NULL: self-attention (k/v from the modulated x, RoPE with
+ * freqs [S, D/2, 2, 2] or NULL).  kv != NULL: cross-attention over that
+ * context cache (wk, wv, k_norm_w and freqs unused; H, D and mode must match
+ * the cache).  LayerNorm has no affine parameters, as the reference calls it.
+ * mode ANIMA_HIP_F32: projections on exact hi+lo bf16 terms and the f32
+ * attention path; ANIMA_HIP_BF16: bf16 activations throughout.  Dm and H*D
+ * must be multiples of 8, Dm <= 4096.  scratch: device memory of
+ * anima_hip_attention_block_scratch_bytes(kv, B, S, Dm, H, D, mode) bytes,
+ * 16-byte aligned; nothing is allocated.  Asynchronous on `stream`. */
+size_t anima_hip_attention_block_scratch_bytes(const anima_hip_ctx_kv *kv, int B, int S, int Dm,
+                                               int H, int D, int mode);
+bool anima_hip_attention_block_dev(float *x, const float *mod, const uint16_t *wq,
+                                   const uint16_t *wk, const uint16_t *wv, const uint16_t *wo,
+                                   const float *q_norm_w, const float *k_norm_w,
+                                   const float *freqs, const anima_hip_ctx_kv *kv, int B, int S,
+                                   int Dm, int H, int D, float eps, int mode, void *scratch,
+                                   size_t scratch_bytes, void *stream);
+
+
 #ifdef __cplusplus
 }
 #endif
