@@ -39,6 +39,12 @@ SIGNATURES = {
                            + [_P]),
     "anima_hip_attention_block_scratch_bytes": (ct.c_size_t, [_P] + [_I] * 6),
     "anima_hip_attention_block_dev": (_B, [_P] * 10 + [_I] * 5 + [_F, _I, _P, ct.c_size_t, _P]),
+    "anima_hip_weights_open": (_P, [ct.c_char_p]),
+    "anima_hip_weights_close": (None, [_P]),
+    "anima_hip_weights_count": (_I, [_P]),
+    "anima_hip_weights_name": (ct.c_char_p, [_P, _I]),
+    "anima_hip_weights_info": (_I, [_P, ct.c_char_p, ct.POINTER(_I), _I64P, _I]),
+    "anima_hip_weights_device": (_P, [_P, ct.c_char_p, _I]),
     "anima_hip_linear_scratch_bytes": (ct.c_size_t, [_I, _I, _I]),
     "anima_hip_linear_dev": (_B, [_P, ct.c_int64, _P, ct.c_int64, _P, ct.c_int64] + [_I] * 4
                              + [_P, ct.c_size_t, _P]),

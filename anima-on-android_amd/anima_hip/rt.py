@@ -160,6 +160,79 @@ def gemm_bf16(a, w_bits) -> np.ndarray:
     return c
 
 
+DTYPES = {0: "F32", 1: "F16", 2: "BF16"}
+
+
+class Weights:
+    """A model file in the reference's safetensors format
+    (scripts/phone_pipeline_nd.py:15-43), memory-mapped and validated by the
+    library.  ``device(name)`` uploads a tensor once and returns its device
+    pointer, resident until ``close()``: BF16 linear weights as bit patterns
+    (the form ``anima_hip_linear_dev`` takes), or widened to f32 with
+    ``as_f32=True`` (what the reference does for its norm weights).  Names
+    match with or without the reference's ``net.`` prefix."""
+
+    def __init__(self, path):
+        self._lib = _lib.load()
+        h = self._lib.anima_hip_weights_open(str(path).encode())
+        if not h:
+            raise _lib.AnimaHipError(f"anima_hip_weights_open failed: {_lib.last_error()}")
+        self._h = h
+
+    @property
+    def handle(self):
+        return self._h
+
+    def names(self) -> list:
+        n = self._lib.anima_hip_weights_count(self._h)
+        return [self._lib.anima_hip_weights_name(self._h, i).decode() for i in range(n)]
+
+    def info(self, name):
+        """(dtype string, shape tuple) of a tensor."""
+        dt = ct.c_int()
+        shape = (ct.c_int64 * 8)()
+        nd = self._lib.anima_hip_weights_info(self._h, name.encode(), ct.byref(dt), shape, 8)
+        if nd < 0:
+            raise KeyError(name)
+        return DTYPES[dt.value], tuple(shape[i] for i in range(min(nd, 8)))
+
+    def device(self, name, as_f32=False) -> int:
+        p = self._lib.anima_hip_weights_device(self._h, name.encode(), int(bool(as_f32)))
+        if not p:
+            raise _lib.AnimaHipError(f"anima_hip_weights_device({name}) failed: "
+                                     f"{_lib.last_error()}")
+        return p
+
+    def close(self):
+        if self._h:
+            self._lib.anima_hip_weights_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def load_context(path) -> np.ndarray:
+    """Text-context embeddings as the reference stores them
+    (context_cond.npy / context_uncond.npy, phone_pipeline_nd.py:79-85):
+    float32 [batch, tokens, 1024].  Loaded without pickle support."""
+    ctx = np.load(path, allow_pickle=False)
+    if ctx.ndim == 2:
+        ctx = ctx[None]
+    if ctx.ndim != 3:
+        raise ValueError(f"context {path}: expected [batch, tokens, dim], got {ctx.shape}")
+    return np.ascontiguousarray(ctx, dtype=np.float32)
+
+
 class ContextKV:
     """Cross-attention K/V of one text context, kept on the GPU
     (anima_hip_ctx_kv_create).  K = RMSNorm_head(ctx . Wk^T), V = ctx . Wv^T,

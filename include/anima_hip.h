@@ -247,6 +247,32 @@ bool anima_hip_attention_block_dev(float *x, const float *mod, const uint16_t *w
                                    size_t scratch_bytes, void *stream);
 
 
+/* ---- Model weights in the reference's on-disk format (safetensors) ----
+ * The file the reference loads at scripts/phone_pipeline_nd.py:15-43 (read in
+ * C++ by vulkan/safetensors_reader.h): u64 header length, JSON header of
+ * {name: {dtype, shape, data_offsets}}, raw data.  Opened read-only and
+ * memory-mapped; the header is validated (offsets inside the file, byte
+ * counts matching dtype and shape).  Names match with or without the
+ * reference's "net." prefix.  dtype codes: 0 = F32, 1 = F16, 2 = BF16 (the
+ * codes of the reference's vk_weight_add, phone_pipeline_nd.py:31). */
+typedef struct anima_hip_weights anima_hip_weights;
+/* NULL on error (anima_hip_last_error() says why). */
+anima_hip_weights *anima_hip_weights_open(const char *path);
+/* Frees the device copies (after draining the device) and unmaps the file. */
+void anima_hip_weights_close(anima_hip_weights *w);
+int anima_hip_weights_count(const anima_hip_weights *w);
+/* Name of tensor i without the "net." prefix; NULL when out of range. */
+const char *anima_hip_weights_name(const anima_hip_weights *w, int i);
+/* dtype code and up to max_ndim dimensions of a tensor; returns its rank,
+ * or -1 when absent. */
+int anima_hip_weights_info(const anima_hip_weights *w, const char *name, int *dtype,
+                           int64_t *shape, int max_ndim);
+/* Device copy of a tensor, uploaded on first request and resident until
+ * close: as stored (as_f32 == 0; BF16 linear weights stay bit patterns, the
+ * form anima_hip_linear_dev takes) or widened to f32 (BF16 bits << 16, F16
+ * converted, as the reference widens its norm weights).  NULL on error. */
+const void *anima_hip_weights_device(anima_hip_weights *w, const char *name, int as_f32);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,7 +57,8 @@ def _ctype_of(c):
     import ctypes as ct
     c = c.replace("const ", "").strip()
     if c.endswith("*"):
-        return "int64*" if c.startswith("int64_t") else "ptr"
+        base = c[:-1].strip()
+        return {"int64_t": "int64*", "int": "int*", "char": "char*"}.get(base, "ptr")
     return {"bool": ct.c_bool, "int": ct.c_int, "float": ct.c_float, "size_t": ct.c_size_t,
             "int64_t": ct.c_int64, "void": None}[c]
 
@@ -75,10 +76,14 @@ def test_ctypes_declarations_match_header_prototypes():
                 assert py is ct.c_void_p, f"{name} arg {i}: {c}"
             elif want == "int64*":
                 assert py is ct.POINTER(ct.c_int64), f"{name} arg {i}: {c}"
+            elif want == "int*":
+                assert py is ct.POINTER(ct.c_int), f"{name} arg {i}: {c}"
+            elif want == "char*":
+                assert py is ct.c_char_p, f"{name} arg {i}: {c}"
             else:
                 assert py is want, f"{name} arg {i}: {c} vs {py}"
         rwant = _ctype_of(ret)
-        if rwant == "ptr":
+        if rwant in ("ptr", "char*"):
             assert res in (ct.c_void_p, ct.c_char_p), name
         else:
             assert res is rwant, f"{name} return {ret} vs {res}"
