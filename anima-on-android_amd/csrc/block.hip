@@ -296,7 +296,15 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
     if (!run_attention(in, attn, st))
         return false;
 
-    // output_proj (numpy_dit.py:294-296) and the gated residual.
+    // output_proj (numpy_dit.py:294-296) and the gated residual.  bf16 mode:
+    // one GEMM per batch entry whose per-channel scale is the gate and whose
+    // C and D are the residual stream.  f32 mode (two terms, each pass would
+    // read and write the residual again), or a shape the library GEMM does
+    // not take with a per-channel scale: the projection into y, then a
+    // residual pass.
+    if (p.bf16 && linear_residual_supported(S, Dm, HD, p.wo, HD, p.x, Dm))
+        return launch_linear_residual(o, HD, p.wo, HD, p.x, Dm, p.mod + 2 * int64_t(Dm),
+                                      3 * int64_t(Dm), B, S, Dm, HD, lin, s.lin, st);
     if (!launch_linear(o, HD, p.wo, HD, y, Dm, int(M), Dm, HD, !p.bf16, lin, s.lin, st))
         return false;
     return launch_gate_residual(p.x, y, p.mod, M, S, Dm, st);

@@ -117,6 +117,18 @@ bool linear_terms_supported(int M, int N, int K, const void *w, int64_t ldw, con
 bool launch_linear_terms(const uint16_t *hi, const uint16_t *lo, const uint16_t *w, int64_t ldw,
                          float *c, int64_t ldc, int M, int N, int K, hipStream_t st);
 
+// x[b*S + s, :] += gate[b*gate_stride + :] (.) (bf16(a[b*S + s, :]) . W^T) for
+// b < B: the output projection fused with the gated residual of a DiT block
+// (the gate scales the N output channels).  Activations round to bf16 (the hi
+// term of launch_linear; scratch: linear_scratch_bytes(B*S, K, false));
+// linear_residual_supported says whether the library GEMM takes this shape
+// with a per-channel scale.
+bool linear_residual_supported(int S, int N, int K, const void *w, int64_t ldw, const float *x,
+                               int64_t ldx);
+bool launch_linear_residual(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *x,
+                            int64_t ldx, const float *gate, int64_t gate_stride, int B, int S, int N,
+                            int K, void *scratch, size_t scratch_bytes, hipStream_t st);
+
 // Per-row RMSNorm (+ optional RoPE) "prologue".
 //   x:   rows indexed (b, s, h) through `xs` (D contiguous), f32
 //   out: same indexing through `os`, f32 or bf16 (out_bf16)

@@ -98,13 +98,16 @@ struct LtPlan {
 
 struct LtDevice {
     hipblasLtHandle_t handle = nullptr;
-    std::map<std::tuple<int, int, int, int64_t, int64_t, int64_t>, std::unique_ptr<LtPlan>> plans;
+    std::map<std::tuple<int, int, int, int64_t, int64_t, int64_t, bool>, std::unique_ptr<LtPlan>>
+        plans;
 };
 
 std::mutex g_lt_mu;
 std::map<int, std::unique_ptr<LtDevice>> g_lt;
 
-LtPlan *lt_plan(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc)
+// alpha_vec: alpha is a device vector over the N output channels (the rows of
+// the column-major product), beta a host scalar.
+LtPlan *lt_plan(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool alpha_vec = false)
 {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess)
@@ -119,12 +122,14 @@ LtPlan *lt_plan(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc)
     }
     if (!slot->handle)
         return nullptr;
-    auto &pp = slot->plans[std::make_tuple(M, N, K, lda, ldw, ldc)];
+    auto &pp = slot->plans[std::make_tuple(M, N, K, lda, ldw, ldc, alpha_vec)];
     if (pp)
         return pp->ok ? pp.get() : nullptr;
     pp.reset(new LtPlan);
     LtPlan &p = *pp;
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    const int32_t pmode = alpha_vec ? HIPBLASLT_POINTER_MODE_ALPHA_DEVICE_VECTOR_BETA_HOST
+                                    : HIPBLASLT_POINTER_MODE_HOST;
     uint64_t ws = 0;
     hipblasLtMatmulPreference_t pref = nullptr;
     hipblasLtMatmulHeuristicResult_t res[1];
@@ -135,6 +140,8 @@ LtPlan *lt_plan(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc)
             HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) ==
             HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_POINTER_MODE, &pmode,
+                                        sizeof(pmode)) == HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatrixLayoutCreate(&p.lw, HIP_R_16BF, K, N, ldw) == HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, M, lda) == HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc) == HIPBLAS_STATUS_SUCCESS &&
@@ -153,12 +160,14 @@ LtPlan *lt_plan(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc)
     return p.ok ? &p : nullptr;
 }
 
-bool lt_matmul(LtPlan *p, const void *w, const void *a, float *c, float beta, hipStream_t st)
+bool lt_matmul(LtPlan *p, const void *w, const void *a, float *c, float beta, hipStream_t st,
+               const float *alpha_vec = nullptr)
 {
     int dev = 0;
     (void)hipGetDevice(&dev);
     const float alpha = 1.0f;
-    const hipblasStatus_t s = hipblasLtMatmul(g_lt[dev]->handle, p->desc, &alpha, w, p->lw, a, p->la,
+    const void *ap = alpha_vec ? static_cast<const void *>(alpha_vec) : &alpha;
+    const hipblasStatus_t s = hipblasLtMatmul(g_lt[dev]->handle, p->desc, ap, w, p->lw, a, p->la,
                                               &beta, c, p->lc, c, p->lc, &p->algo, nullptr, 0, st);
     if (s != HIPBLAS_STATUS_SUCCESS)
         return fail("linear: hipblasLtMatmul failed with status " + std::to_string(int(s)));
@@ -244,6 +253,60 @@ bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, 
     if (!lt_matmul(plan, w, s.hi, c, 0.0f, st))
         return false;
     return !exact || lt_matmul(plan, w, s.lo, c, 1.0f, st);
+}
+
+bool linear_residual_supported(int S, int N, int K, const void *w, int64_t ldw, const float *x,
+                               int64_t ldx)
+{
+    if (S <= 0 || N <= 0 || K <= 0 || ldw < K || ldx < N || (ldw % 8) != 0 || (ldx % 4) != 0 ||
+        (reinterpret_cast<uintptr_t>(w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(x) & 15u) != 0)
+        return false;
+    std::lock_guard<std::mutex> g(g_lt_mu);
+    return lt_plan(S, N, K, padded_k(K), ldw, ldx, true) != nullptr;
+}
+
+bool launch_linear_residual(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *x,
+                            int64_t ldx, const float *gate, int64_t gate_stride, int B, int S, int N,
+                            int K, void *scratch, size_t scratch_bytes, hipStream_t st)
+{
+    if (int64_t(B) * S * N == 0)
+        return true;
+    if (!linear_residual_supported(S, N, K, w, ldw, x, ldx))
+        return fail("linear_residual: no bf16 GEMM with a per-channel scale for this shape");
+    if ((reinterpret_cast<uintptr_t>(gate) & 3u) != 0)
+        return fail("linear_residual: misaligned gate");
+    const int M = B * S;
+    const int64_t kp = padded_k(K);
+    if (!scratch || scratch_bytes < linear_scratch_bytes(M, K, false) ||
+        (reinterpret_cast<uintptr_t>(scratch) & 15u) != 0)
+        return fail("linear_residual: scratch smaller than linear_scratch_bytes()");
+    SplitArgs sa;
+    sa.a = a;
+    sa.lda = lda;
+    sa.hi = static_cast<unsigned int *>(scratch);
+    sa.lo = nullptr;
+    sa.kp = kp;
+    sa.M = M;
+    sa.K = K;
+    sa.vec = (reinterpret_cast<uintptr_t>(a) & 15u) == 0 && lda % 4 == 0;
+    sa.total = int64_t(M) * kp / 8;
+    const int64_t nblk = (sa.total + 255) / 256;
+    if (nblk > INT32_MAX)
+        return fail("linear_residual: problem too large for one launch");
+    hipLaunchKernelGGL(split_kernel, dim3(unsigned(nblk)), dim3(256), 0, st, sa);
+    if (!hip_ok(hipGetLastError(), "split_kernel launch"))
+        return false;
+    std::lock_guard<std::mutex> g(g_lt_mu);
+    LtPlan *plan = lt_plan(S, N, K, kp, ldw, ldx, true);
+    // Per batch entry b: x_b = gate_b (.) (a_b W^T) + x_b, gate over the N
+    // output channels.
+    for (int b = 0; b < B; ++b) {
+        const int64_t r0 = int64_t(b) * S;
+        const uint16_t *hb = reinterpret_cast<const uint16_t *>(sa.hi) + r0 * kp;
+        if (!lt_matmul(plan, w, hb, x + r0 * ldx, 1.0f, st, gate + int64_t(b) * gate_stride))
+            return false;
+    }
+    return true;
 }
 
 }  // namespace anima_hip

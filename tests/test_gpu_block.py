@@ -19,7 +19,7 @@ from anima_hip.rope import generate_rope_freqs
 
 pytestmark = pytest.mark.gpu
 
-B, S, DM, H, D = 1, 256, 2048, 16, 128
+S, DM, H, D = 256, 2048, 16, 128
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -31,7 +31,7 @@ def _weights(rng, n_out, n_in):
     return oracle.f32_to_bf16_bits(rng.standard_normal((n_out, n_in), dtype=np.float32) * 0.02)
 
 
-def _inputs(seed):
+def _inputs(seed, B):
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((B, S, DM), dtype=np.float32)
     mod = (rng.standard_normal((B, 3, DM)) * 0.5).astype(np.float32)
@@ -43,6 +43,7 @@ def _inputs(seed):
 def _run_block(x, mod, w, qw, kw, freqs, kv, mode):
     from devmem import DevBuf
     lib = _lib.load()
+    B = x.shape[0]
     bufs = {name: DevBuf.of(a) for name, a in
             (("x", x), ("mod", mod), ("wq", w[0]), ("wk", w[1]), ("wv", w[2]), ("wo", w[3]),
              ("qw", qw), ("kw", kw))}
@@ -67,23 +68,26 @@ def _check(out, ref, x, mode):
     assert err <= (1e-4 if mode == rt.F32 else 2e-2)
 
 
+# B=2: the gate and the residual rows differ per batch entry.
+@pytest.mark.parametrize("B", [1, 2])
 @pytest.mark.parametrize("mode", [rt.F32, rt.BF16])
-def test_self_attention_block(mode):
-    rng, x, mod, w, qw, kw = _inputs(606 + mode)
+def test_self_attention_block(mode, B):
+    rng, x, mod, w, qw, kw = _inputs(606 + mode + 10 * B, B)
     f = generate_rope_freqs(16, 16)
-    print(f"self-attention block mode={mode}", flush=True)
+    print(f"self-attention block mode={mode} B={B}", flush=True)
     out = _run_block(x, mod, w, qw, kw, f, None, mode)
     ref = oracle.attention_block(x, mod, *w, qw, kw, f, None, heads=H, head_dim=D,
                                  sdpa=lambda a, b, c: oracle.flash_sdpa(a, b, c, threads=8))
     _check(out, ref, x, mode)
 
 
+@pytest.mark.parametrize("B", [1, 2])
 @pytest.mark.parametrize("mode", [rt.F32, rt.BF16])
-def test_cross_attention_block(mode):
-    rng, x, mod, w, qw, kw = _inputs(707 + mode)
-    ctx = (rng.standard_normal((1, 512, 1024)) * 0.5).astype(np.float32)
+def test_cross_attention_block(mode, B):
+    rng, x, mod, w, qw, kw = _inputs(707 + mode + 10 * B, B)
+    ctx = (rng.standard_normal((B, 512, 1024)) * 0.5).astype(np.float32)
     wk, wv = _weights(rng, H * D, 1024), _weights(rng, H * D, 1024)
-    print(f"cross-attention block mode={mode}", flush=True)
+    print(f"cross-attention block mode={mode} B={B}", flush=True)
     kv = rt.ContextKV(ctx, wk, wv, kw, heads=H, head_dim=D, mode=mode)
     try:
         out = _run_block(x, mod, [w[0], wk, wv, w[3]], qw, kw, None, kv, mode)
