@@ -50,6 +50,18 @@ SIGNATURES = {
                              + [_P, ct.c_size_t, _P]),
     "anima_hip_attention_scratch_bytes": (ct.c_size_t, [_I] * 7),
     "anima_hip_attention_dev": (_B, [_P] * 8 + [ct.c_size_t] + [_I] * 6 + [_F, _I, _P]),
+    "anima_hip_dit_default_config": (None, [_P]),
+    "anima_hip_dit_create": (_P, [_P, _P, _P, ct.POINTER(_I), _I64P, _I, _I]),
+    "anima_hip_dit_destroy": (None, [_P]),
+    "anima_hip_dit_set_context_dev": (_B, [_P, _P, _I, _I, _P]),
+    "anima_hip_dit_scratch_bytes": (ct.c_size_t, [_P] + [_I] * 4),
+    "anima_hip_dit_forward_dev": (_B, [_P, _P, ct.c_int64, _P] + [_I] * 4
+                                  + [_P, _P, _P, ct.c_size_t, _P]),
+    "anima_hip_dit_euler_dev": (_B, [_P, _P, _P, _I, _F, _I, _I, _P, _P, ct.c_size_t, _P]),
+    "anima_hip_malloc": (_P, [ct.c_size_t]),
+    "anima_hip_free": (None, [_P]),
+    "anima_hip_memcpy": (_B, [_P, _P, ct.c_size_t, _I]),
+    "anima_hip_synchronize": (_B, []),
     "anima_hip_ctx_kv_create": (_P, [_P] * 4 + [_I] * 5 + [_F, _I]),
     "anima_hip_ctx_kv_destroy": (None, [_P]),
     "anima_hip_cross_attention": (_B, [_P] * 4 + [_I] * 2 + [_F]),

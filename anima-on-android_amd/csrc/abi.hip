@@ -99,6 +99,12 @@ bool ready_for_device_call()
     return ensure_ready(r);
 }
 
+}  // namespace
+
+bool device_ready() { return ready_for_device_call(); }
+
+namespace {
+
 // Device entry points run on the caller's stream; NULL is HIP's default
 // (null) stream, as in other HIP libraries.
 hipStream_t pick_stream(void *s) { return static_cast<hipStream_t>(s); }
@@ -889,6 +895,47 @@ bool anima_hip_cross_attention(const float *q, const float *q_norm_w, const anim
         !d2h(out, r.o.p, f32_bytes(nq), st))
         return false;
     return sync(st);
+}
+
+void *anima_hip_malloc(size_t bytes)
+{
+    if (!ready_for_device_call())
+        return nullptr;
+    void *p = nullptr;
+    if (!hip_ok(hipMalloc(&p, std::max<size_t>(bytes, 1)), "hipMalloc"))
+        return nullptr;
+    return p;
+}
+
+void anima_hip_free(void *p)
+{
+    if (p) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(p);
+    }
+}
+
+bool anima_hip_memcpy(void *dst, const void *src, size_t bytes, int kind)
+{
+    if (!ready_for_device_call())
+        return false;
+    const hipMemcpyKind k = kind == 1   ? hipMemcpyHostToDevice
+                            : kind == 2 ? hipMemcpyDeviceToHost
+                            : kind == 3 ? hipMemcpyDeviceToDevice
+                                        : hipMemcpyDefault;
+    if (kind < 1 || kind > 3)
+        return fail("memcpy: kind must be 1, 2 or 3");
+    if (bytes == 0)
+        return true;
+    if (!dst || !src)
+        return fail("memcpy: null pointer");
+    return hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize") &&
+           hip_ok(hipMemcpy(dst, src, bytes, k), "hipMemcpy");
+}
+
+bool anima_hip_synchronize(void)
+{
+    return ready_for_device_call() && hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
 }
 
 }  // extern "C"

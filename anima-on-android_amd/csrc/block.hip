@@ -50,7 +50,8 @@ __device__ __forceinline__ unsigned int pack_pair(float x, float y)
 struct LnArgs {
     const float *x;
     int64_t ldx;
-    const float *mod;  // [B][3][Dm]: shift, scale, gate
+    const float *mod;  // per batch entry b at mod + b*mod_ld: shift [Dm], scale [Dm], ...
+    int64_t mod_ld;
     unsigned int *hi, *lo;  // [M][kp] bf16 (addressed as pairs); lo may be null
     int64_t kp;
     int64_t M;
@@ -87,7 +88,7 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(LnArgs a)
         }
     }
     const float rstd = 1.0f / sqrtf(wave_sum(sq) / float(a.Dm) + a.eps);
-    const float *shift = a.mod + int64_t(b) * 3 * a.Dm;
+    const float *shift = a.mod + int64_t(b) * a.mod_ld;
     const float *scale = shift + a.Dm;
     unsigned int *hrow = a.hi + row * (a.kp >> 1);
     unsigned int *lrow = a.lo ? a.lo + row * (a.kp >> 1) : nullptr;
@@ -174,19 +175,22 @@ size_t attention_block_scratch_bytes(int B, int S, int Dm, int H, int D, int Bk,
     return block_scratch(B, S, Dm, H, D, Bk, S_kv, bf16, cross).total;
 }
 
-bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, uint16_t *hi, uint16_t *lo,
-                        int64_t M, int S, int Dm, float eps, hipStream_t st)
+bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t mod_ld,
+                        uint16_t *hi, uint16_t *lo, int64_t M, int S, int Dm, float eps,
+                        hipStream_t st)
 {
     if (M == 0)
         return true;
     if (Dm <= 0 || Dm % 4 || Dm > 256 * 16 || S <= 0)
         return fail("ln_modulate: the model width must be a positive multiple of 4, at most 4096");
-    if (!aligned16(x) || ldx % 4 || !aligned16(mod) || !aligned16(hi) || !aligned16(lo))
+    if (!aligned16(x) || ldx % 4 || !aligned16(mod) || mod_ld % 4 || !aligned16(hi) ||
+        !aligned16(lo))
         return fail("ln_modulate: operands must be 16-byte aligned");
     LnArgs a;
     a.x = x;
     a.ldx = ldx;
     a.mod = mod;
+    a.mod_ld = mod_ld;
     a.hi = reinterpret_cast<unsigned int *>(hi);
     a.lo = reinterpret_cast<unsigned int *>(lo);
     a.kp = linear_terms_ld(Dm);
@@ -267,7 +271,7 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
     // x_m as bf16 terms, then the projections of NumpyAttention.forward
     // (numpy_dit.py:273-281): q from x_m, and k/v from x_m (self) or the
     // cached context projections (cross).
-    if (!launch_ln_modulate(p.x, Dm, p.mod, hi, lo, M, S, Dm, p.eps, st))
+    if (!launch_ln_modulate(p.x, Dm, p.mod, 3 * int64_t(Dm), hi, lo, M, S, Dm, p.eps, st))
         return false;
     if (!launch_linear_terms(hi, lo, p.wq, Dm, q, HD, int(M), HD, Dm, st))
         return false;

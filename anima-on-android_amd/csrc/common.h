@@ -11,6 +11,9 @@ namespace anima_hip {
 // Record an error message for anima_hip_last_error(); always returns false so
 // callers can `return fail(...)`.
 bool fail(const std::string &msg);
+// The library's device context exists (created on first use); false with the
+// reason recorded otherwise.
+bool device_ready();
 // Check a HIP status; on error record "<what>: <hip error string>".
 bool hip_ok(hipError_t e, const char *what);
 
@@ -128,6 +131,10 @@ bool linear_residual_supported(int S, int N, int K, const void *w, int64_t ldw, 
 bool launch_linear_residual(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *x,
                             int64_t ldx, const float *gate, int64_t gate_stride, int B, int S, int N,
                             int K, void *scratch, size_t scratch_bytes, hipStream_t st);
+// The same on activations already rounded to bf16: rows of linear_terms_ld(K).
+bool launch_linear_residual_terms(const uint16_t *hi, const uint16_t *w, int64_t ldw, float *x,
+                                  int64_t ldx, const float *gate, int64_t gate_stride, int B,
+                                  int S, int N, int K, hipStream_t st);
 
 // Per-row RMSNorm (+ optional RoPE) "prologue".
 //   x:   rows indexed (b, s, h) through `xs` (D contiguous), f32
@@ -193,11 +200,22 @@ size_t attention_block_scratch_bytes(int B, int S, int Dm, int H, int D, int Bk,
                                      bool bf16, bool cross);
 bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_bytes, hipStream_t st);
 // LayerNorm (no affine) + AdaLN modulation of rows of x, written as the bf16
-// terms (hi, and lo unless null) of the projection GEMM's input.
-bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, uint16_t *hi, uint16_t *lo,
-                        int64_t M, int S, int Dm, float eps, hipStream_t st);
+// terms (hi, and lo unless null) of the projection GEMM's input.  Row r
+// belongs to batch entry r / S, whose shift and scale are mod[b*mod_ld + :Dm]
+// and mod[b*mod_ld + Dm : 2*Dm].
+bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t mod_ld,
+                        uint16_t *hi, uint16_t *lo, int64_t M, int S, int Dm, float eps,
+                        hipStream_t st);
 // x += gate[b] * y for rows of S per batch entry.
 bool launch_gate_residual(float *x, const float *y, const float *mod, int64_t M, int S, int Dm,
                           hipStream_t st);
+
+// ---- MLP sub-layer of a DiT block (dit.hip): x += gate[b] * layer2(gelu(
+// layer1(LN(x)*(1+scale[b]) + shift[b]))), mod [B][3][Dm], w1 [hidden][Dm],
+// w2 [Dm][hidden] bf16 bits.
+size_t mlp_block_scratch_bytes(int B, int S, int Dm, int hidden, bool bf16);
+bool run_mlp_block(float *x, const float *mod, const uint16_t *w1, const uint16_t *w2, int B,
+                   int S, int Dm, int hidden, float eps, bool bf16, void *scratch,
+                   size_t scratch_bytes, hipStream_t st);
 
 }  // namespace anima_hip

@@ -1,0 +1,1009 @@
+// The Anima DiT around the attention path, on the device: NumpyDiT.forward
+// (anima_rt/scripts/numpy_dit.py:82-130) with the residual stream resident in
+// HBM from the patch embedding to the final layer, and the Euler flow-match
+// sampler with classifier-free guidance (anima_rt/scripts/sampling.py:115-140)
+// looping on the device.
+//
+// Per forward:
+//   timestep_kernel   _numpy_timesteps (numpy_dit.py:39-46): [cos, sin] of
+//                     sigma * exp(-ln(1e4) i / half), float32 like numpy;
+//   gemv_kernel       every small-batch linear layer: the timestep MLP
+//                     (numpy_dit.py:153-160) and all AdaLN modulation MLPs
+//                     (numpy_dit.py:211-223, 171-180).  Their inputs depend on
+//                     sigma only, so the 28 x 3 + 1 modulations run as two
+//                     launches (first layers, then second layers plus the
+//                     AdaLN-LoRA term) before the blocks;
+//   silu_kernel       anima_rt_run_silu (silu_kernel.h:9-17);
+//   patchify_kernel   _pad_to_patch_size + the zero padding-mask channel +
+//                     _rearrange_patchify (numpy_dit.py:10-22, 92-95),
+//                     written directly as the bf16 terms of the patch GEMM;
+//   blocks            attention sub-layers (block.hip) and the MLP sub-layer
+//                     below: LN + modulate -> layer1 -> GELU -> layer2 ->
+//                     gated residual (numpy_dit.py:249-253, 304-317);
+//   gelu_terms_kernel anima_rt_run_gelu (gelu_kernel.h:13-23, exact erf form)
+//                     fused with the split of its output into GEMM terms;
+//   final layer       LN + modulate (2 chunks) -> linear (numpy_dit.py:186-201);
+//   unpatchify_kernel _rearrange_unpatchify + crop (numpy_dit.py:24-31, 128-129);
+//   cfg_euler_kernel  sampler only: v = v_u + cfg (v_c - v_u), x += v dt.
+// Linear layers over tokens run on hipBLASLt (linear.hip); f32 mode feeds them
+// exact hi + lo bf16 terms of the f32 activations, bf16 mode rounds the
+// activations to bf16.
+#include "common.h"
+
+#include "anima_hip.h"
+
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#pragma clang fp contract(off)
+
+namespace anima_hip {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kMaxBatch = 4;
+constexpr int kPatch = 2;         // spatial patch (ps); one frame per patch (pt = 1)
+constexpr int kAdaHidden = 256;   // hidden width of every AdaLN MLP (numpy_dit.py:176, 216)
+
+size_t round_up256(size_t n) { return (n + 255) / 256 * 256; }
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+__device__ __forceinline__ unsigned int pack_pair(float x, float y)
+{
+    return __builtin_bit_cast(unsigned int, __builtin_convertvector(f32x2{x, y}, bf16x2));
+}
+
+// hi/lo bf16 terms of 8 consecutive values (lo may be null).
+__device__ __forceinline__ void store_terms8(const float (&v)[8], unsigned int *hi,
+                                             unsigned int *lo)
+{
+    unsigned int h[4], l[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        h[e] = pack_pair(v[2 * e], v[2 * e + 1]);
+        // v - hi is exact in f32 (hi holds the leading bits of v).
+        l[e] = pack_pair(v[2 * e] - __uint_as_float(h[e] << 16),
+                         v[2 * e + 1] - __uint_as_float(h[e] & 0xFFFF0000u));
+    }
+    *reinterpret_cast<uint4 *>(hi) = uint4{h[0], h[1], h[2], h[3]};
+    if (lo)
+        *reinterpret_cast<uint4 *>(lo) = uint4{l[0], l[1], l[2], l[3]};
+}
+
+// ---- timestep features -------------------------------------------------
+struct TimestepArgs {
+    float sigma[kMaxBatch];
+    float *out;  // [B][D]
+    int D;
+};
+
+__global__ __launch_bounds__(256) void timestep_kernel(TimestepArgs a)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int b = blockIdx.y;
+    if (i >= a.D)
+        return;
+    const int half = a.D / 2;
+    const int j = i < half ? i : i - half;
+    // exponent = -log(10000) * arange(half, float32) / float(half), in float32.
+    const float e = (-9.21034037197618f * float(j)) / float(half);
+    const float arg = a.sigma[b] * expf(e);
+    a.out[int64_t(b) * a.D + i] = i < half ? cosf(arg) : sinf(arg);
+}
+
+// ---- SiLU: x / (1 + exp(-x)) ----------------------------------------------
+__global__ __launch_bounds__(256) void silu_kernel(const float *x, float *y, int64_t n)
+{
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) {
+        const float v = x[i];
+        y[i] = v / (1.0f + expf(-v));
+    }
+}
+
+// ---- small-batch linear layers -------------------------------------------
+// y[b][n] = sum_k x[b][k] W[n][k] (+ add[b][n]) for b < B <= kMaxBatch, one
+// job per blockIdx.y.  L lanes share an output row: lane lr takes the 16-byte
+// chunks lr, lr + L, ... of W's row, then the L partial sums combine by
+// butterfly.  All jobs of a launch share K (a multiple of 8).
+struct GemvJob {
+    const uint16_t *w;  // [N][K] bf16 bits
+    const float *x;     // row b at x + b*ldx
+    float *y;           // row b at y + b*ldy
+    const float *add;   // row b at add + b*ld_add, or null
+    int64_t ldx, ldy, ld_add;
+    int N;
+};
+
+template <int L>
+__global__ __launch_bounds__(256) void gemv_kernel(const GemvJob *jobs, int B, int K)
+{
+    constexpr int R = 256 / L;
+    const GemvJob j = jobs[blockIdx.y];
+    const int r = threadIdx.x / L, lr = threadIdx.x % L;
+    const int n = blockIdx.x * R + r;
+    if (n >= j.N)
+        return;  // whole L-lane group
+    float acc[kMaxBatch] = {0.f, 0.f, 0.f, 0.f};
+    const uint16_t *wr = j.w + int64_t(n) * K;
+    for (int c = lr; c < K / 8; c += L) {
+        const uint4 wv = *reinterpret_cast<const uint4 *>(wr + 8 * c);
+        const float w8[8] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xFFFF0000u),
+                             __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xFFFF0000u),
+                             __uint_as_float(wv.z << 16), __uint_as_float(wv.z & 0xFFFF0000u),
+                             __uint_as_float(wv.w << 16), __uint_as_float(wv.w & 0xFFFF0000u)};
+#pragma unroll
+        for (int b = 0; b < kMaxBatch; ++b) {
+            if (b < B) {
+                const float *xb = j.x + b * j.ldx + 8 * c;
+                const f32x4 x0 = *reinterpret_cast<const f32x4 *>(xb);
+                const f32x4 x1 = *reinterpret_cast<const f32x4 *>(xb + 4);
+                acc[b] += ((w8[0] * x0.x + w8[1] * x0.y) + (w8[2] * x0.z + w8[3] * x0.w)) +
+                          ((w8[4] * x1.x + w8[5] * x1.y) + (w8[6] * x1.z + w8[7] * x1.w));
+            }
+        }
+    }
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) {
+#pragma unroll
+        for (int b = 0; b < kMaxBatch; ++b)
+            acc[b] += __shfl_xor(acc[b], off);
+    }
+    if (lr == 0) {
+#pragma unroll
+        for (int b = 0; b < kMaxBatch; ++b) {
+            if (b < B)
+                j.y[b * j.ldy + n] = acc[b] + (j.add ? j.add[b * j.ld_add + n] : 0.0f);
+        }
+    }
+}
+
+// ---- GELU, written as GEMM terms ------------------------------------------
+// g = x * 0.5 * (1 + erf(x / sqrt(2))) of h [M][N] (N % 8 == 0) into hi/lo
+// rows of N bf16.
+struct GeluArgs {
+    const float *h;
+    unsigned int *hi, *lo;
+    int64_t n8;  // M * N / 8
+};
+
+__global__ __launch_bounds__(256) void gelu_terms_kernel(GeluArgs a)
+{
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= a.n8)
+        return;
+    const f32x4 u = *reinterpret_cast<const f32x4 *>(a.h + 8 * i);
+    const f32x4 w = *reinterpret_cast<const f32x4 *>(a.h + 8 * i + 4);
+    const float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+    float g[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        g[e] = x[e] * 0.5f * (1.0f + erff(x[e] * 0.70710678118654752440f));
+    store_terms8(g, a.hi + 4 * i, a.lo ? a.lo + 4 * i : nullptr);
+}
+
+// ---- patch embedding input ------------------------------------------------
+// Token m = ((b*T + t)*Hp + h)*Wp + w, feature k = ch*4 + 2*dy + dx (ch < C
+// latent channels, ch == C the zero padding-mask channel), value
+// x[b][ch][t][2h+dy][2w+dx], zero past the unpadded Hi x Wi.  Rows of kp
+// (padded K) bf16 terms.
+struct PatchArgs {
+    const float *x;
+    int64_t xb;  // batch stride of x (0: every batch entry reads entry 0)
+    unsigned int *hi, *lo;
+    int64_t kp, M;
+    int C, T, Hi, Wi, Hp, Wp, K;
+};
+
+__global__ __launch_bounds__(256) void patchify_kernel(PatchArgs a)
+{
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t chunks = a.kp / 8;
+    if (i >= a.M * chunks)
+        return;
+    const int64_t m = i / chunks;
+    const int k0 = int(i - m * chunks) * 8;
+    const int w = int(m % a.Wp);
+    const int h = int((m / a.Wp) % a.Hp);
+    const int t = int((m / (int64_t(a.Wp) * a.Hp)) % a.T);
+    const int b = int(m / (int64_t(a.Wp) * a.Hp * a.T));
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int k = k0 + e;
+        const int ch = k >> 2, y = 2 * h + ((k >> 1) & 1), xx = 2 * w + (k & 1);
+        v[e] = (k < a.K && ch < a.C && y < a.Hi && xx < a.Wi)
+                   ? a.x[b * a.xb + ((int64_t(ch) * a.T + t) * a.Hi + y) * a.Wi + xx]
+                   : 0.0f;
+    }
+    store_terms8(v, a.hi + (m * a.kp + k0) / 2, a.lo ? a.lo + (m * a.kp + k0) / 2 : nullptr);
+}
+
+// ---- final-layer output -----------------------------------------------------
+// out[b][c][t][y][x] = f[token(b, t, y/2, x/2)][((y%2)*2 + x%2)*Cout + c],
+// cropped to Hi x Wi.
+struct UnpatchArgs {
+    const float *f;
+    float *out;
+    int64_t n;  // B*Cout*T*Hi*Wi
+    int Cout, T, Hi, Wi, Hp, Wp;
+};
+
+__global__ __launch_bounds__(256) void unpatchify_kernel(UnpatchArgs a)
+{
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= a.n)
+        return;
+    const int x = int(i % a.Wi);
+    const int y = int((i / a.Wi) % a.Hi);
+    const int t = int((i / (int64_t(a.Wi) * a.Hi)) % a.T);
+    const int64_t bc = i / (int64_t(a.Wi) * a.Hi * a.T);
+    const int c = int(bc % a.Cout);
+    const int b = int(bc / a.Cout);
+    const int64_t m = ((int64_t(b) * a.T + t) * a.Hp + (y >> 1)) * a.Wp + (x >> 1);
+    a.out[i] = a.f[m * 4 * a.Cout + ((y & 1) * 2 + (x & 1)) * a.Cout + c];
+}
+
+// Sampler update of the latent x [C][Hi][Wi] from the two CFG branches'
+// final-layer rows (batch entry 0 unconditional, 1 conditional).
+struct EulerArgs {
+    const float *f;
+    float *x;
+    int64_t n, S;  // C*Hi*Wi; tokens per branch
+    int Cout, Hi, Wi, Wp;
+    float cfg, dt;
+};
+
+__global__ __launch_bounds__(256) void cfg_euler_kernel(EulerArgs a)
+{
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= a.n)
+        return;
+    const int x = int(i % a.Wi);
+    const int y = int((i / a.Wi) % a.Hi);
+    const int c = int(i / (int64_t(a.Wi) * a.Hi));
+    const int64_t m = int64_t(y >> 1) * a.Wp + (x >> 1);
+    const int col = ((y & 1) * 2 + (x & 1)) * a.Cout + c;
+    const float vu = a.f[m * 4 * a.Cout + col];
+    const float vc = a.f[(a.S + m) * 4 * a.Cout + col];
+    const float v = vu + a.cfg * (vc - vu);
+    a.x[i] = a.x[i] + v * a.dt;
+}
+
+// bf16 bit patterns -> f32 (the reference's widening of norm weights).
+__global__ __launch_bounds__(256) void widen_kernel(const uint16_t *in, float *out, int64_t n)
+{
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n)
+        out[i] = __uint_as_float(uint32_t(in[i]) << 16);
+}
+
+unsigned grid1(int64_t n) { return unsigned((n + 255) / 256); }
+
+bool launch_silu(const float *x, float *y, int64_t n, hipStream_t st)
+{
+    if (n == 0)
+        return true;
+    hipLaunchKernelGGL(silu_kernel, dim3(grid1(n)), dim3(256), 0, st, x, y, n);
+    return hip_ok(hipGetLastError(), "silu_kernel launch");
+}
+
+bool launch_gemv(const GemvJob *jobs, int njobs, int maxN, int B, int K, hipStream_t st)
+{
+    if (njobs == 0)
+        return true;
+    if (K % 8 || B < 1 || B > kMaxBatch)
+        return fail("gemv: K must be a multiple of 8 and the batch at most 4");
+    const int L = K >= 512 ? 64 : K >= 256 ? 32 : K >= 128 ? 16 : 8;
+    const unsigned gx = unsigned((int64_t(maxN) * L + 255) / 256);
+    const dim3 grid(gx, unsigned(njobs));
+    switch (L) {
+    case 64: hipLaunchKernelGGL(gemv_kernel<64>, grid, dim3(256), 0, st, jobs, B, K); break;
+    case 32: hipLaunchKernelGGL(gemv_kernel<32>, grid, dim3(256), 0, st, jobs, B, K); break;
+    case 16: hipLaunchKernelGGL(gemv_kernel<16>, grid, dim3(256), 0, st, jobs, B, K); break;
+    default: hipLaunchKernelGGL(gemv_kernel<8>, grid, dim3(256), 0, st, jobs, B, K); break;
+    }
+    return hip_ok(hipGetLastError(), "gemv_kernel launch");
+}
+
+// Scratch regions of the MLP sub-layer, 256-byte aligned, in order.
+struct MlpScratch {
+    size_t terms, h, g, y, total;
+};
+
+MlpScratch mlp_scratch(int64_t M, int Dm, int hidden, bool bf16)
+{
+    MlpScratch s{};
+    s.terms = round_up256(size_t(M) * size_t(linear_terms_ld(Dm)) * 2) * (bf16 ? 1 : 2);
+    s.h = round_up256(size_t(M) * hidden * 4);
+    s.g = round_up256(size_t(M) * size_t(linear_terms_ld(hidden)) * 2) * (bf16 ? 1 : 2);
+    s.y = round_up256(size_t(M) * Dm * 4);
+    s.total = s.terms + s.h + s.g + s.y;
+    return s;
+}
+
+}  // namespace
+
+size_t mlp_block_scratch_bytes(int B, int S, int Dm, int hidden, bool bf16)
+{
+    return mlp_scratch(int64_t(B) * S, Dm, hidden, bf16).total;
+}
+
+// The MLP sub-layer of NumpyBlock.forward (numpy_dit.py:249-253) with
+// NumpyMLP (numpy_dit.py:304-317): x += gate[b] * layer2(gelu(layer1(
+// layernorm(x) * (1 + scale[b]) + shift[b]))), mod [B][3][Dm].
+bool run_mlp_block(float *x, const float *mod, const uint16_t *w1, const uint16_t *w2, int B,
+                   int S, int Dm, int hidden, float eps, bool bf16, void *scratch,
+                   size_t scratch_bytes, hipStream_t st)
+{
+    const int64_t M = int64_t(B) * S;
+    if (M == 0)
+        return true;
+    if (Dm % 8 || hidden % 8)
+        return fail("mlp_block: the model width and the hidden width must be multiples of 8");
+    if (!x || !mod || !w1 || !w2)
+        return fail("mlp_block: null pointer");
+    const MlpScratch s = mlp_scratch(M, Dm, hidden, bf16);
+    if (!scratch || scratch_bytes < s.total || !aligned16(scratch))
+        return fail("mlp_block: scratch smaller than the size query or not 16-byte aligned");
+    char *cur = static_cast<char *>(scratch);
+    auto take = [&](size_t n) {
+        char *r = cur;
+        cur += n;
+        return r;
+    };
+    uint16_t *hi = reinterpret_cast<uint16_t *>(take(s.terms));
+    uint16_t *lo = bf16 ? nullptr : hi + (s.terms / 2) / sizeof(uint16_t);
+    float *h = reinterpret_cast<float *>(take(s.h));
+    uint16_t *ghi = reinterpret_cast<uint16_t *>(take(s.g));
+    uint16_t *glo = bf16 ? nullptr : ghi + (s.g / 2) / sizeof(uint16_t);
+    float *y = reinterpret_cast<float *>(take(s.y));
+
+    if (!launch_ln_modulate(x, Dm, mod, 3 * int64_t(Dm), hi, lo, M, S, Dm, eps, st) ||
+        !launch_linear_terms(hi, lo, w1, Dm, h, hidden, int(M), hidden, Dm, st))
+        return false;
+    GeluArgs ga;
+    ga.h = h;
+    ga.hi = reinterpret_cast<unsigned int *>(ghi);
+    ga.lo = reinterpret_cast<unsigned int *>(glo);
+    ga.n8 = M * hidden / 8;
+    hipLaunchKernelGGL(gelu_terms_kernel, dim3(grid1(ga.n8)), dim3(256), 0, st, ga);
+    if (!hip_ok(hipGetLastError(), "gelu_terms_kernel launch"))
+        return false;
+    // layer2 and the gated residual: fused in bf16 mode (see block.hip).
+    if (bf16 && linear_residual_supported(S, Dm, hidden, w2, hidden, x, Dm))
+        return launch_linear_residual_terms(ghi, w2, hidden, x, Dm, mod + 2 * int64_t(Dm),
+                                            3 * int64_t(Dm), B, S, Dm, hidden, st);
+    if (!launch_linear_terms(ghi, glo, w2, hidden, y, Dm, int(M), Dm, hidden, st))
+        return false;
+    return launch_gate_residual(x, y, mod, M, S, Dm, st);
+}
+
+}  // namespace anima_hip
+
+using namespace anima_hip;
+
+namespace {
+
+struct BlockWeights {
+    const uint16_t *sa_q = nullptr, *sa_k = nullptr, *sa_v = nullptr, *sa_o = nullptr;
+    const uint16_t *cx_q = nullptr, *cx_k = nullptr, *cx_v = nullptr, *cx_o = nullptr;
+    const uint16_t *fc1 = nullptr, *fc2 = nullptr;
+    const float *sa_qn = nullptr, *sa_kn = nullptr, *cx_qn = nullptr, *cx_kn = nullptr;
+    const uint16_t *ada1[3] = {nullptr, nullptr, nullptr}, *ada2[3] = {nullptr, nullptr, nullptr};
+    void *ctx_k = nullptr, *ctx_v = nullptr;  // cross-attention cache (owned)
+};
+
+}  // namespace
+
+struct anima_hip_dit {
+    anima_hip_dit_config cfg{};
+    bool bf16 = false;
+    int device = 0;
+    std::vector<BlockWeights> blk;
+    const uint16_t *x_emb = nullptr;  // [D][kp_in] zero-padded copy (owned)
+    const uint16_t *t1 = nullptr, *t2 = nullptr;
+    const float *t_norm = nullptr;
+    const uint16_t *fin_ada1 = nullptr, *fin_ada2 = nullptr, *fin_lin = nullptr;
+    int kp_in = 0;                    // padded patch feature count
+    // Per-forward vectors (sized for cfg.max_batch), owned.
+    float *feat = nullptr, *h1 = nullptr, *h1s = nullptr, *emb = nullptr, *semb = nullptr;
+    float *lora = nullptr, *m1 = nullptr, *mods = nullptr;
+    GemvJob *jobs = nullptr;          // device table: t1, t2, layer-1 x n_ada, layer-2 x n_ada
+    int n_ada = 0;
+    std::vector<void *> owned;        // device allocations freed at destroy
+    // Context cache state.
+    int ctx_B = 0, ctx_S = 0;
+    void *ctx_work = nullptr;
+    size_t ctx_work_bytes = 0;
+};
+
+namespace {
+
+void dit_free(anima_hip_dit *d)
+{
+    if (!d)
+        return;
+    (void)hipDeviceSynchronize();
+    for (void *p : d->owned)
+        (void)hipFree(p);
+    for (auto &b : d->blk) {
+        if (b.ctx_k)
+            (void)hipFree(b.ctx_k);
+        if (b.ctx_v)
+            (void)hipFree(b.ctx_v);
+    }
+    if (d->ctx_work)
+        (void)hipFree(d->ctx_work);
+    delete d;
+}
+
+template <typename T>
+bool dev_alloc(anima_hip_dit *d, T *&p, size_t bytes, const char *what)
+{
+    void *v = nullptr;
+    if (!hip_ok(hipMalloc(&v, std::max<size_t>(bytes, 256)), what))
+        return false;
+    d->owned.push_back(v);
+    p = static_cast<T *>(v);
+    return true;
+}
+
+std::string strip_net(const char *n)
+{
+    std::string s(n ? n : "");
+    if (s.rfind("net.", 0) == 0)
+        s = s.substr(4);
+    return s;
+}
+
+// Token count of one batch entry and the patch grid of a T x H x W latent.
+void grid_of(int T, int H, int W, int &Hp, int &Wp, int64_t &S)
+{
+    Hp = (H + kPatch - 1) / kPatch;
+    Wp = (W + kPatch - 1) / kPatch;
+    S = int64_t(T) * Hp * Wp;
+}
+
+// Scratch regions of one forward, 256-byte aligned, in order.
+struct DitScratch {
+    size_t x, patch, f, arena, total;
+};
+
+DitScratch dit_scratch(const anima_hip_dit *d, int B, int64_t S)
+{
+    const anima_hip_dit_config &c = d->cfg;
+    const int64_t M = int64_t(B) * S;
+    const bool bf16 = d->bf16;
+    DitScratch s{};
+    s.x = round_up256(size_t(M) * c.dim * 4);
+    s.patch = round_up256(size_t(M) * d->kp_in * 2) * 2;
+    s.f = round_up256(size_t(M) * 4 * c.out_channels * 4);
+    size_t arena = attention_block_scratch_bytes(B, int(S), c.dim, c.heads, c.head_dim, B, int(S),
+                                                 bf16, false);
+    arena = std::max(arena, attention_block_scratch_bytes(B, int(S), c.dim, c.heads, c.head_dim,
+                                                          std::max(d->ctx_B, 1),
+                                                          std::max(d->ctx_S, 1), bf16, true));
+    arena = std::max(arena, mlp_block_scratch_bytes(B, int(S), c.dim, c.mlp_hidden, bf16));
+    arena = std::max(arena, round_up256(size_t(M) * linear_terms_ld(c.dim) * 2) * 2);
+    s.arena = round_up256(arena);
+    s.total = s.x + s.patch + s.f + s.arena;
+    return s;
+}
+
+bool check_cfg(const anima_hip_dit_config &c)
+{
+    if (c.dim <= 0 || c.dim % 8 || c.dim > 4096 || c.blocks < 0 || c.heads <= 0 ||
+        c.head_dim <= 0 || (c.heads * c.head_dim) % 8 || c.mlp_hidden <= 0 ||
+        c.mlp_hidden % 8 || c.ctx_dim <= 0 || c.ctx_dim % 8 || c.in_channels <= 0 ||
+        c.out_channels <= 0 || c.max_batch < 1 || c.max_batch > kMaxBatch)
+        return fail("dit: invalid configuration (widths multiples of 8, model width <= 4096, "
+                    "max_batch 1..4)");
+    return true;
+}
+
+// The forward pass on B batch entries of the latent x ([B][C][T][H][W] with
+// batch stride xb) at noise levels sigma[B]; the final layer's token rows land
+// in the `f` region of the scratch (returned through f_out).
+bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, int B, int T,
+             int H, int W, const float *freqs, void *scratch, size_t scratch_bytes,
+             hipStream_t st, float **f_out)
+{
+    const anima_hip_dit_config &c = d->cfg;
+    if (B < 1 || B > c.max_batch)
+        return fail("dit: batch must be in 1..max_batch");
+    if (T <= 0 || H <= 0 || W <= 0)
+        return fail("dit: latent dimensions must be positive");
+    if (!x || !sigma || (!freqs && c.blocks > 0))
+        return fail("dit: null pointer");
+    if (c.blocks > 0 && !d->blk[0].ctx_k)
+        return fail("dit: no text context set (anima_hip_dit_set_context_dev)");
+    if (d->ctx_B != 1 && d->ctx_B != B && c.blocks > 0)
+        return fail("dit: the context batch must be 1 or the forward batch");
+    int Hp, Wp;
+    int64_t S;
+    grid_of(T, H, W, Hp, Wp, S);
+    const int64_t M = int64_t(B) * S;
+    if (M > INT32_MAX / 8)
+        return fail("dit: too many tokens");
+    const DitScratch s = dit_scratch(d, B, S);
+    if (!scratch || scratch_bytes < s.total || !aligned16(scratch))
+        return fail("dit: scratch smaller than anima_hip_dit_scratch_bytes() or not 16-byte "
+                    "aligned");
+    char *base = static_cast<char *>(scratch);
+    float *xr = reinterpret_cast<float *>(base);
+    uint16_t *phi = reinterpret_cast<uint16_t *>(base + s.x);
+    uint16_t *plo = d->bf16 ? nullptr : phi + (s.patch / 2) / 2;
+    float *f = reinterpret_cast<float *>(base + s.x + s.patch);
+    void *arena = base + s.x + s.patch + s.f;
+    const int D = c.dim;
+
+    // Timestep embedding, its MLP (the AdaLN-LoRA term), the normalised
+    // embedding and every AdaLN modulation of this forward.
+    TimestepArgs ta;
+    for (int b = 0; b < kMaxBatch; ++b)
+        ta.sigma[b] = b < B ? sigma[b] : 0.0f;
+    ta.out = d->feat;
+    ta.D = D;
+    hipLaunchKernelGGL(timestep_kernel, dim3(grid1(D), unsigned(B)), dim3(256), 0, st, ta);
+    if (!hip_ok(hipGetLastError(), "timestep_kernel launch"))
+        return false;
+    RowProblem rp{};
+    rp.x = d->feat;
+    rp.out = d->emb;
+    rp.w = d->t_norm;
+    rp.xs = rp.os = Strides{D, D, D};
+    rp.B = B;
+    rp.S = 1;
+    rp.H = 1;
+    rp.D = D;
+    rp.eps = 1e-6f;
+    rp.norm = true;
+    if (!launch_gemv(d->jobs, 1, D, B, D, st) || !launch_silu(d->h1, d->h1s, int64_t(B) * D, st) ||
+        !launch_gemv(d->jobs + 1, 1, 3 * D, B, D, st) || !launch_rows(rp, st) ||
+        !launch_silu(d->emb, d->semb, int64_t(B) * D, st) ||
+        !launch_gemv(d->jobs + 2, d->n_ada, kAdaHidden, B, D, st) ||
+        !launch_gemv(d->jobs + 2 + d->n_ada, d->n_ada, 3 * D, B, kAdaHidden, st))
+        return false;
+
+    // Patch embedding into the residual stream.
+    PatchArgs pa;
+    pa.x = x;
+    pa.xb = xb;
+    pa.hi = reinterpret_cast<unsigned int *>(phi);
+    pa.lo = reinterpret_cast<unsigned int *>(plo);
+    pa.kp = d->kp_in;
+    pa.M = M;
+    pa.C = c.in_channels;
+    pa.T = T;
+    pa.Hi = H;
+    pa.Wi = W;
+    pa.Hp = Hp;
+    pa.Wp = Wp;
+    pa.K = (c.in_channels + 1) * kPatch * kPatch;
+    hipLaunchKernelGGL(patchify_kernel, dim3(grid1(M * (d->kp_in / 8))), dim3(256), 0, st, pa);
+    if (!hip_ok(hipGetLastError(), "patchify_kernel launch") ||
+        !launch_linear_terms(phi, plo, d->x_emb, d->kp_in, xr, D, int(M), D, d->kp_in, st))
+        return false;
+
+    // The blocks (numpy_dit.py:232-253).
+    const int64_t mod_stride = int64_t(c.max_batch) * 3 * D;  // one modulation's rows
+    for (int i = 0; i < c.blocks; ++i) {
+        const BlockWeights &bw = d->blk[i];
+        BlockProblem p;
+        p.x = xr;
+        p.B = B;
+        p.S = int(S);
+        p.Dm = D;
+        p.H = c.heads;
+        p.D = c.head_dim;
+        p.eps = 1e-6f;
+        p.bf16 = d->bf16;
+        p.mod = d->mods + (3 * i + 0) * mod_stride;
+        p.wq = bw.sa_q;
+        p.wk = bw.sa_k;
+        p.wv = bw.sa_v;
+        p.wo = bw.sa_o;
+        p.q_norm_w = bw.sa_qn;
+        p.k_norm_w = bw.sa_kn;
+        p.freqs = freqs;
+        if (!run_attention_block(p, arena, s.arena, st))
+            return false;
+        p.mod = d->mods + (3 * i + 1) * mod_stride;
+        p.wq = bw.cx_q;
+        p.wk = p.wv = nullptr;
+        p.wo = bw.cx_o;
+        p.q_norm_w = bw.cx_qn;
+        p.k_norm_w = bw.cx_kn;
+        p.freqs = nullptr;
+        p.k_prep = bw.ctx_k;
+        p.v_prep = bw.ctx_v;
+        p.Bk = d->ctx_B;
+        p.S_kv = d->ctx_S;
+        if (!run_attention_block(p, arena, s.arena, st) ||
+            !run_mlp_block(xr, d->mods + (3 * i + 2) * mod_stride, bw.fc1, bw.fc2, B, int(S), D,
+                           c.mlp_hidden, 1e-6f, d->bf16, arena, s.arena, st))
+            return false;
+    }
+
+    // Final layer: LN + modulate (shift, scale) and the output linear.
+    uint16_t *thi = static_cast<uint16_t *>(arena);
+    const size_t tbytes = round_up256(size_t(M) * linear_terms_ld(D) * 2);
+    uint16_t *tlo = d->bf16 ? nullptr : thi + tbytes / 2;
+    const float *fmod = d->mods + int64_t(3 * c.blocks) * mod_stride;
+    if (!launch_ln_modulate(xr, D, fmod, 3 * int64_t(D), thi, tlo, M, int(S), D, 1e-6f, st) ||
+        !launch_linear_terms(thi, tlo, d->fin_lin, D, f, 4 * c.out_channels, int(M),
+                             4 * c.out_channels, D, st))
+        return false;
+    *f_out = f;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+void anima_hip_dit_default_config(anima_hip_dit_config *cfg)
+{
+    if (!cfg)
+        return;
+    cfg->dim = 2048;
+    cfg->blocks = 28;
+    cfg->heads = 16;
+    cfg->head_dim = 128;
+    cfg->mlp_hidden = 8192;
+    cfg->ctx_dim = 1024;
+    cfg->in_channels = 16;
+    cfg->out_channels = 16;
+    cfg->max_batch = 2;
+}
+
+anima_hip_dit *anima_hip_dit_create(const anima_hip_dit_config *cfg, const char *const *names,
+                                    const void *const *ptrs, const int *dtypes,
+                                    const int64_t *shapes, int n, int mode)
+{
+    if (!cfg) {
+        fail("dit_create: null configuration");
+        return nullptr;
+    }
+    if (!check_cfg(*cfg))
+        return nullptr;
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16) {
+        fail("dit_create: unknown mode " + std::to_string(mode));
+        return nullptr;
+    }
+    if (n < 0 || (n > 0 && (!names || !ptrs || !dtypes || !shapes))) {
+        fail("dit_create: null weight table");
+        return nullptr;
+    }
+    if (!device_ready())
+        return nullptr;
+    auto *d = new anima_hip_dit;
+    d->cfg = *cfg;
+    d->bf16 = mode == ANIMA_HIP_BF16;
+    (void)hipGetDevice(&d->device);
+    const anima_hip_dit_config &c = d->cfg;
+    const int D = c.dim, HD = c.heads * c.head_dim;
+    const int K_in = (c.in_channels + 1) * kPatch * kPatch;
+    d->blk.resize(c.blocks);
+    const hipStream_t st = nullptr;
+
+    // Look up every tensor the forward needs; linear weights must be bf16.
+    auto find = [&](const std::string &name) -> int {
+        for (int i = 0; i < n; ++i)
+            if (strip_net(names[i]) == name)
+                return i;
+        return -1;
+    };
+    std::string err;
+    auto shape_ok = [&](int i, const std::string &name, int64_t rows, int64_t cols) {
+        if (shapes[2 * i] == rows && shapes[2 * i + 1] == cols)
+            return true;
+        if (err.empty())
+            err = "dit_create: " + name + " has shape [" + std::to_string(shapes[2 * i]) + ", " +
+                  std::to_string(shapes[2 * i + 1]) + "], expected [" + std::to_string(rows) +
+                  ", " + std::to_string(cols) + "]";
+        return false;
+    };
+    auto lin = [&](const std::string &name, int64_t rows, int64_t cols) -> const uint16_t * {
+        const int i = find(name);
+        if (i < 0 || !ptrs[i]) {
+            if (err.empty())
+                err = "dit_create: missing weight " + name;
+            return nullptr;
+        }
+        if (!shape_ok(i, name, rows, cols))
+            return nullptr;
+        if (dtypes[i] != ANIMA_HIP_DTYPE_BF16) {
+            if (err.empty())
+                err = "dit_create: linear weight " + name + " must be BF16";
+            return nullptr;
+        }
+        if (!aligned16(ptrs[i])) {
+            if (err.empty())
+                err = "dit_create: weight " + name + " is not 16-byte aligned";
+            return nullptr;
+        }
+        return static_cast<const uint16_t *>(ptrs[i]);
+    };
+    auto norm = [&](const std::string &name, int len) -> const float * {
+        const int i = find(name);
+        if (i < 0 || !ptrs[i]) {
+            if (err.empty())
+                err = "dit_create: missing weight " + name;
+            return nullptr;
+        }
+        if (!shape_ok(i, name, len, 0))
+            return nullptr;
+        if (dtypes[i] == ANIMA_HIP_DTYPE_F32) {
+            if (!aligned16(ptrs[i])) {
+                if (err.empty())
+                    err = "dit_create: weight " + name + " is not 16-byte aligned";
+                return nullptr;
+            }
+            return static_cast<const float *>(ptrs[i]);
+        }
+        if (dtypes[i] != ANIMA_HIP_DTYPE_BF16) {
+            if (err.empty())
+                err = "dit_create: norm weight " + name + " must be F32 or BF16";
+            return nullptr;
+        }
+        float *w = nullptr;
+        if (dev_alloc(d, w, size_t(len) * 4, "dit norm weight")) {
+            hipLaunchKernelGGL(widen_kernel, dim3(grid1(len)), dim3(256), 0, st,
+                               static_cast<const uint16_t *>(ptrs[i]), w, int64_t(len));
+            if (hip_ok(hipGetLastError(), "widen_kernel launch"))
+                return w;
+        }
+        if (err.empty())
+            err = anima_hip_last_error();
+        return nullptr;
+    };
+    static const char *kSub[3] = {"self_attn", "cross_attn", "mlp"};
+    for (int i = 0; i < c.blocks; ++i) {
+        BlockWeights &b = d->blk[i];
+        const std::string p = "blocks." + std::to_string(i) + ".";
+        b.sa_q = lin(p + "self_attn.q_proj.weight", HD, D);
+        b.sa_k = lin(p + "self_attn.k_proj.weight", HD, D);
+        b.sa_v = lin(p + "self_attn.v_proj.weight", HD, D);
+        b.sa_o = lin(p + "self_attn.output_proj.weight", D, HD);
+        b.sa_qn = norm(p + "self_attn.q_norm.weight", c.head_dim);
+        b.sa_kn = norm(p + "self_attn.k_norm.weight", c.head_dim);
+        b.cx_q = lin(p + "cross_attn.q_proj.weight", HD, D);
+        b.cx_k = lin(p + "cross_attn.k_proj.weight", HD, c.ctx_dim);
+        b.cx_v = lin(p + "cross_attn.v_proj.weight", HD, c.ctx_dim);
+        b.cx_o = lin(p + "cross_attn.output_proj.weight", D, HD);
+        b.cx_qn = norm(p + "cross_attn.q_norm.weight", c.head_dim);
+        b.cx_kn = norm(p + "cross_attn.k_norm.weight", c.head_dim);
+        b.fc1 = lin(p + "mlp.layer1.weight", c.mlp_hidden, D);
+        b.fc2 = lin(p + "mlp.layer2.weight", D, c.mlp_hidden);
+        for (int k = 0; k < 3; ++k) {
+            b.ada1[k] = lin(p + "adaln_modulation_" + kSub[k] + ".1.weight", kAdaHidden, D);
+            b.ada2[k] = lin(p + "adaln_modulation_" + kSub[k] + ".2.weight", 3 * D, kAdaHidden);
+        }
+    }
+    const uint16_t *xe = lin("x_embedder.proj.1.weight", D, K_in);
+    d->t1 = lin("t_embedder.1.linear_1.weight", D, D);
+    d->t2 = lin("t_embedder.1.linear_2.weight", 3 * D, D);
+    d->t_norm = norm("t_embedding_norm.weight", D);
+    d->fin_ada1 = lin("final_layer.adaln_modulation.1.weight", kAdaHidden, D);
+    d->fin_ada2 = lin("final_layer.adaln_modulation.2.weight", 2 * D, kAdaHidden);
+    d->fin_lin = lin("final_layer.linear.weight", 4 * c.out_channels, D);
+    if (!err.empty()) {
+        fail(err);
+        dit_free(d);
+        return nullptr;
+    }
+
+    // x_embedder weight [D][K_in] copied into rows of kp_in zero-padded bf16.
+    d->kp_in = int(linear_terms_ld(K_in));
+    uint16_t *xp = nullptr;
+    d->n_ada = 3 * c.blocks + 1;
+    const int nj = 2 + 2 * d->n_ada;
+    bool ok = dev_alloc(d, xp, size_t(D) * d->kp_in * 2, "dit x_embedder copy") &&
+              hip_ok(hipMemsetAsync(xp, 0, size_t(D) * d->kp_in * 2, st), "hipMemset") &&
+              hip_ok(hipMemcpy2DAsync(xp, size_t(d->kp_in) * 2, xe, size_t(K_in) * 2,
+                                      size_t(K_in) * 2, size_t(D), hipMemcpyDeviceToDevice, st),
+                     "x_embedder copy");
+    d->x_emb = xp;
+    const int MB = c.max_batch;
+    ok = ok && dev_alloc(d, d->feat, size_t(MB) * D * 4, "dit vectors") &&
+         dev_alloc(d, d->h1, size_t(MB) * D * 4, "dit vectors") &&
+         dev_alloc(d, d->h1s, size_t(MB) * D * 4, "dit vectors") &&
+         dev_alloc(d, d->emb, size_t(MB) * D * 4, "dit vectors") &&
+         dev_alloc(d, d->semb, size_t(MB) * D * 4, "dit vectors") &&
+         dev_alloc(d, d->lora, size_t(MB) * 3 * D * 4, "dit vectors") &&
+         dev_alloc(d, d->m1, size_t(d->n_ada) * MB * kAdaHidden * 4, "dit vectors") &&
+         dev_alloc(d, d->mods, size_t(d->n_ada) * MB * 3 * D * 4, "dit vectors") &&
+         dev_alloc(d, d->jobs, size_t(nj) * sizeof(GemvJob), "dit job table");
+    if (ok) {
+        // The job table holds the batch strides of max_batch-sized buffers;
+        // a forward on B <= max_batch rows uses the first B of each.
+        std::vector<GemvJob> jobs(nj);
+        jobs[0] = GemvJob{d->t1, d->feat, d->h1, nullptr, D, D, 0, D};
+        jobs[1] = GemvJob{d->t2, d->h1s, d->lora, nullptr, D, 3 * D, 0, 3 * D};
+        for (int a = 0; a < d->n_ada; ++a) {
+            const bool fin = a == 3 * c.blocks;
+            const uint16_t *w1 = fin ? d->fin_ada1 : d->blk[a / 3].ada1[a % 3];
+            const uint16_t *w2 = fin ? d->fin_ada2 : d->blk[a / 3].ada2[a % 3];
+            const int chunks = fin ? 2 : 3;
+            // Modulation a: rows b of 3D floats at mods + (a * max_batch + b) * 3D,
+            // i.e. the [B][3][D] (shift, scale, gate) layout of the sub-layers;
+            // the final layer's two chunks fill the first 2D of each row.
+            float *m1 = d->m1 + int64_t(a) * MB * kAdaHidden;
+            float *mod = d->mods + int64_t(a) * MB * 3 * D;
+            jobs[2 + a] = GemvJob{w1, d->semb, m1, nullptr, D, kAdaHidden, 0, kAdaHidden};
+            jobs[2 + d->n_ada + a] =
+                GemvJob{w2, m1, mod, d->lora, kAdaHidden, 3 * D, 3 * D, chunks * D};
+        }
+        ok = hip_ok(hipMemcpy(d->jobs, jobs.data(), jobs.size() * sizeof(GemvJob),
+                              hipMemcpyHostToDevice),
+                    "dit job table upload");
+    }
+    ok = ok && hip_ok(hipStreamSynchronize(st), "dit_create");
+    if (!ok) {
+        dit_free(d);
+        return nullptr;
+    }
+    return d;
+}
+
+void anima_hip_dit_destroy(anima_hip_dit *dit) { dit_free(dit); }
+
+bool anima_hip_dit_set_context_dev(anima_hip_dit *d, const float *ctx, int Bc, int S_kv,
+                                   void *stream)
+{
+    if (!d || !ctx)
+        return fail("dit_set_context: null pointer");
+    const anima_hip_dit_config &c = d->cfg;
+    if (Bc < 1 || Bc > c.max_batch || S_kv <= 0)
+        return fail("dit_set_context: context batch must be in 1..max_batch and S_kv positive");
+    if (!aligned16(ctx))
+        return fail("dit_set_context: context must be 16-byte aligned");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const int C = c.ctx_dim, H = c.heads, hd = c.head_dim, HD = H * hd;
+    const int64_t M64 = int64_t(Bc) * S_kv;
+    if (M64 > INT32_MAX / 8)
+        return fail("dit_set_context: context too long");
+    const int M = int(M64);
+    if (Bc != d->ctx_B || S_kv != d->ctx_S) {
+        // New cache shape: drain the device before the old caches go.
+        if (!hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize"))
+            return false;
+        for (auto &b : d->blk) {
+            if (b.ctx_k)
+                (void)hipFree(b.ctx_k);
+            if (b.ctx_v)
+                (void)hipFree(b.ctx_v);
+            b.ctx_k = b.ctx_v = nullptr;
+        }
+        d->ctx_B = d->ctx_S = 0;
+        for (auto &b : d->blk) {
+            if (!hip_ok(hipMalloc(&b.ctx_k, prepared_k_bytes(Bc, S_kv, H, hd, d->bf16)),
+                        "dit context K cache") ||
+                !hip_ok(hipMalloc(&b.ctx_v, prepared_v_bytes(Bc, S_kv, H, hd, d->bf16)),
+                        "dit context V cache"))
+                return false;
+        }
+    }
+    const size_t proj = round_up256(size_t(M) * HD * 4);
+    const size_t lin = round_up256(linear_scratch_bytes(M, C, !d->bf16));
+    const size_t need = 2 * proj + lin;
+    if (need > d->ctx_work_bytes) {
+        if (!hip_ok(hipStreamSynchronize(st), "hipStreamSynchronize"))
+            return false;
+        if (d->ctx_work)
+            (void)hipFree(d->ctx_work);
+        d->ctx_work = nullptr;
+        d->ctx_work_bytes = 0;
+        if (!hip_ok(hipMalloc(&d->ctx_work, need), "dit context workspace"))
+            return false;
+        d->ctx_work_bytes = need;
+    }
+    float *kf = static_cast<float *>(d->ctx_work);
+    float *vf = reinterpret_cast<float *>(static_cast<char *>(d->ctx_work) + proj);
+    void *ls = static_cast<char *>(d->ctx_work) + 2 * proj;
+    // Per block: K = k_norm(ctx Wk^T), V = ctx Wv^T (numpy_dit.py:277-286),
+    // prepared once for every later forward.
+    for (auto &b : d->blk) {
+        float *ko = d->bf16 ? kf : static_cast<float *>(b.ctx_k);
+        float *vo = d->bf16 ? vf : static_cast<float *>(b.ctx_v);
+        if (!launch_linear(ctx, C, b.cx_k, C, ko, HD, M, HD, C, !d->bf16, ls, lin, st) ||
+            !launch_linear(ctx, C, b.cx_v, C, vo, HD, M, HD, C, !d->bf16, ls, lin, st))
+            return false;
+        const bool ok = d->bf16 ? prepare_kv(kf, vf, b.cx_kn, nullptr, b.ctx_k, b.ctx_v, Bc, S_kv,
+                                             H, hd, 1e-6f, true, st)
+                                : prepare_kv(ko, nullptr, b.cx_kn, nullptr, b.ctx_k, nullptr, Bc,
+                                             S_kv, H, hd, 1e-6f, false, st);
+        if (!ok)
+            return false;
+    }
+    d->ctx_B = Bc;
+    d->ctx_S = S_kv;
+    return true;
+}
+
+size_t anima_hip_dit_scratch_bytes(const anima_hip_dit *d, int B, int T, int H, int W)
+{
+    if (!d || B < 0 || T < 0 || H < 0 || W < 0)
+        return 0;
+    int Hp, Wp;
+    int64_t S;
+    grid_of(T, H, W, Hp, Wp, S);
+    return dit_scratch(d, B, S).total;
+}
+
+bool anima_hip_dit_forward_dev(anima_hip_dit *d, const float *x, int64_t x_batch_stride,
+                               const float *sigma, int B, int T, int H, int W, const float *freqs,
+                               float *out, void *scratch, size_t scratch_bytes, void *stream)
+{
+    if (!d || !out)
+        return fail("dit_forward: null pointer");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    float *f = nullptr;
+    if (!dit_run(d, x, x_batch_stride, sigma, B, T, H, W, freqs, scratch, scratch_bytes, st, &f))
+        return false;
+    int Hp, Wp;
+    int64_t S;
+    grid_of(T, H, W, Hp, Wp, S);
+    UnpatchArgs ua;
+    ua.f = f;
+    ua.out = out;
+    ua.Cout = d->cfg.out_channels;
+    ua.T = T;
+    ua.Hi = H;
+    ua.Wi = W;
+    ua.Hp = Hp;
+    ua.Wp = Wp;
+    ua.n = int64_t(B) * ua.Cout * T * H * W;
+    hipLaunchKernelGGL(unpatchify_kernel, dim3(grid1(ua.n)), dim3(256), 0, st, ua);
+    return hip_ok(hipGetLastError(), "unpatchify_kernel launch");
+}
+
+bool anima_hip_dit_euler_dev(anima_hip_dit *d, float *latent, const float *sigmas, int steps,
+                             float cfg, int H, int W, const float *freqs, void *scratch,
+                             size_t scratch_bytes, void *stream)
+{
+    if (!d || !latent || !sigmas)
+        return fail("dit_euler: null pointer");
+    if (steps < 0)
+        return fail("dit_euler: negative step count");
+    if (d->cfg.max_batch < 2 || d->ctx_B != 2)
+        return fail("dit_euler: needs max_batch >= 2 and a context of 2 entries "
+                    "(unconditional, conditional)");
+    if (d->cfg.in_channels != d->cfg.out_channels)
+        return fail("dit_euler: the latent needs as many output channels as input channels");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    int Hp, Wp;
+    int64_t S;
+    grid_of(1, H, W, Hp, Wp, S);
+    for (int i = 0; i < steps; ++i) {
+        // CFG batch [uncond, cond] of the same latent (sampling.py:124-130).
+        const float sig[2] = {sigmas[i], sigmas[i]};
+        float *f = nullptr;
+        if (!dit_run(d, latent, 0, sig, 2, 1, H, W, freqs, scratch, scratch_bytes, st, &f))
+            return false;
+        EulerArgs ea;
+        ea.f = f;
+        ea.x = latent;
+        ea.S = S;
+        ea.Cout = d->cfg.out_channels;
+        ea.Hi = H;
+        ea.Wi = W;
+        ea.Wp = Wp;
+        ea.n = int64_t(ea.Cout) * H * W;
+        ea.cfg = cfg;
+        ea.dt = float(double(sigmas[i + 1]) - double(sigmas[i]));
+        hipLaunchKernelGGL(cfg_euler_kernel, dim3(grid1(ea.n)), dim3(256), 0, st, ea);
+        if (!hip_ok(hipGetLastError(), "cfg_euler_kernel launch"))
+            return false;
+    }
+    return true;
+}
+
+}  // extern "C"

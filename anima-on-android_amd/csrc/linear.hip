@@ -296,14 +296,29 @@ bool launch_linear_residual(const float *a, int64_t lda, const uint16_t *w, int6
     hipLaunchKernelGGL(split_kernel, dim3(unsigned(nblk)), dim3(256), 0, st, sa);
     if (!hip_ok(hipGetLastError(), "split_kernel launch"))
         return false;
+    return launch_linear_residual_terms(reinterpret_cast<const uint16_t *>(sa.hi), w, ldw, x, ldx,
+                                        gate, gate_stride, B, S, N, K, st);
+}
+
+bool launch_linear_residual_terms(const uint16_t *hi, const uint16_t *w, int64_t ldw, float *x,
+                                  int64_t ldx, const float *gate, int64_t gate_stride, int B,
+                                  int S, int N, int K, hipStream_t st)
+{
+    if (int64_t(B) * S * N == 0)
+        return true;
+    if (!linear_residual_supported(S, N, K, w, ldw, x, ldx))
+        return fail("linear_residual: no bf16 GEMM with a per-channel scale for this shape");
+    if ((reinterpret_cast<uintptr_t>(gate) & 3u) != 0 || (reinterpret_cast<uintptr_t>(hi) & 15u) != 0)
+        return fail("linear_residual: misaligned gate or terms");
+    const int64_t kp = padded_k(K);
     std::lock_guard<std::mutex> g(g_lt_mu);
     LtPlan *plan = lt_plan(S, N, K, kp, ldw, ldx, true);
     // Per batch entry b: x_b = gate_b (.) (a_b W^T) + x_b, gate over the N
     // output channels.
     for (int b = 0; b < B; ++b) {
         const int64_t r0 = int64_t(b) * S;
-        const uint16_t *hb = reinterpret_cast<const uint16_t *>(sa.hi) + r0 * kp;
-        if (!lt_matmul(plan, w, hb, x + r0 * ldx, 1.0f, st, gate + int64_t(b) * gate_stride))
+        if (!lt_matmul(plan, w, hi + r0 * kp, x + r0 * ldx, 1.0f, st,
+                       gate + int64_t(b) * gate_stride))
             return false;
     }
     return true;

@@ -273,6 +273,7 @@ def other_configs(c, cpu_rate):
         res["c4_denoise_step_28_blocks"] = denoise_step(c, mode)
         res["proj_gemm_8192x2048x2048"] = projection_gemm(c, mode)
         res["c4_denoise_step_28_blocks_attention_sublayers"] = denoise_step_blocks(c, mode)
+        res["c4_sampler_step_full_dit"] = sampler_step(c, mode)
         out[variant] = res
         log(f"[bench] configs {variant}: " + json.dumps(res))
     if cpu_rate:
@@ -406,6 +407,65 @@ def denoise_step_blocks(c, mode, blocks=28, B=2, S=4096, H=16, D=128, Dm=2048):
                         "projection's bf16 terms), q(/k/v)_proj, q/k RMSNorm+RoPE, flash attention "
                         "(cross: cached context K/V), output_proj, gated residual into the "
                         "resident stream"}
+
+
+def sampler_step(c, mode, H=128, W=128, steps=3):
+    """One Euler/CFG sampler step of the whole DiT at 1024x1024
+    (EulerSampler.sample, sampling.py:115-140, on NumpyDiT.forward): the
+    latent [1,16,128,128] runs as the CFG pair through patch embedding, 28
+    blocks (self-attention, cross-attention over the cached 2x512x1024
+    context K/V, MLP) and the final layer, then v = v_u + 5 (v_c - v_u),
+    x += v dt (anima_hip_dit_euler_dev).  Seeded random bf16 weights of the
+    Anima 2B shapes; the context K/V are built once, outside the step."""
+    import numpy as np
+    torch, lib, _lib = c.torch, c.lib, c._lib
+    from anima_hip.dit import AnimaDiT, DiTConfig, weight_shapes
+    cfg = DiTConfig.anima_2b()
+    g = torch.Generator(device=c.dev)
+    g.manual_seed(9001)
+    tensors, table = [], {}
+    for name, shape in weight_shapes(cfg).items():
+        if len(shape) == 2:
+            t = (torch.randn(shape, generator=g, device=c.dev) * 0.02).to(torch.bfloat16)
+            table[name] = (t.data_ptr(), "BF16", shape)
+        else:
+            t = 1.0 + 0.1 * torch.randn(shape, generator=g, device=c.dev)
+            table[name] = (t.data_ptr(), "F32", shape)
+        tensors.append(t)
+    rng = np.random.default_rng(9002)
+    ctx = (rng.standard_normal((2, 512, cfg.ctx_dim), dtype=np.float32) * np.float32(0.5))
+    lat0 = torch.randn((1, cfg.in_channels, H, W), generator=g, device=c.dev)
+    lat = torch.empty_like(lat0)
+    from anima_hip.rope import generate_rope_freqs
+    freqs = torch.from_numpy(generate_rope_freqs(H // 2, W // 2)).to(c.dev)
+    sig = (ct.c_float * 2)(1.0, 0.8571428)
+    with AnimaDiT(table, cfg, mode) as m:
+        m.set_context(ctx)
+        n = lib.anima_hip_dit_scratch_bytes(m.handle, 2, 1, H, W)
+        scratch = torch.empty(n, dtype=torch.uint8, device=c.dev)
+
+        def step():
+            lat.copy_(lat0)
+            _lib.check(lib.anima_hip_dit_euler_dev(m.handle, lat.data_ptr(), sig, 1,
+                                                   ct.c_float(5.0), H, W, freqs.data_ptr(),
+                                                   scratch.data_ptr(), n, c.stp), "dit_euler_dev")
+        with torch.cuda.stream(c.st):
+            ms = c.time(step, steps, 1)
+        if not torch.isfinite(lat).all():
+            raise RuntimeError("non-finite latent")
+    S, B, D, hd, Hh = (H // 2) * (W // 2), 2, cfg.dim, cfg.heads * cfg.head_dim, cfg.heads
+    M = B * S
+    attn = cfg.blocks * 4.0 * B * Hh * S * cfg.head_dim * (S + 512)
+    lin = cfg.blocks * (6 * 2.0 * M * D * hd + 2 * 2.0 * M * D * cfg.mlp_hidden)
+    lin += 2.0 * M * D * (cfg.in_channels + 1) * 4 + 2.0 * M * D * 4 * cfg.out_channels
+    del tensors, scratch
+    torch.cuda.empty_cache()
+    return {"ms_per_step": round(ms, 3), "s_per_step": round(ms / 1e3, 4),
+            "tflops": round((attn + lin) / ms / 1e9, 2), "flops_per_step": attn + lin,
+            "includes": "timestep embedding + every AdaLN modulation, patch embedding, 28 x "
+                        "(self-attention, cross-attention on cached context K/V, GELU MLP) "
+                        "sub-layers on the resident residual stream, final layer, CFG + Euler "
+                        "update of the latent; synthetic Anima 2B-shaped weights"}
 
 
 def cpu_baseline(qn, kn, v, B, H, S, D, heads):

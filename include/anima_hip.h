@@ -273,6 +273,90 @@ int anima_hip_weights_info(const anima_hip_weights *w, const char *name, int *dt
  * converted, as the reference widens its norm weights).  NULL on error. */
 const void *anima_hip_weights_device(anima_hip_weights *w, const char *name, int as_f32);
 
+/* dtype codes of weight tables (the codes above). */
+#define ANIMA_HIP_DTYPE_F32 0
+#define ANIMA_HIP_DTYPE_F16 1
+#define ANIMA_HIP_DTYPE_BF16 2
+
+/* ---- The whole DiT on the device (NumpyDiT, anima_rt/scripts/numpy_dit.py:67-130)
+ * Shapes of the model; anima_hip_dit_default_config fills the Anima 2B values
+ * (2048 wide, 28 blocks, 16 heads x 128, MLP 8192, text context 1024 wide,
+ * 16 latent channels in and out, CFG batch 2).  The patch is 2 x 2 pixels of
+ * one frame and the AdaLN hidden width 256, as in the reference. */
+typedef struct anima_hip_dit_config {
+    int dim;           /* model width D */
+    int blocks;        /* DiT blocks */
+    int heads;         /* attention heads */
+    int head_dim;      /* per-head width */
+    int mlp_hidden;    /* MLP hidden width */
+    int ctx_dim;       /* text-context width */
+    int in_channels;   /* latent channels (a zero padding-mask channel is appended) */
+    int out_channels;  /* output channels */
+    int max_batch;     /* largest forward batch, 1..4 (the CFG pair needs 2) */
+} anima_hip_dit_config;
+
+typedef struct anima_hip_dit anima_hip_dit;
+
+void anima_hip_dit_default_config(anima_hip_dit_config *cfg);
+
+/* A model over device-resident weights given as a table of n (name, device
+ * pointer, dtype code, shape) entries; shapes holds two int64 per entry,
+ * [out, in] for a matrix and [len, 0] for a vector, and every tensor is
+ * checked against the configuration.  Names are the reference's checkpoint's, with or
+ * without its "net." prefix (blocks.{i}.self_attn.q_proj.weight, ...,
+ * x_embedder.proj.1.weight, t_embedder.1.linear_{1,2}.weight,
+ * t_embedding_norm.weight, final_layer.adaln_modulation.{1,2}.weight,
+ * final_layer.linear.weight).  Linear weights must be BF16 bit patterns
+ * [out, in]; norm weights F32 or BF16 (widened like the reference).  The
+ * pointers are borrowed and must stay valid for the model's life (the weight
+ * store's anima_hip_weights_device copies do).  mode: ANIMA_HIP_F32 (f32
+ * activations, exact hi+lo bf16 GEMM terms, f32 attention) or ANIMA_HIP_BF16
+ * (bf16 activations and attention inputs).  NULL on error. */
+anima_hip_dit *anima_hip_dit_create(const anima_hip_dit_config *cfg, const char *const *names,
+                                    const void *const *ptrs, const int *dtypes,
+                                    const int64_t *shapes, int n, int mode);
+void anima_hip_dit_destroy(anima_hip_dit *dit);
+
+/* Text context ctx [Bc, S_kv, ctx_dim] f32 on the device: every block's
+ * cross-attention K = k_norm(ctx Wk^T) and V = ctx Wv^T are computed once here
+ * and reused by every later forward (the reference recomputes them per call).
+ * Bc = 1 serves every batch entry; the sampler needs Bc = 2 in the order
+ * [unconditional, conditional] (sampling.py:127).  Allocates the caches. */
+bool anima_hip_dit_set_context_dev(anima_hip_dit *dit, const float *ctx, int Bc, int S_kv,
+                                   void *stream);
+
+/* Device scratch of one forward on a [B, C, T, H, W] latent (bytes); query it
+ * after the context is set. */
+size_t anima_hip_dit_scratch_bytes(const anima_hip_dit *dit, int B, int T, int H, int W);
+
+/* NumpyDiT.forward (numpy_dit.py:82-130) on device memory: x [B, C, T, H, W]
+ * f32 with batch stride x_batch_stride elements (0: every batch entry reads
+ * entry 0), sigma: B noise levels (host), freqs: the RoPE table [T*Hp*Wp, 64,
+ * 2, 2] of the patch grid (Hp = ceil(H/2), Wp = ceil(W/2); the reference's
+ * _generate_rope_freqs(Hp, Wp, T, head_dim)), out [B, out_channels, T, H, W].
+ * Uses the context set last.  Nothing is allocated; asynchronous on stream;
+ * calls on one model are not concurrent (they share its modulation vectors). */
+bool anima_hip_dit_forward_dev(anima_hip_dit *dit, const float *x, int64_t x_batch_stride,
+                               const float *sigma, int B, int T, int H, int W, const float *freqs,
+                               float *out, void *scratch, size_t scratch_bytes, void *stream);
+
+/* EulerSampler.sample (sampling.py:115-140) on the device: `steps` Euler
+ * steps of the latent [C, H, W] (one frame, updated in place) over host
+ * sigmas[steps + 1], each a B = 2 forward of the latent against the context
+ * [unconditional, conditional] followed by v = v_u + cfg (v_c - v_u),
+ * x += v (sigma_next - sigma).  scratch: anima_hip_dit_scratch_bytes(dit, 2,
+ * 1, H, W).  Asynchronous on stream. */
+bool anima_hip_dit_euler_dev(anima_hip_dit *dit, float *latent, const float *sigmas, int steps,
+                             float cfg, int H, int W, const float *freqs, void *scratch,
+                             size_t scratch_bytes, void *stream);
+
+/* ---- Device memory for hosts without another HIP binding ---- */
+void *anima_hip_malloc(size_t bytes);              /* NULL on error */
+void anima_hip_free(void *p);
+/* Synchronous copy; kind: 1 host->device, 2 device->host, 3 device->device. */
+bool anima_hip_memcpy(void *dst, const void *src, size_t bytes, int kind);
+bool anima_hip_synchronize(void);
+
 #ifdef __cplusplus
 }
 #endif

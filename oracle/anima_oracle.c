@@ -28,6 +28,8 @@
  *       fp64 two-pass mean/variance.
  *   oracle_silu             -- bit-identical to oracle/_ref anima_rt_run_silu;
  *       fp64 x / (1 + exp(-x)).
+ *   oracle_gelu             -- bit-identical to oracle/_ref anima_rt_run_gelu;
+ *       fp64 x * Phi(x) via math.erf; GELU(0) = 0, GELU(x) - GELU(-x) = x.
  *   oracle_modulate, oracle_gate_residual -- numpy float32 evaluation of the
  *       same expressions (each operation rounded to float32).
  */
@@ -396,6 +398,17 @@ void oracle_silu(const float *x, float *y, int64_t n)
 {
     for (int64_t i = 0; i < n; i++)
         y[i] = x[i] / (1.0f + expf(-x[i]));
+}
+
+/* GELU, exact erf form (anima_rt/include/cpu/gelu_kernel.h:13-23):
+ * x * 0.5 * (1 + erf(x * (float)M_SQRT1_2)), evaluated left to right. */
+void oracle_gelu(const float *x, float *y, int64_t n)
+{
+    const float alpha = 0.70710678118654752440f;
+    for (int64_t i = 0; i < n; i++) {
+        const float h = x[i] * 0.5f;
+        y[i] = h * (1.0f + erff(x[i] * alpha));
+    }
 }
 
 /* AdaLN modulation of NumpyBlock.forward (anima_rt/scripts/numpy_dit.py:238,

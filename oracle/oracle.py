@@ -88,6 +88,8 @@ def oracle_lib():
         lib.oracle_layernorm.restype = None
         lib.oracle_silu.argtypes = [_P, _P, _ct.c_int64]
         lib.oracle_silu.restype = None
+        lib.oracle_gelu.argtypes = [_P, _P, _ct.c_int64]
+        lib.oracle_gelu.restype = None
         lib.oracle_modulate.argtypes = [_P, _P, _P, _P, _I, _ct.c_int64, _ct.c_int64]
         lib.oracle_modulate.restype = None
         lib.oracle_gate_residual.argtypes = [_P, _P, _P, _I, _ct.c_int64, _ct.c_int64]
@@ -121,6 +123,8 @@ def ref_lib():
         lib.anima_rt_run_layernorm.restype = _ct.c_bool
         lib.anima_rt_run_silu.argtypes = [_P, _P, _I]
         lib.anima_rt_run_silu.restype = _ct.c_bool
+        lib.anima_rt_run_gelu.argtypes = [_P, _P, _I]
+        lib.anima_rt_run_gelu.restype = _ct.c_bool
         if not lib.anima_rt_init():
             raise RuntimeError("reference anima_rt_init failed")
         _ref_lib = lib
@@ -194,6 +198,14 @@ def silu(x):
     x = _f32c(x)
     y = np.empty_like(x)
     oracle_lib().oracle_silu(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def gelu(x):
+    """GELU, exact erf form, restated (gelu_kernel.h:13-23)."""
+    x = _f32c(x)
+    y = np.empty_like(x)
+    oracle_lib().oracle_gelu(_ptr(x), _ptr(y), x.size)
     return y
 
 
@@ -318,6 +330,13 @@ def ref_silu(x):
     x = _f32c(x)
     y = np.zeros_like(x)
     assert ref_lib().anima_rt_run_silu(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def ref_gelu(x):
+    x = _f32c(x)
+    y = np.zeros_like(x)
+    assert ref_lib().anima_rt_run_gelu(_ptr(x), _ptr(y), x.size)
     return y
 
 
@@ -486,3 +505,133 @@ def rope_freqs_fp64(H: int, W: int, T: int = 1, head_dim: int = 128) -> np.ndarr
             col += 1
     c, s = np.cos(tab), np.sin(tab)
     return np.stack([c, -s, s, c], axis=-1).reshape(T * H * W, head_dim // 2, 2, 2)
+
+
+# ------------------------------------------------- the DiT around the path
+# numpy restatements of NumpyDiT's host pieces and of the Euler/CFG sampler
+# (anima_rt/scripts/numpy_dit.py, anima_rt/scripts/sampling.py), composed from
+# the C restatements above.  Weights are a dict name -> array: linear weights
+# as bf16 bit patterns [out, in] (uint16), norm weights as float32 vectors.
+
+PATCH = 2  # spatial patch; one frame per patch
+
+
+def timesteps(sigma, dim):
+    """Sinusoidal timestep features, _numpy_timesteps (numpy_dit.py:39-46):
+    [cos(sigma f_i), sin(sigma f_i)] with f_i = exp(-ln(1e4) i / half), every
+    operation in float32."""
+    half = dim // 2
+    exponent = (np.float32(-math.log(10000)) * np.arange(half, dtype=np.float32)
+                / np.float32(half))
+    freqs = np.exp(exponent)
+    s = np.atleast_1d(np.asarray(sigma, np.float32)).reshape(-1, 1)
+    arg = s * freqs.reshape(1, -1)
+    return np.concatenate([np.cos(arg), np.sin(arg)], axis=-1).astype(np.float32)
+
+
+def patchify(x):
+    """Pad H and W to the patch, append the zero padding-mask channel and cut
+    2x2 patches (numpy_dit.py:10-22, 92-95): [B,C,T,H,W] -> [B,T,Hp,Wp,(C+1)*4]
+    with feature index (c*2 + dy)*2 + dx."""
+    x = _f32c(x)
+    B, C, T, H, W = x.shape
+    Hp, Wp = -(-H // PATCH), -(-W // PATCH)
+    xp = np.zeros((B, C + 1, T, Hp * PATCH, Wp * PATCH), np.float32)
+    xp[:, :C, :, :H, :W] = x
+    t = xp.reshape(B, C + 1, T, Hp, PATCH, Wp, PATCH).transpose(0, 2, 3, 5, 1, 4, 6)
+    return np.ascontiguousarray(t.reshape(B, T, Hp, Wp, (C + 1) * PATCH * PATCH))
+
+
+def unpatchify(f, out_ch, H, W):
+    """Inverse patch rearrangement and crop (numpy_dit.py:24-31, 128-129):
+    [B,T,Hp,Wp,4*out_ch] with feature (dy*2 + dx)*out_ch + c -> [B,out_ch,T,H,W]."""
+    B, T, Hp, Wp, _ = f.shape
+    o = f.reshape(B, T, Hp, Wp, PATCH, PATCH, out_ch).transpose(0, 6, 1, 2, 4, 3, 5)
+    o = o.reshape(B, out_ch, T, Hp * PATCH, Wp * PATCH)
+    return np.ascontiguousarray(o[:, :, :, :H, :W]).astype(np.float32)
+
+
+def adaln(emb, w1, w2, lora, n_chunks):
+    """AdaLN modulation (NumpyBlock._adaln, numpy_dit.py:211-223; the final
+    layer's, :171-180): one SiLU, two bias-free linears D -> 256 -> n*D, plus
+    the first n*D entries of the AdaLN-LoRA term.  Returns n chunks [B, D]."""
+    emb = _f32c(emb)
+    D = emb.shape[-1]
+    m2 = gemm_bf16(gemm_bf16(silu(emb), w1), w2)
+    m2 = (m2 + _f32c(lora)[:, :n_chunks * D]).astype(np.float32)
+    return [np.ascontiguousarray(m2[:, i * D:(i + 1) * D]) for i in range(n_chunks)]
+
+
+def mlp_block(x, mod, w1, w2, eps=1e-6):
+    """MLP sub-layer of NumpyBlock.forward with NumpyMLP (numpy_dit.py:249-253,
+    304-317): x + gate * layer2(gelu(layer1(layernorm(x)*(1+scale) + shift)))."""
+    x = _f32c(x)
+    B, S, D = x.shape
+    shift, scale, gate = (np.ascontiguousarray(mod[:, i]) for i in range(3))
+    xm = modulate(layernorm(x, eps), scale, shift)
+    h = gelu(gemm_bf16(xm.reshape(B * S, D), w1))
+    return gate_residual(x, gate, gemm_bf16(h, w2).reshape(B, S, D))
+
+
+def dit_forward(x, sigma, ctx, w, blocks, heads, head_dim, out_ch=16, eps=1e-6, sdpa=None):
+    """NumpyDiT.forward (numpy_dit.py:82-130) on latent x [B,C,T,H,W], noise
+    levels sigma [B] and text context ctx [B,S_kv,ctx_dim]; returns
+    [B,out_ch,T,H,W]."""
+    x = _f32c(x)
+    B, C, T, H, W = x.shape
+    tok = patchify(x)
+    _, _, Hp, Wp, K = tok.shape
+    S = T * Hp * Wp
+    xr = gemm_bf16(tok.reshape(B * S, K), w["x_embedder.proj.1.weight"])
+    D = xr.shape[-1]
+    xr = xr.reshape(B, S, D)
+    freqs = rope_freqs(Hp, Wp, T, head_dim)
+    feat = timesteps(sigma, D)
+    lora = gemm_bf16(silu(gemm_bf16(feat, w["t_embedder.1.linear_1.weight"])),
+                     w["t_embedder.1.linear_2.weight"])
+    emb = rmsnorm(feat, w["t_embedding_norm.weight"], 1e-6)
+    for i in range(blocks):
+        p = f"blocks.{i}."
+
+        def mods(sub):
+            return np.stack(adaln(emb, w[p + f"adaln_modulation_{sub}.1.weight"],
+                                  w[p + f"adaln_modulation_{sub}.2.weight"], lora, 3), axis=1)
+
+        a = p + "self_attn."
+        xr = attention_block(xr, mods("self_attn"), w[a + "q_proj.weight"], w[a + "k_proj.weight"],
+                             w[a + "v_proj.weight"], w[a + "output_proj.weight"],
+                             w[a + "q_norm.weight"], w[a + "k_norm.weight"], freqs, None,
+                             heads, head_dim, eps, sdpa)
+        a = p + "cross_attn."
+        xr = attention_block(xr, mods("cross_attn"), w[a + "q_proj.weight"],
+                             w[a + "k_proj.weight"], w[a + "v_proj.weight"],
+                             w[a + "output_proj.weight"], w[a + "q_norm.weight"],
+                             w[a + "k_norm.weight"], None, ctx, heads, head_dim, eps, sdpa)
+        xr = mlp_block(xr, mods("mlp"), w[p + "mlp.layer1.weight"], w[p + "mlp.layer2.weight"],
+                       eps)
+    shift, scale = adaln(emb, w["final_layer.adaln_modulation.1.weight"],
+                         w["final_layer.adaln_modulation.2.weight"], lora, 2)
+    xm = modulate(layernorm(xr, eps), scale, shift)
+    f = gemm_bf16(xm.reshape(B * S, D), w["final_layer.linear.weight"])
+    return unpatchify(f.reshape(B, T, Hp, Wp, -1), out_ch, H, W)
+
+
+def z_image_sigmas(steps, denoise=1.0, shift=3.0):
+    """ZImageScheduler.get_sigmas (sampling.py:74-83): linspace from denoise
+    to 0 in float32, then shift*s / (1 + (shift-1)*s)."""
+    s = np.linspace(denoise, 0.0, steps + 1, dtype=np.float32)
+    return (shift * s / (1.0 + (shift - 1.0) * s)).astype(np.float32)
+
+
+def euler_sample(forward, noise, sigmas, ctx_cond, ctx_uncond, cfg):
+    """EulerSampler.sample (sampling.py:115-140): per step one forward of the
+    CFG pair [uncond, cond], v = v_u + cfg (v_c - v_u), x += v (s_next - s)."""
+    x = _f32c(noise)
+    ctx_b = np.concatenate([ctx_uncond, ctx_cond], axis=0)
+    for i in range(len(sigmas) - 1):
+        s, s_next = float(sigmas[i]), float(sigmas[i + 1])
+        x_b = np.tile(np.expand_dims(x, 2), (2, 1, 1, 1, 1))
+        v = forward(x_b, np.array([s, s], np.float32), ctx_b)
+        v_cfg = v[0:1] + cfg * (v[1:2] - v[0:1])
+        x = x + v_cfg[:, :, 0] * (s_next - s)
+    return x

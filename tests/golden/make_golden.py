@@ -17,6 +17,7 @@ Cases
   rope_*   anima_rt_run_rope on a 4x4 token grid, and the D=4 known-answer
            input of scripts/test_rope_debug.py:17-34
   gemm_*   anima_rt_run_gemm_bf16 (fp32 activations x bf16 weights)
+  ln_*, silu_*, gelu_*  anima_rt_run_layernorm / _silu / _gelu
 
 Run:  python tests/golden/make_golden.py
 """
@@ -97,6 +98,12 @@ def main():
                                        -100.0], np.float32)]).astype(np.float32)
     vec["silu_x"] = silu_x
     vec["silu_out"] = oracle.ref_silu(silu_x)
+    # GELU (exact erf form) over the MLP's activation range and its tails.
+    gelu_x = np.concatenate([normal(rng, 1000, sigma=3.0),
+                             np.array([0.0, -0.0, 1e-8, -1e-8, 5.0, -5.0, 10.0, -10.0, 40.0,
+                                       -40.0], np.float32)]).astype(np.float32)
+    vec["gelu_x"] = gelu_x
+    vec["gelu_out"] = oracle.ref_gelu(gelu_x)
 
     np.savez_compressed(OUT, **vec)
     print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes, {len(vec)} arrays)")
