@@ -59,6 +59,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true",
                     help="skip the other variant and the extra configurations")
+    ap.add_argument("--sampler-step", action="store_true",
+                    help="only the whole-DiT Euler/CFG sampler step at 1024x1024, both modes; "
+                         "prints one JSON line of its own")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 256 MiB device copy (calibrates "
                          "FETCH_SIZE/WRITE_SIZE) then 2 steps of each variant; prints no JSON")
@@ -541,6 +544,12 @@ def main():
     lib = _lib.load()
     _lib.check(lib.anima_rt_init(), "anima_rt_init")
     c = Ctx(torch, lib, _lib)
+
+    if args.sampler_step:
+        res = {v: sampler_step(c, MODE[v]) for v in ("bf16", "f32")}
+        print(json.dumps({"config": "c4_sampler_step_full_dit", "latent": [1, 16, 128, 128],
+                          "results": res}), flush=True)
+        return
 
     log("[bench] generating inputs")
     rng = np.random.default_rng(3003)
