@@ -52,6 +52,12 @@ struct LnArgs {
     int64_t ldx;
     const float *mod;  // per batch entry b at mod + b*mod_ld: shift [Dm], scale [Dm], ...
     int64_t mod_ld;
+    // Pending residual of the previous sub-layer, or null: before the norm,
+    // x += gate[b] * y (gate at res_gate + b*res_ld), written back to x.
+    const float *res_y;
+    const float *res_gate;
+    int64_t res_ld;
+    float *xw;  // x itself, writable (set with res_y)
     unsigned int *hi, *lo;  // [M][kp] bf16 (addressed as pairs); lo may be null
     int64_t kp;
     int64_t M;
@@ -76,6 +82,12 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(LnArgs a)
     for (int i = 0; i < VPL; ++i) {
         const int c = lane + 64 * i;
         v[i] = c < n4 ? *reinterpret_cast<const f32x4 *>(x + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+        if (a.res_y && c < n4) {
+            const f32x4 y = *reinterpret_cast<const f32x4 *>(a.res_y + row * a.Dm + 4 * c);
+            const f32x4 g = *reinterpret_cast<const f32x4 *>(a.res_gate + b * a.res_ld + 4 * c);
+            v[i] = v[i] + g * y;
+            *reinterpret_cast<f32x4 *>(a.xw + row * a.ldx + 4 * c) = v[i];
+        }
         sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     }
     const float mean = wave_sum(sum) / float(a.Dm);
@@ -177,7 +189,8 @@ size_t attention_block_scratch_bytes(int B, int S, int Dm, int H, int D, int Bk,
 
 bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t mod_ld,
                         uint16_t *hi, uint16_t *lo, int64_t M, int S, int Dm, float eps,
-                        hipStream_t st)
+                        hipStream_t st, float *res_x, const float *res_y, const float *res_gate,
+                        int64_t res_ld)
 {
     if (M == 0)
         return true;
@@ -186,11 +199,19 @@ bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t m
     if (!aligned16(x) || ldx % 4 || !aligned16(mod) || mod_ld % 4 || !aligned16(hi) ||
         !aligned16(lo))
         return fail("ln_modulate: operands must be 16-byte aligned");
+    if (res_y && (res_x != x || ldx != Dm || !aligned16(res_y) || !aligned16(res_gate) ||
+                  res_ld % 4))
+        return fail("ln_modulate: the pending residual needs x itself, dense rows and 16-byte "
+                    "alignment");
     LnArgs a;
     a.x = x;
     a.ldx = ldx;
     a.mod = mod;
     a.mod_ld = mod_ld;
+    a.res_y = res_y;
+    a.res_gate = res_gate;
+    a.res_ld = res_ld;
+    a.xw = res_y ? res_x : nullptr;
     a.hi = reinterpret_cast<unsigned int *>(hi);
     a.lo = reinterpret_cast<unsigned int *>(lo);
     a.kp = linear_terms_ld(Dm);
@@ -271,7 +292,9 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
     // x_m as bf16 terms, then the projections of NumpyAttention.forward
     // (numpy_dit.py:273-281): q from x_m, and k/v from x_m (self) or the
     // cached context projections (cross).
-    if (!launch_ln_modulate(p.x, Dm, p.mod, 3 * int64_t(Dm), hi, lo, M, S, Dm, p.eps, st))
+    if (!launch_ln_modulate(p.x, Dm, p.mod, 3 * int64_t(Dm), hi, lo, M, S, Dm, p.eps, st, p.x,
+                            p.res_y, p.res_y ? p.res_mod + 2 * int64_t(Dm) : nullptr,
+                            3 * int64_t(Dm)))
         return false;
     if (!launch_linear_terms(hi, lo, p.wq, Dm, q, HD, int(M), HD, Dm, st))
         return false;
@@ -306,6 +329,9 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
     // read and write the residual again), or a shape the library GEMM does
     // not take with a per-channel scale: the projection into y, then a
     // residual pass.
+    if (p.defer_y)  // the next sub-layer's norm pass applies x += gate * y
+        return launch_linear(o, HD, p.wo, HD, p.defer_y, Dm, int(M), Dm, HD, !p.bf16, lin, s.lin,
+                             st);
     if (p.bf16 && linear_residual_supported(S, Dm, HD, p.wo, HD, p.x, Dm))
         return launch_linear_residual(o, HD, p.wo, HD, p.x, Dm, p.mod + 2 * int64_t(Dm),
                                       3 * int64_t(Dm), B, S, Dm, HD, lin, s.lin, st);

@@ -195,6 +195,12 @@ struct BlockProblem {
     int B = 0, S = 0, Dm = 0, H = 0, D = 0;
     float eps = 1e-6f;
     bool bf16 = false;
+    // Deferred residuals between sub-layers (optional): res_y/res_mod is the
+    // previous sub-layer's output and modulation, applied (x += gate * y) by
+    // this sub-layer's norm pass; with defer_y set, this sub-layer writes its
+    // output projection there and leaves x for the next norm pass.
+    const float *res_y = nullptr, *res_mod = nullptr;
+    float *defer_y = nullptr;
 };
 size_t attention_block_scratch_bytes(int B, int S, int Dm, int H, int D, int Bk, int S_kv,
                                      bool bf16, bool cross);
@@ -203,9 +209,12 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
 // terms (hi, and lo unless null) of the projection GEMM's input.  Row r
 // belongs to batch entry r / S, whose shift and scale are mod[b*mod_ld + :Dm]
 // and mod[b*mod_ld + Dm : 2*Dm].
+// res_y != null: first x += gate[b] * res_y (gate at res_gate + b*res_ld,
+// res_y dense [M][Dm]), written back to x (res_x must be x).
 bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t mod_ld,
                         uint16_t *hi, uint16_t *lo, int64_t M, int S, int Dm, float eps,
-                        hipStream_t st);
+                        hipStream_t st, float *res_x = nullptr, const float *res_y = nullptr,
+                        const float *res_gate = nullptr, int64_t res_ld = 0);
 // x += gate[b] * y for rows of S per batch entry.
 bool launch_gate_residual(float *x, const float *y, const float *mod, int64_t M, int S, int Dm,
                           hipStream_t st);
@@ -213,9 +222,11 @@ bool launch_gate_residual(float *x, const float *y, const float *mod, int64_t M,
 // ---- MLP sub-layer of a DiT block (dit.hip): x += gate[b] * layer2(gelu(
 // layer1(LN(x)*(1+scale[b]) + shift[b]))), mod [B][3][Dm], w1 [hidden][Dm],
 // w2 [Dm][hidden] bf16 bits.
+// res_y/res_mod and defer_y: deferred residuals as in BlockProblem.
 size_t mlp_block_scratch_bytes(int B, int S, int Dm, int hidden, bool bf16);
 bool run_mlp_block(float *x, const float *mod, const uint16_t *w1, const uint16_t *w2, int B,
                    int S, int Dm, int hidden, float eps, bool bf16, void *scratch,
-                   size_t scratch_bytes, hipStream_t st);
+                   size_t scratch_bytes, hipStream_t st, const float *res_y = nullptr,
+                   const float *res_mod = nullptr, float *defer_y = nullptr);
 
 }  // namespace anima_hip

@@ -339,7 +339,8 @@ size_t mlp_block_scratch_bytes(int B, int S, int Dm, int hidden, bool bf16)
 // layernorm(x) * (1 + scale[b]) + shift[b]))), mod [B][3][Dm].
 bool run_mlp_block(float *x, const float *mod, const uint16_t *w1, const uint16_t *w2, int B,
                    int S, int Dm, int hidden, float eps, bool bf16, void *scratch,
-                   size_t scratch_bytes, hipStream_t st)
+                   size_t scratch_bytes, hipStream_t st, const float *res_y,
+                   const float *res_mod, float *defer_y)
 {
     const int64_t M = int64_t(B) * S;
     if (M == 0)
@@ -364,7 +365,8 @@ bool run_mlp_block(float *x, const float *mod, const uint16_t *w1, const uint16_
     uint16_t *glo = bf16 ? nullptr : ghi + (s.g / 2) / sizeof(uint16_t);
     float *y = reinterpret_cast<float *>(take(s.y));
 
-    if (!launch_ln_modulate(x, Dm, mod, 3 * int64_t(Dm), hi, lo, M, S, Dm, eps, st) ||
+    if (!launch_ln_modulate(x, Dm, mod, 3 * int64_t(Dm), hi, lo, M, S, Dm, eps, st, x, res_y,
+                            res_y ? res_mod + 2 * int64_t(Dm) : nullptr, 3 * int64_t(Dm)) ||
         !launch_linear_terms(hi, lo, w1, Dm, h, hidden, int(M), hidden, Dm, st))
         return false;
     GeluArgs ga;
@@ -375,6 +377,8 @@ bool run_mlp_block(float *x, const float *mod, const uint16_t *w1, const uint16_
     hipLaunchKernelGGL(gelu_terms_kernel, dim3(grid1(ga.n8)), dim3(256), 0, st, ga);
     if (!hip_ok(hipGetLastError(), "gelu_terms_kernel launch"))
         return false;
+    if (defer_y)  // the next norm pass applies x += gate * y
+        return launch_linear_terms(ghi, glo, w2, hidden, defer_y, Dm, int(M), Dm, hidden, st);
     // layer2 and the gated residual: fused in bf16 mode (see block.hip).
     if (bf16 && linear_residual_supported(S, Dm, hidden, w2, hidden, x, Dm))
         return launch_linear_residual_terms(ghi, w2, hidden, x, Dm, mod + 2 * int64_t(Dm),
@@ -472,7 +476,7 @@ void grid_of(int T, int H, int W, int &Hp, int &Wp, int64_t &S)
 
 // Scratch regions of one forward, 256-byte aligned, in order.
 struct DitScratch {
-    size_t x, patch, f, arena, total;
+    size_t x, y, patch, f, arena, total;
 };
 
 DitScratch dit_scratch(const anima_hip_dit *d, int B, int64_t S)
@@ -482,6 +486,7 @@ DitScratch dit_scratch(const anima_hip_dit *d, int B, int64_t S)
     const bool bf16 = d->bf16;
     DitScratch s{};
     s.x = round_up256(size_t(M) * c.dim * 4);
+    s.y = s.x;
     s.patch = round_up256(size_t(M) * d->kp_in * 2) * 2;
     s.f = round_up256(size_t(M) * 4 * c.out_channels * 4);
     size_t arena = attention_block_scratch_bytes(B, int(S), c.dim, c.heads, c.head_dim, B, int(S),
@@ -492,7 +497,7 @@ DitScratch dit_scratch(const anima_hip_dit *d, int B, int64_t S)
     arena = std::max(arena, mlp_block_scratch_bytes(B, int(S), c.dim, c.mlp_hidden, bf16));
     arena = std::max(arena, round_up256(size_t(M) * linear_terms_ld(c.dim) * 2) * 2);
     s.arena = round_up256(arena);
-    s.total = s.x + s.patch + s.f + s.arena;
+    s.total = s.x + s.y + s.patch + s.f + s.arena;
     return s;
 }
 
@@ -537,10 +542,11 @@ bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, i
                     "aligned");
     char *base = static_cast<char *>(scratch);
     float *xr = reinterpret_cast<float *>(base);
-    uint16_t *phi = reinterpret_cast<uint16_t *>(base + s.x);
+    float *yp = reinterpret_cast<float *>(base + s.x);  // pending sub-layer output
+    uint16_t *phi = reinterpret_cast<uint16_t *>(base + s.x + s.y);
     uint16_t *plo = d->bf16 ? nullptr : phi + (s.patch / 2) / 2;
-    float *f = reinterpret_cast<float *>(base + s.x + s.patch);
-    void *arena = base + s.x + s.patch + s.f;
+    float *f = reinterpret_cast<float *>(base + s.x + s.y + s.patch);
+    void *arena = base + s.x + s.y + s.patch + s.f;
     const int D = c.dim;
 
     // Timestep embedding, its MLP (the AdaLN-LoRA term), the normalised
@@ -591,8 +597,11 @@ bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, i
         !launch_linear_terms(phi, plo, d->x_emb, d->kp_in, xr, D, int(M), D, d->kp_in, st))
         return false;
 
-    // The blocks (numpy_dit.py:232-253).
+    // The blocks (numpy_dit.py:232-253).  Each sub-layer writes its output
+    // projection to yp as one GEMM over all B*S rows; the next sub-layer's
+    // (or the final layer's) LayerNorm pass applies x += gate * yp first.
     const int64_t mod_stride = int64_t(c.max_batch) * 3 * D;  // one modulation's rows
+    const float *pend_mod = nullptr;                           // modulation owning yp
     for (int i = 0; i < c.blocks; ++i) {
         const BlockWeights &bw = d->blk[i];
         BlockProblem p;
@@ -612,8 +621,13 @@ bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, i
         p.q_norm_w = bw.sa_qn;
         p.k_norm_w = bw.sa_kn;
         p.freqs = freqs;
+        p.res_y = pend_mod ? yp : nullptr;
+        p.res_mod = pend_mod;
+        p.defer_y = yp;
         if (!run_attention_block(p, arena, s.arena, st))
             return false;
+        p.res_y = yp;
+        p.res_mod = p.mod;
         p.mod = d->mods + (3 * i + 1) * mod_stride;
         p.wq = bw.cx_q;
         p.wk = p.wv = nullptr;
@@ -625,10 +639,12 @@ bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, i
         p.v_prep = bw.ctx_v;
         p.Bk = d->ctx_B;
         p.S_kv = d->ctx_S;
+        const float *mlp_mod = d->mods + (3 * i + 2) * mod_stride;
         if (!run_attention_block(p, arena, s.arena, st) ||
-            !run_mlp_block(xr, d->mods + (3 * i + 2) * mod_stride, bw.fc1, bw.fc2, B, int(S), D,
-                           c.mlp_hidden, 1e-6f, d->bf16, arena, s.arena, st))
+            !run_mlp_block(xr, mlp_mod, bw.fc1, bw.fc2, B, int(S), D, c.mlp_hidden, 1e-6f,
+                           d->bf16, arena, s.arena, st, yp, p.mod, yp))
             return false;
+        pend_mod = mlp_mod;
     }
 
     // Final layer: LN + modulate (shift, scale) and the output linear.
@@ -636,7 +652,9 @@ bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, i
     const size_t tbytes = round_up256(size_t(M) * linear_terms_ld(D) * 2);
     uint16_t *tlo = d->bf16 ? nullptr : thi + tbytes / 2;
     const float *fmod = d->mods + int64_t(3 * c.blocks) * mod_stride;
-    if (!launch_ln_modulate(xr, D, fmod, 3 * int64_t(D), thi, tlo, M, int(S), D, 1e-6f, st) ||
+    if (!launch_ln_modulate(xr, D, fmod, 3 * int64_t(D), thi, tlo, M, int(S), D, 1e-6f, st, xr,
+                            pend_mod ? yp : nullptr,
+                            pend_mod ? pend_mod + 2 * int64_t(D) : nullptr, 3 * int64_t(D)) ||
         !launch_linear_terms(thi, tlo, d->fin_lin, D, f, 4 * c.out_channels, int(M),
                              4 * c.out_channels, D, st))
         return false;
