@@ -170,3 +170,26 @@ def test_create_and_call_errors(gold):
         ok = lib.anima_hip_dit_forward_dev(m.handle, x.ptr, 16 * 70, sig, 3, 1, 7, 10, x.ptr,
                                            out.ptr, x.ptr, 1 << 30, None)
         assert not ok and "batch" in _lib.last_error()
+
+
+def test_model_from_checkpoint_file(gold, tmp_path):
+    """The reference's on-disk format: safetensors with the "net." prefix,
+    BF16 linear and norm weights (as the checkpoint stores them) and a tensor
+    the model does not read; AnimaDiT(Weights(path)) computes exactly what the
+    device-table model with the same values does."""
+    import safetensors_file
+    g, cfg, w = gold
+    tensors = {"net." + k: ("BF16", a if a.ndim == 2 else oracle.f32_to_bf16_bits(a))
+               for k, a in w.items()}
+    tensors["net.pos_embedder.seq"] = ("F32", np.arange(8, dtype=np.float32))
+    path = tmp_path / "dit.safetensors"
+    safetensors_file.write(path, tensors, metadata={"format": "pt"})
+    print("dit from file", flush=True)
+    with rt.Weights(path) as store:
+        with AnimaDiT(store, _config(cfg), rt.F32) as m:
+            a = m.forward(g["fwd_x"], g["fwd_sigma"], g["fwd_ctx"])
+    table, keep = _device_table(w)
+    with AnimaDiT(table, _config(cfg), rt.F32) as m:
+        b = m.forward(g["fwd_x"], g["fwd_sigma"], g["fwd_ctx"])
+    np.testing.assert_array_equal(a, b)
+    assert _err(a, g["fwd_out"]) <= TOL[rt.F32]
