@@ -56,6 +56,7 @@ struct Bf16Args {
     int H, S_q, S_kv, n_qtiles;
     float c;  // scale * log2(e), > 0
     int causal;
+    int dma32;  // K/V^T tile rows fit 32-bit byte offsets from the tile start
     FlashSplitArgs split;  // n == 1: write O; n > 1: write this split's partial
 };
 
@@ -77,6 +78,17 @@ __device__ __forceinline__ void dma16(const u16 *src, u16 *lds)
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                  :
                  : "s"(m0), "v"(src)
+                 : "memory", "m0");
+}
+// The same copy addressed as a wave-uniform 64-bit base (SGPRs) plus this
+// lane's 32-bit byte offset, so no per-lane 64-bit address arithmetic runs.
+__device__ __forceinline__ void dma16s(const void *base, unsigned voff, u16 *lds)
+{
+    const unsigned m0 = static_cast<unsigned>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)lds));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(m0), "v"(voff), "s"(base)
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -117,18 +129,15 @@ __device__ __forceinline__ float row_pair_max(float v)
 
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
-// Sum of the 16 bf16 values of two P operands, in f32 (v_dot2_f32_bf16 with
-// a vector of ones).
-__device__ __forceinline__ float row_sum16(const bf16x8 &p, const bf16x8 &q)
+// Adds the 8 bf16 values of a P operand to the running sum acc, in f32
+// (v_dot2_f32_bf16 with a vector of ones).
+__device__ __forceinline__ float row_sum8(const bf16x8 &p, float acc)
 {
     const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-    float a = 0.0f, b = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-        a = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{p[i], p[i + 1]}, one, a, false);
-        b = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{q[i], q[i + 1]}, one, b, false);
-    }
-    return a + b;
+    for (int i = 0; i < 8; i += 2)
+        acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{p[i], p[i + 1]}, one, acc, false);
+    return acc;
 }
 
 __device__ __forceinline__ bf16x8 pack8(const f32x16 &s, int base)
@@ -206,25 +215,50 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     //   V^T [128 d][64 keys]: chunk c of d row r at chunk c ^ ((r >> 1) & 7).
     // Keys past S_kv copy row S_kv - 1 (their scores are masked); V^T is
     // zero-padded in HBM to whole tiles.
+    // This lane's source chunks: window w = wave*DMA + i of a tile, chunk
+    // slot f = 64w + lane; byte offsets from the tile's first row (whole
+    // tiles, with dma32) or the row index for the clamped path.
+    unsigned koff_b[DMA], voff_b[DMA];
+    int krow[DMA], kchk[DMA];
+#pragma unroll
+    for (int i = 0; i < DMA; ++i) {
+        const int f = (wave * DMA + i) * 64 + lane;
+        const int r = f >> 4, c = (f & 15) ^ (r & 15);
+        krow[i] = r;
+        kchk[i] = c;
+        koff_b[i] = unsigned(r * a.ks + 8 * c) * 2u;
+        const int rv = f >> 3, cv = (f & 7) ^ ((rv >> 1) & 7);
+        voff_b[i] = unsigned(rv * a.vd + 8 * cv) * 2u;
+    }
     auto dma_k = [&](int t, int stage) {
         const int key0 = (j0 + t) * kBN;
+        if (a.dma32 && key0 + kBN <= a.S_kv) {
+            const u16 *base = kp + int64_t(key0) * a.ks;
 #pragma unroll
-        for (int i = 0; i < DMA; ++i) {
-            const int w = wave * DMA + i;  // 1 KiB window of the tile
-            const int f = w * 64 + lane;   // 16-byte chunk slot
-            const int r = f >> 4, c = (f & 15) ^ (r & 15);
-            const int key = min(key0 + r, a.S_kv - 1);
-            dma16(kp + key * a.ks + 8 * c, &Ks[stage][w * 512]);
+            for (int i = 0; i < DMA; ++i)
+                dma16s(base, koff_b[i], &Ks[stage][(wave * DMA + i) * 512]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < DMA; ++i) {
+                const int key = min(key0 + krow[i], a.S_kv - 1);
+                dma16(kp + key * a.ks + 8 * kchk[i], &Ks[stage][(wave * DMA + i) * 512]);
+            }
         }
     };
     auto dma_v = [&](int t, int stage) {
         const int key0 = (j0 + t) * kBN;
+        if (a.dma32) {
+            const u16 *base = vp + key0;
 #pragma unroll
-        for (int i = 0; i < DMA; ++i) {
-            const int w = wave * DMA + i;
-            const int f = w * 64 + lane;
-            const int r = f >> 3, c = (f & 7) ^ ((r >> 1) & 7);
-            dma16(vp + r * a.vd + key0 + 8 * c, &Vs[stage][w * 512]);
+            for (int i = 0; i < DMA; ++i)
+                dma16s(base, voff_b[i], &Vs[stage][(wave * DMA + i) * 512]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < DMA; ++i) {
+                const int f = (wave * DMA + i) * 64 + lane;
+                const int r = f >> 3, c = (f & 7) ^ ((r >> 1) & 7);
+                dma16(vp + r * a.vd + key0 + 8 * c, &Vs[stage][(wave * DMA + i) * 512]);
+            }
         }
     };
     // Element offsets of this lane's fragments inside a stage: K rows col and
@@ -248,7 +282,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
 
     f32x16 o0 = {}, o1 = {}, o2 = {}, o3 = {};
     float m = -INFINITY;
-    float l = 0.0f;
+    float l = 0.0f, l2 = 0.0f;  // two running row sums (chains of v_dot2)
     // Scores of two consecutive tiles; the loop below is unrolled by two so
     // the pair being consumed and the pair being produced swap roles without
     // register copies.
@@ -324,6 +358,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
                 m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
             m = m_new;
             l *= alpha;
+            l2 *= alpha;
             o0 *= alpha;
             o1 *= alpha;
             o2 *= alpha;
@@ -376,7 +411,8 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
         const bf16x8 p10 = pack8(sc1, 0), p11 = pack8(sc1, 8);
         // Row sum of the bf16 probabilities the P.V MFMAs consume, two per
         // v_dot2_f32_bf16.
-        l += row_sum16(p00, p01) + row_sum16(p10, p11);
+        l = row_sum8(p10, row_sum8(p00, l));
+        l2 = row_sum8(p11, row_sum8(p01, l2));
 
         // P.V of tile j, reading the V^T fragments of block blk+1 ahead;
         // meanwhile the VALU takes the max of tile j+1.
@@ -421,6 +457,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     if (j < ntiles)
         tile(j, sa0, sa1, sb0, sb1);
 
+    l += l2;
     l += __shfl_xor(l, 32);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     if (qrow < a.S_q) {
@@ -543,6 +580,10 @@ bool launch_flash_bf16(const FlashProblem &p, hipStream_t st, void *part, size_t
     a.S_kv = p.S_kv;
     a.c = p.scale * kLog2e;
     a.causal = p.causal ? 1 : 0;
+    // Byte offsets of a tile's rows from its first row: K rows r < 64 at
+    // r*ks, V^T d-rows r < 128 at r*Sp, plus 256 bytes.
+    a.dma32 = (int64_t(kBN) * p.ks.s * 2 + 256 < (int64_t(1) << 31)) &&
+              (int64_t(kD) * sp * 2 + 256 < (int64_t(1) << 31));
     const FlashPlan pl = flash_plan(BH, p.S_q, p.S_kv, p.D);
     a.split = flash_split_args(pl, BH, p.S_q, part, part_bytes);
     if (!(pl.waves == 4 ? launch_d128<4>(a, BH, st) : launch_d128<8>(a, BH, st)))
