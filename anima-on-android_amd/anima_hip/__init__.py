@@ -1,15 +1,16 @@
 """anima_hip -- MI355X (gfx950) attention path of the Anima 2B DiT.
 
 Torch-free host interface over libanima_hip.so:
-  * `rt`: anima_rt drop-in functions and the `AnimaRT` class (NumpyRT mirror);
+  * `rt`: anima_rt drop-in functions, `AnimaRT` (NumpyRT mirror) and `AnimaVK`
+    (NumpyVK mirror);
+  * `dit`: the whole DiT on the device, `AnimaDiT` (NumpyDiT drop-in);
   * `rope`: the host-built 3D RoPE table;
-  * `workloads`: seeded synthetic inputs of the benchmark configurations.
 """
 from . import _lib
 from ._lib import AnimaHipError, LIB_PATH, last_error, load
 from . import rope, rt
 from .rope import generate_rope_freqs
-from .rt import AnimaRT
+from .rt import AnimaRT, AnimaVK
 
-__all__ = ["AnimaHipError", "AnimaRT", "LIB_PATH", "generate_rope_freqs", "last_error", "load",
-           "rope", "rt"]
+__all__ = ["AnimaHipError", "AnimaRT", "AnimaVK", "LIB_PATH", "generate_rope_freqs", "last_error",
+           "load", "rope", "rt"]

@@ -24,6 +24,11 @@ SIGNATURES = {
     "anima_rt_run_sdpa": (_B, [_P] * 4 + [_I] * 4 + [_F, _B]),
     "anima_rt_run_rmsnorm": (_B, [_P, _P, _P, _I, _I, _F]),
     "anima_rt_run_rope": (_B, [_P, _P, _P, _I, _I, _I]),
+    "anima_rt_run_gelu": (_B, [_P, _P, _I]),
+    "anima_rt_run_silu": (_B, [_P, _P, _I]),
+    "anima_rt_run_layernorm": (_B, [_P, _P, _I, _I, _F]),
+    "anima_rt_run_softmax": (_B, [_P, _P, _I, _I]),
+    "anima_rt_run_bias_add": (_B, [_P, _P, _I, _I]),
     "anima_rt_run_gemm_fp32": (_B, [_P] * 3 + [_I] * 3),
     "anima_rt_run_gemm_bf16": (_B, [_P] * 3 + [_I] * 3),
     "anima_hip_last_error": (ct.c_char_p, []),

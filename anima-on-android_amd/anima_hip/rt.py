@@ -1,8 +1,9 @@
 """Torch-free host interface of the attention path, on numpy buffers.
 
 `AnimaRT` is a drop-in for the ``rt`` object NumpyDiT calls
-(``NumpyRT`` in scripts/phone_pipeline_nd.py:46-68): the same method names,
-argument meanings and array layouts, backed by libanima_hip.so on the GPU.
+(``NumpyRT`` in scripts/phone_pipeline_nd.py:46-68) and `AnimaVK` for its
+GEMM engine ``vk`` (NumpyVK, :69-72): the same method names, argument
+meanings and array layouts, backed by libanima_hip.so on the GPU.
 One deliberate difference: a false return from the library raises
 `AnimaHipError` (the reference's ``run_sdpa`` ignores the return value,
 phone_pipeline_nd.py:67, and would hand back zeros).
@@ -95,6 +96,52 @@ def rmsnorm(x, w=None, eps=1e-6) -> np.ndarray:
     ok = _lib.load().anima_rt_run_rmsnorm(_p(x), _p(w), _p(out), M, D, ct.c_float(eps))
     _lib.check(ok, "anima_rt_run_rmsnorm")
     return out
+
+
+def _unary(name, x, *extra):
+    x = _f32(x)
+    out = np.zeros_like(x)
+    _lib.check(getattr(_lib.load(), "anima_rt_run_" + name)(_p(x), _p(out), *extra),
+               "anima_rt_run_" + name)
+    return out
+
+
+def gelu(x) -> np.ndarray:
+    """anima_rt_run_gelu, exact erf form (anima_rt.cpp:24-27). Needs init()."""
+    return _unary("gelu", x, int(np.size(x)))
+
+
+def silu(x) -> np.ndarray:
+    """anima_rt_run_silu (anima_rt.cpp:29-32). Needs init()."""
+    return _unary("silu", x, int(np.size(x)))
+
+
+def layernorm(x, eps=1e-6) -> np.ndarray:
+    """anima_rt_run_layernorm over the last axis, no affine (anima_rt.cpp:36-43).
+    Needs init()."""
+    x = _f32(x)
+    D = x.shape[-1]
+    return _unary("layernorm", x, x.size // D if D else 0, D, ct.c_float(eps))
+
+
+def softmax(x) -> np.ndarray:
+    """anima_rt_run_softmax over the last axis (anima_rt.cpp:52-57). Needs init()."""
+    x = _f32(x)
+    D = x.shape[-1]
+    return _unary("softmax", x, x.size // D if D else 0, D)
+
+
+def bias_add(c, bias) -> np.ndarray:
+    """anima_rt_run_bias_add (gemm_backend.cpp:173-183): c[i, :] += bias, in
+    place on a C-contiguous float32 matrix; returns c."""
+    if c.dtype != np.float32 or not c.flags.c_contiguous or c.ndim != 2:
+        raise ValueError("bias_add: c must be a C-contiguous float32 matrix")
+    b = None if bias is None else _f32(bias)
+    if b is not None and b.shape != (c.shape[1],):
+        raise ValueError("bias_add: bias must have one entry per column")
+    _lib.check(_lib.load().anima_rt_run_bias_add(_p(c), _p(b), c.shape[0], c.shape[1]),
+               "anima_rt_run_bias_add")
+    return c
 
 
 def rope(t, freqs) -> np.ndarray:
@@ -311,6 +358,16 @@ class AnimaRT:
         x = np.asarray(x, np.float32)
         return rmsnorm(x, self._w(key), eps)
 
+    def run_layernorm(self, x, D):
+        """[M, D] rows, eps 1e-6, no affine (NumpyRT.run_layernorm)."""
+        return layernorm(np.asarray(x, np.float32).reshape(-1, D), 1e-6)
+
+    def run_gelu(self, x):
+        return gelu(np.asarray(x, np.float32).reshape(-1))
+
+    def run_silu(self, x):
+        return silu(np.asarray(x, np.float32).reshape(-1))
+
     def run_sdpa(self, q, k, v):
         """[B,H,S,D] q/k/v -> [B,H,S_q,D], scale 1/sqrt(D), non-causal."""
         B, H, Sq, D = q.shape
@@ -333,3 +390,47 @@ class AnimaRT:
             q.shape[1], q.shape[3] // 2, 2, 2)
         return attention(q, k, v, self._w(f"{prefix}.q_norm"), self._w(f"{prefix}.k_norm"),
                          freqs, mode=mode)
+
+
+class AnimaVK:
+    """Drop-in for NumpyDiT's GEMM engine ``vk`` (NumpyVK,
+    scripts/phone_pipeline_nd.py:69-72, over vk_run_gemm of
+    vulkan/hybrid_engine.cpp): ``vk_run_gemm(name, x, out, M, N, K)`` writes
+    out[M, N] = x[M, K] . W[name]^T with the named bf16 weight resident on the
+    GPU (a ``Weights`` store).  mode F32 feeds x as exact hi + lo bf16 terms,
+    BF16 rounds it.  Raises RuntimeError on failure, like NumpyVK."""
+
+    def __init__(self, weights, mode=F32):
+        from .dit import DeviceArray
+        self._w = weights
+        self._mode = int(mode)
+        self._lib = _lib.load()
+        self._dev = DeviceArray
+        self._bufs = {}
+
+    def _buf(self, role, nbytes):
+        b = self._bufs.get(role)
+        if b is None or b.nbytes < nbytes:
+            if b is not None:
+                b.close()
+            b = self._bufs[role] = self._dev(max(int(nbytes), 256))
+        return b
+
+    def vk_run_gemm(self, name, x, out, M, N, K):
+        dt, shape = self._w.info(name)
+        if dt != "BF16" or tuple(shape) != (N, K):
+            raise RuntimeError(f"vk_run_gemm({name}) failed: weight is {dt} {shape}, "
+                               f"expected BF16 ({N}, {K})")
+        x = _f32(x).reshape(M, K)
+        if out.dtype != np.float32 or out.size != M * N or not out.flags.c_contiguous:
+            raise RuntimeError(f"vk_run_gemm({name}) failed: out must be float32 [{M}, {N}]")
+        xd = self._buf("x", x.nbytes)
+        xd.upload(x)
+        od = self._buf("out", out.nbytes)
+        n = self._lib.anima_hip_linear_scratch_bytes(M, K, self._mode)
+        sd = self._buf("scratch", n)
+        ok = self._lib.anima_hip_linear_dev(xd.ptr, K, self._w.device(name), K, od.ptr, N, M, N,
+                                            K, self._mode, sd.ptr, n, None)
+        if not ok:
+            raise RuntimeError(f"vk_run_gemm({name}) failed: {_lib.last_error()}")
+        out.reshape(-1)[:] = od.download((M * N,))

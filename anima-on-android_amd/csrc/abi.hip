@@ -367,6 +367,88 @@ bool anima_rt_run_rmsnorm(const float *x, const float *w, float *out, int m, int
     return sync(st);
 }
 
+}  // extern "C"
+
+namespace {
+
+// Host-pointer form of a one-input, one-output operator over n floats: the
+// input through the runtime's workspace, `run` on the device, the output
+// back; synchronous like the reference.
+template <typename Run>
+bool host_unary(const char *what, const float *x, float *out, int64_t n, Run run)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!r.user_init)
+        return fail(std::string("anima_rt_run_") + what + ": anima_rt_init() has not been called");
+    if (n <= 0)
+        return true;
+    if (!x || !out)
+        return fail(std::string(what) + ": null pointer");
+    const hipStream_t st = r.stream;
+    if (!r.q.reserve(f32_bytes(n), "workspace x") || !r.o.reserve(f32_bytes(n), "workspace y") ||
+        !h2d(r.q.p, x, f32_bytes(n), st) ||
+        !run(static_cast<const float *>(r.q.p), static_cast<float *>(r.o.p), st) ||
+        !d2h(out, r.o.p, f32_bytes(n), st))
+        return false;
+    return sync(st);
+}
+
+}  // namespace
+
+extern "C" {
+
+bool anima_rt_run_gelu(const float *x, float *out, int n)
+{
+    return host_unary("gelu", x, out, n, [&](const float *xd, float *yd, hipStream_t st) {
+        return launch_gelu(xd, yd, n, st);
+    });
+}
+
+bool anima_rt_run_silu(const float *x, float *out, int n)
+{
+    return host_unary("silu", x, out, n, [&](const float *xd, float *yd, hipStream_t st) {
+        return launch_silu(xd, yd, n, st);
+    });
+}
+
+bool anima_rt_run_layernorm(const float *x, float *out, int m, int d, float eps)
+{
+    const int64_t n = (m > 0 && d > 0) ? int64_t(m) * d : 0;
+    return host_unary("layernorm", x, out, n, [&](const float *xd, float *yd, hipStream_t st) {
+        return launch_layernorm_rows(xd, yd, m, d, eps, st);
+    });
+}
+
+bool anima_rt_run_softmax(const float *x, float *out, int outer, int dim)
+{
+    const int64_t n = (outer > 0 && dim > 0) ? int64_t(outer) * dim : 0;
+    return host_unary("softmax", x, out, n, [&](const float *xd, float *yd, hipStream_t st) {
+        return launch_softmax_rows(xd, yd, outer, dim, st);
+    });
+}
+
+bool anima_rt_run_bias_add(float *C, const float *bias, int M, int N)
+{
+    if (!bias || M <= 0 || N <= 0)
+        return true;
+    if (!C)
+        return fail("bias_add: null pointer");
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (!ensure_ready(r))
+        return false;
+    const int64_t n = int64_t(M) * N;
+    const hipStream_t st = r.stream;
+    if (!r.o.reserve(f32_bytes(n), "workspace C") || !r.w0.reserve(f32_bytes(N), "workspace bias") ||
+        !h2d(r.o.p, C, f32_bytes(n), st) || !h2d(r.w0.p, bias, f32_bytes(N), st) ||
+        !launch_bias_add(static_cast<float *>(r.o.p), static_cast<const float *>(r.w0.p), M, N,
+                         st) ||
+        !d2h(C, r.o.p, f32_bytes(n), st))
+        return false;
+    return sync(st);
+}
+
 bool anima_rt_run_rope(const float *t, const float *freqs, float *out, int N, int S, int D)
 {
     Runtime &r = rt();

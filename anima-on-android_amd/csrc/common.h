@@ -219,6 +219,15 @@ bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t m
 bool launch_gate_residual(float *x, const float *y, const float *mod, int64_t M, int S, int Dm,
                           hipStream_t st);
 
+// ---- Element-wise and row operators (ops.hip), device pointers ----
+// GELU (exact erf form), SiLU, LayerNorm without affine over rows of D,
+// softmax over rows of D, and C[i][j] += bias[j] for an M x N matrix.
+bool launch_gelu(const float *x, float *y, int64_t n, hipStream_t st);
+bool launch_silu(const float *x, float *y, int64_t n, hipStream_t st);
+bool launch_layernorm_rows(const float *x, float *y, int64_t M, int D, float eps, hipStream_t st);
+bool launch_softmax_rows(const float *x, float *y, int64_t M, int D, hipStream_t st);
+bool launch_bias_add(float *c, const float *bias, int64_t M, int N, hipStream_t st);
+
 // ---- MLP sub-layer of a DiT block (dit.hip): x += gate[b] * layer2(gelu(
 // layer1(LN(x)*(1+scale[b]) + shift[b]))), mod [B][3][Dm], w1 [hidden][Dm],
 // w2 [Dm][hidden] bf16 bits.

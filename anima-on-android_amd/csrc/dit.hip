@@ -13,7 +13,7 @@
 //                     sigma only, so the 28 x 3 + 1 modulations run as two
 //                     launches (first layers, then second layers plus the
 //                     AdaLN-LoRA term) before the blocks;
-//   silu_kernel       anima_rt_run_silu (silu_kernel.h:9-17);
+//   launch_silu       anima_rt_run_silu (silu_kernel.h:9-17), from ops.hip;
 //   patchify_kernel   _pad_to_patch_size + the zero padding-mask channel +
 //                     _rearrange_patchify (numpy_dit.py:10-22, 92-95),
 //                     written directly as the bf16 terms of the patch GEMM;
@@ -94,16 +94,6 @@ __global__ __launch_bounds__(256) void timestep_kernel(TimestepArgs a)
     const float e = (-9.21034037197618f * float(j)) / float(half);
     const float arg = a.sigma[b] * expf(e);
     a.out[int64_t(b) * a.D + i] = i < half ? cosf(arg) : sinf(arg);
-}
-
-// ---- SiLU: x / (1 + exp(-x)) ----------------------------------------------
-__global__ __launch_bounds__(256) void silu_kernel(const float *x, float *y, int64_t n)
-{
-    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i < n) {
-        const float v = x[i];
-        y[i] = v / (1.0f + expf(-v));
-    }
 }
 
 // ---- small-batch linear layers -------------------------------------------
@@ -284,14 +274,6 @@ __global__ __launch_bounds__(256) void widen_kernel(const uint16_t *in, float *o
 }
 
 unsigned grid1(int64_t n) { return unsigned((n + 255) / 256); }
-
-bool launch_silu(const float *x, float *y, int64_t n, hipStream_t st)
-{
-    if (n == 0)
-        return true;
-    hipLaunchKernelGGL(silu_kernel, dim3(grid1(n)), dim3(256), 0, st, x, y, n);
-    return hip_ok(hipGetLastError(), "silu_kernel launch");
-}
 
 bool launch_gemv(const GemvJob *jobs, int njobs, int maxN, int B, int K, hipStream_t st)
 {

@@ -66,6 +66,27 @@ bool anima_rt_run_sdpa(const float *Q, const float *K, const float *V, float *ou
  * succeeded first (anima_rt.cpp:47). */
 bool anima_rt_run_rmsnorm(const float *x, const float *w, float *out, int m, int d, float eps);
 
+/* Replace anima_rt_run_gelu / anima_rt_run_silu (anima_rt.cpp:24-32 ->
+ * gelu_kernel.h:13-23, exact erf form, and silu_kernel.h:9-17): out[i] =
+ * f(x[i]) for i < n.  False (with a message) before anima_rt_init(), as the
+ * reference without a backend; n <= 0 does nothing. */
+bool anima_rt_run_gelu(const float *x, float *out, int n);
+bool anima_rt_run_silu(const float *x, float *out, int n);
+
+/* Replaces anima_rt_run_layernorm (anima_rt.cpp:36-43 -> layernorm_kernel.h:13-33):
+ * LayerNorm without affine parameters over the rows of x [m, d].  False before
+ * anima_rt_init(). */
+bool anima_rt_run_layernorm(const float *x, float *out, int m, int d, float eps);
+
+/* Replaces anima_rt_run_softmax (anima_rt.cpp:52-57 -> softmax_kernel.h:16-40):
+ * softmax over the last axis of x [outer, dim].  False before anima_rt_init(). */
+bool anima_rt_run_softmax(const float *x, float *out, int outer, int dim);
+
+/* Replaces anima_rt_run_bias_add (gemm_backend.cpp:173-183): C[i][j] += bias[j]
+ * on host memory C [M, N]; a NULL bias does nothing.  Needs no init, like the
+ * reference. */
+bool anima_rt_run_bias_add(float *C, const float *bias, int M, int N);
+
 /* Replaces anima_rt_run_rope (anima_rt.cpp:160-164 -> rope_kernel,
  * anima_rt/include/cpu/rope_kernel.h:65-97).  t,out: [N, S, D];
  * freqs: [S, D/2, 2, 2].  Bit-identical to the reference. */

@@ -28,6 +28,8 @@
  *       fp64 two-pass mean/variance.
  *   oracle_silu             -- bit-identical to oracle/_ref anima_rt_run_silu;
  *       fp64 x / (1 + exp(-x)).
+ *   oracle_softmax          -- bit-identical to oracle/_ref anima_rt_run_softmax;
+ *       fp64 exp(x - max) / sum, rows summing to 1.
  *   oracle_gelu             -- bit-identical to oracle/_ref anima_rt_run_gelu;
  *       fp64 x * Phi(x) via math.erf; GELU(0) = 0, GELU(x) - GELU(-x) = x.
  *   oracle_modulate, oracle_gate_residual -- numpy float32 evaluation of the
@@ -408,6 +410,30 @@ void oracle_gelu(const float *x, float *y, int64_t n)
     for (int64_t i = 0; i < n; i++) {
         const float h = x[i] * 0.5f;
         y[i] = h * (1.0f + erff(x[i] * alpha));
+    }
+}
+
+/* Softmax over the last axis (anima_rt/include/cpu/softmax_kernel.h:16-40):
+ * max by strict comparison from the first element, exp(x - max) stored and
+ * summed in order, then multiplied by 1/sum. */
+void oracle_softmax(const float *X, float *Y, int64_t outer, int64_t dim)
+{
+    for (int64_t i = 0; i < outer; i++) {
+        const float *x = X + i * dim;
+        float *y = Y + i * dim;
+        float mx = x[0];
+        for (int64_t j = 1; j < dim; j++)
+            if (x[j] > mx)
+                mx = x[j];
+        float sum = 0.0f;
+        for (int64_t j = 0; j < dim; j++) {
+            const float v = expf(x[j] - mx);
+            y[j] = v;
+            sum += v;
+        }
+        const float inv = 1.0f / sum;
+        for (int64_t j = 0; j < dim; j++)
+            y[j] *= inv;
     }
 }
 

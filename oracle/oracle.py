@@ -27,8 +27,13 @@ Pinning status (each function is checked by something other than itself):
       numpy_dit.py's float32 rounding is "parity unpinned" (would need an
       import of the reference) and is covered only to 1 ulp-level tolerance.
   numpy_rope -- same arithmetic as rope (checked bit-identical against it).
-  layernorm, silu -- bit-identical to the compiled reference and the golden
-      vectors it wrote; fp64 two-pass moments / fp64 x/(1+exp(-x)).
+  layernorm, silu, gelu, softmax -- bit-identical to the compiled reference
+      and the golden vectors it wrote; fp64 two-pass moments, x/(1+exp(-x)),
+      x*Phi(x), exp(x - max)/sum.
+  timesteps, patchify, unpatchify, adaln, mlp_block, dit_forward,
+  z_image_sigmas, euler_sample -- bit-identical to the reference's own
+      numpy_dit.py / sampling.py on tests/golden/dit_ref_vectors.npz; closed
+      forms and index identities.
   modulate, gate_residual -- fp64 evaluation within float32 rounding, and
       closed cases (scale = shift = 0 is identity, gate = 0 keeps x).
   attention_block -- composition of the pinned pieces above.
@@ -90,6 +95,8 @@ def oracle_lib():
         lib.oracle_silu.restype = None
         lib.oracle_gelu.argtypes = [_P, _P, _ct.c_int64]
         lib.oracle_gelu.restype = None
+        lib.oracle_softmax.argtypes = [_P, _P, _ct.c_int64, _ct.c_int64]
+        lib.oracle_softmax.restype = None
         lib.oracle_modulate.argtypes = [_P, _P, _P, _P, _I, _ct.c_int64, _ct.c_int64]
         lib.oracle_modulate.restype = None
         lib.oracle_gate_residual.argtypes = [_P, _P, _P, _I, _ct.c_int64, _ct.c_int64]
@@ -125,6 +132,8 @@ def ref_lib():
         lib.anima_rt_run_silu.restype = _ct.c_bool
         lib.anima_rt_run_gelu.argtypes = [_P, _P, _I]
         lib.anima_rt_run_gelu.restype = _ct.c_bool
+        lib.anima_rt_run_softmax.argtypes = [_P, _P, _I, _I]
+        lib.anima_rt_run_softmax.restype = _ct.c_bool
         if not lib.anima_rt_init():
             raise RuntimeError("reference anima_rt_init failed")
         _ref_lib = lib
@@ -206,6 +215,15 @@ def gelu(x):
     x = _f32c(x)
     y = np.empty_like(x)
     oracle_lib().oracle_gelu(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def softmax(x):
+    """Softmax over the last axis restated (softmax_kernel.h:16-40)."""
+    x = _f32c(x)
+    D = x.shape[-1]
+    y = np.empty_like(x)
+    oracle_lib().oracle_softmax(_ptr(x), _ptr(y), x.size // D, D)
     return y
 
 
@@ -337,6 +355,14 @@ def ref_gelu(x):
     x = _f32c(x)
     y = np.zeros_like(x)
     assert ref_lib().anima_rt_run_gelu(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def ref_softmax(x):
+    x = _f32c(x)
+    D = x.shape[-1]
+    y = np.zeros_like(x)
+    assert ref_lib().anima_rt_run_softmax(_ptr(x), _ptr(y), x.size // D, D)
     return y
 
 

@@ -17,7 +17,7 @@ Cases
   rope_*   anima_rt_run_rope on a 4x4 token grid, and the D=4 known-answer
            input of scripts/test_rope_debug.py:17-34
   gemm_*   anima_rt_run_gemm_bf16 (fp32 activations x bf16 weights)
-  ln_*, silu_*, gelu_*  anima_rt_run_layernorm / _silu / _gelu
+  ln_*, silu_*, gelu_*, softmax_*  anima_rt_run_layernorm / _silu / _gelu / _softmax
 
 Run:  python tests/golden/make_golden.py
 """
@@ -104,6 +104,14 @@ def main():
                                        -40.0], np.float32)]).astype(np.float32)
     vec["gelu_x"] = gelu_x
     vec["gelu_out"] = oracle.ref_gelu(gelu_x)
+    # Softmax rows: ordinary, a large offset, a row with a dominant entry and
+    # a constant row.
+    sm_x = normal(rng, 5, 77, sigma=3.0)
+    sm_x[1] += np.float32(500.0)
+    sm_x[2, 13] = np.float32(60.0)
+    sm_x[3] = np.float32(-2.5)
+    vec["softmax_x"] = sm_x
+    vec["softmax_out"] = oracle.ref_softmax(sm_x)
 
     np.savez_compressed(OUT, **vec)
     print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes, {len(vec)} arrays)")

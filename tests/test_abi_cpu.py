@@ -1,5 +1,6 @@
 """The C-ABI library without a GPU: it loads, exports every declared symbol,
 and reports errors instead of returning silently (no compute is launched)."""
+import ctypes as ct
 import os
 import re
 import subprocess
@@ -103,6 +104,35 @@ def test_reference_drop_in_signatures():
         assert sig[name][0] is ct.c_bool
 
 
+# The symbols and ctypes argument types the reference's own binding declares
+# at import time (anima_rt/scripts/anima_rt_ops.py:11-34); a library missing
+# any of them cannot be loaded in its place.
+_P, _I, _F = ct.c_void_p, ct.c_int, ct.c_float
+REFERENCE_BINDING = {
+    "anima_rt_run_gelu": [_P, _P, _I],
+    "anima_rt_run_silu": [_P, _P, _I],
+    "anima_rt_run_layernorm": [_P, _P, _I, _I, _F],
+    "anima_rt_run_rmsnorm": [_P, _P, _P, _I, _I, _F],
+    "anima_rt_run_softmax": [_P, _P, _I, _I],
+    "anima_rt_run_gemm_fp32": [_P, _P, _P, _I, _I, _I],
+    "anima_rt_run_gemm_bf16": [_P, _P, _P, _I, _I, _I],
+    "anima_rt_run_sdpa": [_P] * 4 + [_I] * 4 + [_F, ct.c_bool],
+    "anima_rt_run_sdpa_flash": [_P] * 4 + [_I] * 4 + [_F, ct.c_bool],
+    "anima_rt_run_rope": [_P, _P, _P, _I, _I, _I],
+}
+
+
+def test_reference_binding_loads_against_this_library():
+    lib = ct.CDLL(_lib.LIB_PATH)
+    lib.anima_rt_init.restype = ct.c_bool
+    for name, args in REFERENCE_BINDING.items():
+        fn = getattr(lib, name)  # AttributeError if the symbol were missing
+        fn.argtypes = args
+        fn.restype = ct.c_bool
+        assert _lib.SIGNATURES[name] == (ct.c_bool, args), name
+    assert _lib.SIGNATURES["anima_rt_run_bias_add"] == (ct.c_bool, [_P, _P, _I, _I])
+
+
 def test_rmsnorm_and_math_sdpa_require_init():
     # anima_rt.cpp:47 and :84 return false before anima_rt_init(); so does the
     # drop-in, and the Python layer turns that into an exception.
@@ -117,6 +147,16 @@ def test_rmsnorm_and_math_sdpa_require_init():
     q = np.ones((1, 4, 8), np.float32)
     with pytest.raises(anima_hip.AnimaHipError, match="anima_rt_init"):
         rt.sdpa_math(q, q, q)
+    # anima_rt.cpp:25, :30, :38, :54: the activations, LayerNorm and softmax
+    # need the backend too.
+    for fn in (rt.gelu, rt.silu, rt.layernorm, rt.softmax):
+        with pytest.raises(anima_hip.AnimaHipError, match="anima_rt_init"):
+            fn(x)
+    # bias_add with a null bias does nothing and needs no init
+    # (gemm_backend.cpp:176); zero-sized inputs succeed after init-free checks.
+    c = np.ones((2, 3), np.float32)
+    assert lib.anima_rt_run_bias_add(c.ctypes.data, None, 2, 3)
+    assert np.all(c == 1.0)
 
 
 def test_python_shape_validation():

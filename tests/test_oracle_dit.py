@@ -35,6 +35,18 @@ def test_gelu_matches_reference_vectors():
     np.testing.assert_array_equal(oracle.gelu(gold["gelu_x"]), gold["gelu_out"])
 
 
+def test_softmax_matches_reference_vectors_and_fp64():
+    gold = np.load(GOLDEN)
+    x = gold["softmax_x"]
+    y = oracle.softmax(x)
+    np.testing.assert_array_equal(y, gold["softmax_out"])
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(axis=1, keepdims=True))
+    np.testing.assert_allclose(y, e / e.sum(axis=1, keepdims=True), rtol=2e-6, atol=1e-9)
+    np.testing.assert_allclose(y.sum(axis=1), 1.0, rtol=2e-6)
+    np.testing.assert_allclose(y[3], 1.0 / 77, rtol=1e-6)  # constant row
+
+
 def test_gelu_vs_fp64_and_identities():
     x = np.linspace(-8, 8, 4001).astype(np.float32)
     ref = np.array([v * 0.5 * (1 + math.erf(v / math.sqrt(2))) for v in x.astype(np.float64)])

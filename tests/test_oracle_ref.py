@@ -62,3 +62,4 @@ def test_layernorm_silu_bitwise_vs_reference():
     np.testing.assert_array_equal(oracle.layernorm(x[:, :77], 1e-5), oracle.ref_layernorm(x[:, :77], 1e-5))
     np.testing.assert_array_equal(oracle.silu(x), oracle.ref_silu(x))
     np.testing.assert_array_equal(oracle.gelu(x), oracle.ref_gelu(x))
+    np.testing.assert_array_equal(oracle.softmax(x[:, :300]), oracle.ref_softmax(x[:, :300]))
