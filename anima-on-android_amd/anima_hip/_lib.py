@@ -63,6 +63,7 @@ SIGNATURES = {
     "anima_hip_dit_forward_dev": (_B, [_P, _P, ct.c_int64, _P] + [_I] * 4
                                   + [_P, _P, _P, ct.c_size_t, _P]),
     "anima_hip_dit_euler_dev": (_B, [_P, _P, _P, _I, _F, _I, _I, _P, _P, ct.c_size_t, _P]),
+    "anima_hip_last_call_ms": (_B, [ct.POINTER(_F), ct.POINTER(_F)]),
     "anima_hip_malloc": (_P, [ct.c_size_t]),
     "anima_hip_free": (None, [_P]),
     "anima_hip_memcpy": (_B, [_P, _P, ct.c_size_t, _I]),

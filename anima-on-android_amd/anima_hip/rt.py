@@ -39,6 +39,16 @@ def destroy() -> None:
     _lib.load().anima_rt_destroy()
 
 
+def last_call_ms():
+    """(kernel_ms, total_ms) of the last host-pointer call: device time between
+    its uploads and downloads, and from the first upload to the last download
+    (anima_hip_last_call_ms)."""
+    k, t = ct.c_float(), ct.c_float()
+    _lib.check(_lib.load().anima_hip_last_call_ms(ct.byref(k), ct.byref(t)),
+               "anima_hip_last_call_ms")
+    return k.value, t.value
+
+
 def sdpa_flash(q, k, v, scale=None, is_causal=False) -> np.ndarray:
     """anima_rt_run_sdpa_flash on [BH,S,D] arrays (anima_rt.cpp:147-156)."""
     q, k, v = _f32(q), _f32(k), _f32(v)

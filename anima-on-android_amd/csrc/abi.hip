@@ -58,6 +58,15 @@ struct DevBuf {
     }
 };
 
+// Timing hook of the host-pointer entries: events on the runtime stream at
+// the first upload, after the last upload, before the first download and
+// after the last download of a call.
+struct CallTimer {
+    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+    bool up = false, down = false;
+    float kernel_ms = -1.0f, total_ms = -1.0f;
+};
+
 struct Runtime {
     std::recursive_mutex mu;
     bool ready = false;      // device + stream exist
@@ -65,6 +74,7 @@ struct Runtime {
     int device = 0;
     hipStream_t stream = nullptr;
     DevBuf q, k, v, o, w0, w1, fr, q2, k2, v2, scratch;
+    CallTimer timer;
 };
 
 Runtime &rt()
@@ -86,6 +96,9 @@ bool ensure_ready(Runtime &r)
         return false;
     if (!hip_ok(hipStreamCreateWithFlags(&r.stream, hipStreamNonBlocking), "hipStreamCreate"))
         return false;
+    for (hipEvent_t &e : r.timer.ev)
+        if (!hip_ok(hipEventCreate(&e), "hipEventCreate"))
+            return false;
     r.ready = true;
     return true;
 }
@@ -128,17 +141,67 @@ bool check_dims(int B, int H, int S_q, int S_kv, int D)
 
 size_t f32_bytes(int64_t n) { return size_t(n) * sizeof(float); }
 
+// Timing marks on the runtime stream (no-ops on other streams).
+void mark(hipStream_t st, int i)
+{
+    Runtime &r = rt();
+    if (st == r.stream && r.timer.ev[i])
+        (void)hipEventRecord(r.timer.ev[i], st);
+}
+
 bool h2d(void *dst, const void *src, size_t n, hipStream_t st)
 {
-    return n == 0 || hip_ok(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, st), "H2D copy");
+    if (n == 0)
+        return true;
+    Runtime &r = rt();
+    if (!r.timer.up && st == r.stream) {
+        mark(st, 0);
+        r.timer.up = true;
+    }
+    const bool ok = hip_ok(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, st), "H2D copy");
+    mark(st, 1);
+    return ok;
 }
 
 bool d2h(void *dst, const void *src, size_t n, hipStream_t st)
 {
-    return n == 0 || hip_ok(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, st), "D2H copy");
+    if (n == 0)
+        return true;
+    Runtime &r = rt();
+    if (!r.timer.down && st == r.stream) {
+        mark(st, 2);
+        r.timer.down = true;
+    }
+    const bool ok = hip_ok(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, st), "D2H copy");
+    mark(st, 3);
+    return ok;
 }
 
 bool sync(hipStream_t st) { return hip_ok(hipStreamSynchronize(st), "hipStreamSynchronize"); }
+
+// Start of a timed host-pointer call.
+void begin_call(Runtime &r)
+{
+    r.timer.up = r.timer.down = false;
+}
+
+// End of a timed host-pointer call: synchronise, then keep the device time
+// between the uploads and the downloads (kernels) and from the first upload
+// to the last download (whole call).
+bool finish_call(Runtime &r)
+{
+    if (!sync(r.stream))
+        return false;
+    CallTimer &t = r.timer;
+    float k = 0.0f, w = 0.0f;
+    if (t.up && t.down && hipEventElapsedTime(&k, t.ev[1], t.ev[2]) == hipSuccess &&
+        hipEventElapsedTime(&w, t.ev[0], t.ev[3]) == hipSuccess) {
+        t.kernel_ms = k;
+        t.total_ms = w;
+    }
+    t.up = t.down = false;
+    return true;
+}
 
 // Shared body of the host-pointer SDPA entries ([BH, S, D] f32 host arrays).
 bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int BH, int S_q,
@@ -155,6 +218,7 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
         return fail("sdpa: the bf16 mode needs D == 128");
     Runtime &r = rt();
     const hipStream_t st = r.stream;
+    begin_call(r);
     if (!r.q.reserve(f32_bytes(nq), "workspace Q") || !r.o.reserve(f32_bytes(nq), "workspace O") ||
         !r.k.reserve(f32_bytes(nk), "workspace K") || !r.v.reserve(f32_bytes(nk), "workspace V"))
         return false;
@@ -218,7 +282,7 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
     }
     if (!d2h(out, r.o.p, f32_bytes(nq), st))
         return false;
-    return sync(st);
+    return finish_call(r);
 }
 
 // Host -> device copy of an optional per-head weight or RoPE table.
@@ -247,6 +311,7 @@ bool host_gemm(const float *A, const void *W, bool w_bf16, float *C, int M, int 
     if (!C || (K > 0 && (!A || !W)))
         return fail("gemm: null pointer");
     const hipStream_t st = r.stream;
+    begin_call(r);
     const size_t wbytes = size_t(N) * K * (w_bf16 ? 2 : 4);
     if (!r.q.reserve(f32_bytes(int64_t(M) * K), "workspace A") ||
         !r.k.reserve(wbytes, "workspace W") || !r.o.reserve(f32_bytes(int64_t(M) * N), "workspace C"))
@@ -265,7 +330,7 @@ bool host_gemm(const float *A, const void *W, bool w_bf16, float *C, int M, int 
                              static_cast<float *>(r.o.p), N, M, N, K, st);
     if (!ok || !d2h(C, r.o.p, f32_bytes(int64_t(M) * N), st))
         return false;
-    return sync(st);
+    return finish_call(r);
 }
 
 }  // namespace
@@ -344,6 +409,7 @@ bool anima_rt_run_rmsnorm(const float *x, const float *w, float *out, int m, int
     if (!x || !out)
         return fail("rmsnorm: null pointer");
     const hipStream_t st = r.stream;
+    begin_call(r);
     if (!r.q.reserve(f32_bytes(n), "workspace x") || !r.o.reserve(f32_bytes(n), "workspace y"))
         return false;
     const float *wd = nullptr;
@@ -364,7 +430,7 @@ bool anima_rt_run_rmsnorm(const float *x, const float *w, float *out, int m, int
     p.out_bf16 = false;
     if (!launch_rows(p, st) || !d2h(out, r.o.p, f32_bytes(n), st))
         return false;
-    return sync(st);
+    return finish_call(r);
 }
 
 }  // extern "C"
@@ -386,12 +452,13 @@ bool host_unary(const char *what, const float *x, float *out, int64_t n, Run run
     if (!x || !out)
         return fail(std::string(what) + ": null pointer");
     const hipStream_t st = r.stream;
+    begin_call(r);
     if (!r.q.reserve(f32_bytes(n), "workspace x") || !r.o.reserve(f32_bytes(n), "workspace y") ||
         !h2d(r.q.p, x, f32_bytes(n), st) ||
         !run(static_cast<const float *>(r.q.p), static_cast<float *>(r.o.p), st) ||
         !d2h(out, r.o.p, f32_bytes(n), st))
         return false;
-    return sync(st);
+    return finish_call(r);
 }
 
 }  // namespace
@@ -440,13 +507,14 @@ bool anima_rt_run_bias_add(float *C, const float *bias, int M, int N)
         return false;
     const int64_t n = int64_t(M) * N;
     const hipStream_t st = r.stream;
+    begin_call(r);
     if (!r.o.reserve(f32_bytes(n), "workspace C") || !r.w0.reserve(f32_bytes(N), "workspace bias") ||
         !h2d(r.o.p, C, f32_bytes(n), st) || !h2d(r.w0.p, bias, f32_bytes(N), st) ||
         !launch_bias_add(static_cast<float *>(r.o.p), static_cast<const float *>(r.w0.p), M, N,
                          st) ||
         !d2h(C, r.o.p, f32_bytes(n), st))
         return false;
-    return sync(st);
+    return finish_call(r);
 }
 
 bool anima_rt_run_rope(const float *t, const float *freqs, float *out, int N, int S, int D)
@@ -463,6 +531,7 @@ bool anima_rt_run_rope(const float *t, const float *freqs, float *out, int N, in
     if (!t || !freqs || !out)
         return fail("rope: null pointer");
     const hipStream_t st = r.stream;
+    begin_call(r);
     if (!r.q.reserve(f32_bytes(n), "workspace t") || !r.o.reserve(f32_bytes(n), "workspace out") ||
         !r.fr.reserve(f32_bytes(nf), "workspace freqs"))
         return false;
@@ -483,7 +552,7 @@ bool anima_rt_run_rope(const float *t, const float *freqs, float *out, int N, in
     p.out_bf16 = false;
     if (!launch_rows(p, st) || !d2h(out, r.o.p, f32_bytes(n), st))
         return false;
-    return sync(st);
+    return finish_call(r);
 }
 
 bool anima_rt_run_gemm_fp32(const float *A, const float *B, float *C, int M, int N, int K)
@@ -709,6 +778,7 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
     if (!q || !out || (nk > 0 && (!k || !v)))
         return fail("anima_hip_attention: null pointer");
     const hipStream_t st = r.stream;
+    begin_call(r);
     const size_t scratch = attention_scratch_bytes(B, S_q, B, S_kv, H, D, bf16, false);
     if (!r.q.reserve(f32_bytes(nq), "workspace q") || !r.k.reserve(f32_bytes(nk), "workspace k") ||
         !r.v.reserve(f32_bytes(nk), "workspace v") || !r.o.reserve(f32_bytes(nq), "workspace o") ||
@@ -735,7 +805,7 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
     in.bf16 = bf16;
     if (!run_attention(in, r.scratch.p, st) || !d2h(out, r.o.p, f32_bytes(nq), st))
         return false;
-    return sync(st);
+    return finish_call(r);
 }
 
 anima_hip_ctx_kv *anima_hip_ctx_kv_create(const float *ctx, const uint16_t *wk, const uint16_t *wv,
@@ -963,6 +1033,7 @@ bool anima_hip_cross_attention(const float *q, const float *q_norm_w, const anim
     if (!q || !out)
         return fail("cross_attention: null pointer");
     const hipStream_t st = r.stream;
+    begin_call(r);
     const bool bf16 = kv->mode == ANIMA_HIP_BF16;
     const size_t scratch =
         attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D, bf16, true);
@@ -976,7 +1047,7 @@ bool anima_hip_cross_attention(const float *q, const float *q_norm_w, const anim
                                        eps, st) ||
         !d2h(out, r.o.p, f32_bytes(nq), st))
         return false;
-    return sync(st);
+    return finish_call(r);
 }
 
 void *anima_hip_malloc(size_t bytes)
@@ -1018,6 +1089,19 @@ bool anima_hip_memcpy(void *dst, const void *src, size_t bytes, int kind)
 bool anima_hip_synchronize(void)
 {
     return ready_for_device_call() && hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+}
+
+bool anima_hip_last_call_ms(float *kernel_ms, float *total_ms)
+{
+    Runtime &r = rt();
+    std::lock_guard<std::recursive_mutex> g(r.mu);
+    if (r.timer.total_ms < 0.0f)
+        return fail("last_call_ms: no host-pointer call has completed yet");
+    if (kernel_ms)
+        *kernel_ms = r.timer.kernel_ms;
+    if (total_ms)
+        *total_ms = r.timer.total_ms;
+    return true;
 }
 
 }  // extern "C"

@@ -471,6 +471,32 @@ def sampler_step(c, mode, H=128, W=128, steps=3):
                         "update of the latent; synthetic Anima 2B-shaped weights"}
 
 
+def dropin_call(c, host, B, H, S, D, iters=3):
+    """The headline attention through the reference's own C-ABI entry,
+    anima_rt_run_sdpa_flash, on host numpy [B*H, S, D] buffers: host wall
+    time, and from the library's timing hook (anima_hip_last_call_ms) the
+    device time of the whole call (PCIe copies included) and of its kernels."""
+    import numpy as np
+    from anima_hip import rt
+    q, k, v = (np.ascontiguousarray(x.transpose(0, 2, 1, 3)).reshape(B * H, S, D) for x in host)
+    rt.sdpa_flash(q, k, v)
+    walls, kern, tot = [], [], []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        rt.sdpa_flash(q, k, v)
+        walls.append((time.perf_counter() - t0) * 1e3)
+        km, tm = rt.last_call_ms()
+        kern.append(km)
+        tot.append(tm)
+    i = int(np.argmin(walls))
+    moved = 4 * q.nbytes  # Q, K, V up, O down
+    return {"entry": "anima_rt_run_sdpa_flash (host pointers, f32)", "wall_ms": round(walls[i], 3),
+            "device_call_ms": round(tot[i], 3), "kernel_ms": round(kern[i], 3),
+            "pcie_bytes": moved, "pcie_GBps": round(moved / ((tot[i] - kern[i]) * 1e-3) / 1e9, 1),
+            "note": "best of %d calls; kernel_ms spans the prologue-free flash launch between "
+                    "the uploads and the download" % iters}
+
+
 def cpu_baseline(qn, kn, v, B, H, S, D, heads):
     """anima_rt flash attention on `heads` (b, h) slices, one core, plus the
     same per-head work spread over this host's cores."""
@@ -581,6 +607,8 @@ def main():
                            "roofline": r["roofline"]}
         del r
 
+    dropin = None if args.headline_only else dropin_call(c, host, B, H, S, D)
+
     cpu = multi = None
     if not args.no_cpu_baseline:
         cpu, multi = cpu_baseline(main_res["qn"], main_res["kn"], v, B, H, S, D, args.cpu_heads)
@@ -613,6 +641,7 @@ def main():
         "speedup_vs_cpu": None if cpu is None else round(value / cpu["value"], 1),
         "speedup_vs_cpu_multicore": None if multi is None else round(value / multi["value"], 1),
         "variants": variants,
+        "dropin_c_abi": dropin,
         "configs": configs,
     }
     print(json.dumps(line), flush=True)

@@ -59,7 +59,8 @@ def _ctype_of(c):
     c = c.replace("const ", "").strip()
     if c.endswith("*"):
         base = c[:-1].strip()
-        return {"int64_t": "int64*", "int": "int*", "char": "char*"}.get(base, "ptr")
+        return {"int64_t": "int64*", "int": "int*", "char": "char*", "float": "float*"}.get(
+            base, "ptr")
     return {"bool": ct.c_bool, "int": ct.c_int, "float": ct.c_float, "size_t": ct.c_size_t,
             "int64_t": ct.c_int64, "void": None}[c]
 
@@ -81,6 +82,8 @@ def test_ctypes_declarations_match_header_prototypes():
                 assert py is ct.POINTER(ct.c_int), f"{name} arg {i}: {c}"
             elif want == "char*":
                 assert py is ct.c_char_p, f"{name} arg {i}: {c}"
+            elif want == "float*":
+                assert py in (ct.POINTER(ct.c_float), ct.c_void_p), f"{name} arg {i}: {c}"
             else:
                 assert py is want, f"{name} arg {i}: {c} vs {py}"
         rwant = _ctype_of(ret)
@@ -157,6 +160,9 @@ def test_rmsnorm_and_math_sdpa_require_init():
     c = np.ones((2, 3), np.float32)
     assert lib.anima_rt_run_bias_add(c.ctypes.data, None, 2, 3)
     assert np.all(c == 1.0)
+    # The timing hook has nothing to report until a host call completes.
+    assert not lib.anima_hip_last_call_ms(None, None)
+    assert "no host-pointer call" in _lib.last_error()
 
 
 def test_python_shape_validation():

@@ -104,3 +104,17 @@ def test_anima_vk_gemm_from_checkpoint(tmp_path):
             rt.AnimaVK(store).vk_run_gemm("blocks.0.mlp.layer1.weight", x, out, 37, 96, 100)
     ref = oracle.gemm_bf16(x, w)
     assert np.abs(out - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_timing_hook_reports_the_last_host_call():
+    """anima_hip_last_call_ms: device time of the last host-pointer call, the
+    kernels between its uploads and downloads inside the whole call."""
+    rng = np.random.default_rng(87)
+    q = rng.standard_normal((16, 1024, 128)).astype(np.float32)
+    rt.sdpa_flash(q, q, q)
+    k_ms, t_ms = rt.last_call_ms()
+    print(f"sdpa 16x1024^2: kernels {k_ms:.3f} ms of {t_ms:.3f} ms", flush=True)
+    assert 0.0 < k_ms < t_ms < 1e4
+    rt.softmax(q[0])
+    k2, t2 = rt.last_call_ms()
+    assert 0.0 < k2 <= t2 and (k2, t2) != (k_ms, t_ms)
