@@ -120,6 +120,11 @@ bool linear_terms_supported(int M, int N, int K, const void *w, int64_t ldw, con
 bool launch_linear_terms(const uint16_t *hi, const uint16_t *lo, const uint16_t *w, int64_t ldw,
                          float *c, int64_t ldc, int M, int N, int K, hipStream_t st);
 
+// C[M,N] = hi . W^T rounded to bf16 (C bf16, ldc % 8 == 0): one product on
+// activations already rounded to bf16.
+bool launch_linear_terms_bf16out(const uint16_t *hi, const uint16_t *w, int64_t ldw, uint16_t *c,
+                                 int64_t ldc, int M, int N, int K, hipStream_t st);
+
 // x[b*S + s, :] += gate[b*gate_stride + :] (.) (bf16(a[b*S + s, :]) . W^T) for
 // b < B: the output projection fused with the gated residual of a DiT block
 // (the gate scales the N output channels).  Activations round to bf16 (the hi

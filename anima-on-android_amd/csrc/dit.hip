@@ -157,19 +157,33 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvJob *jobs, int B, i
 // g = x * 0.5 * (1 + erf(x / sqrt(2))) of h [M][N] (N % 8 == 0) into hi/lo
 // rows of N bf16.
 struct GeluArgs {
-    const float *h;
+    const void *h;  // f32, or bf16 (H_BF16)
     unsigned int *hi, *lo;
     int64_t n8;  // M * N / 8
 };
 
+template <bool H_BF16>
 __global__ __launch_bounds__(256) void gelu_terms_kernel(GeluArgs a)
 {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= a.n8)
         return;
-    const f32x4 u = *reinterpret_cast<const f32x4 *>(a.h + 8 * i);
-    const f32x4 w = *reinterpret_cast<const f32x4 *>(a.h + 8 * i + 4);
-    const float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+    float x[8];
+    if (H_BF16) {
+        const uint4 v = reinterpret_cast<const uint4 *>(a.h)[i];
+        const unsigned int w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[2 * e] = __uint_as_float(w4[e] << 16);
+            x[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
+        }
+    } else {
+        const float *h = static_cast<const float *>(a.h);
+        const f32x4 u = *reinterpret_cast<const f32x4 *>(h + 8 * i);
+        const f32x4 w = *reinterpret_cast<const f32x4 *>(h + 8 * i + 4);
+        x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
+        x[4] = w.x; x[5] = w.y; x[6] = w.z; x[7] = w.w;
+    }
     float g[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -302,7 +316,7 @@ MlpScratch mlp_scratch(int64_t M, int Dm, int hidden, bool bf16)
 {
     MlpScratch s{};
     s.terms = round_up256(size_t(M) * size_t(linear_terms_ld(Dm)) * 2) * (bf16 ? 1 : 2);
-    s.h = round_up256(size_t(M) * hidden * 4);
+    s.h = round_up256(size_t(M) * hidden * (bf16 ? 2 : 4));  // layer1 output
     s.g = round_up256(size_t(M) * size_t(linear_terms_ld(hidden)) * 2) * (bf16 ? 1 : 2);
     s.y = round_up256(size_t(M) * Dm * 4);
     s.total = s.terms + s.h + s.g + s.y;
@@ -342,21 +356,31 @@ bool run_mlp_block(float *x, const float *mod, const uint16_t *w1, const uint16_
     };
     uint16_t *hi = reinterpret_cast<uint16_t *>(take(s.terms));
     uint16_t *lo = bf16 ? nullptr : hi + (s.terms / 2) / sizeof(uint16_t);
-    float *h = reinterpret_cast<float *>(take(s.h));
+    void *h = take(s.h);
     uint16_t *ghi = reinterpret_cast<uint16_t *>(take(s.g));
     uint16_t *glo = bf16 ? nullptr : ghi + (s.g / 2) / sizeof(uint16_t);
     float *y = reinterpret_cast<float *>(take(s.y));
 
+    // layer1: f32 output in f32 mode; in bf16 mode the product rounds to
+    // bf16 on the way out, halving the round trip through the GELU pass.
     if (!launch_ln_modulate(x, Dm, mod, 3 * int64_t(Dm), hi, lo, M, S, Dm, eps, st, x, res_y,
-                            res_y ? res_mod + 2 * int64_t(Dm) : nullptr, 3 * int64_t(Dm)) ||
-        !launch_linear_terms(hi, lo, w1, Dm, h, hidden, int(M), hidden, Dm, st))
+                            res_y ? res_mod + 2 * int64_t(Dm) : nullptr, 3 * int64_t(Dm)))
+        return false;
+    const bool ok1 = bf16 ? launch_linear_terms_bf16out(hi, w1, Dm, static_cast<uint16_t *>(h),
+                                                        hidden, int(M), hidden, Dm, st)
+                          : launch_linear_terms(hi, lo, w1, Dm, static_cast<float *>(h), hidden,
+                                                int(M), hidden, Dm, st);
+    if (!ok1)
         return false;
     GeluArgs ga;
     ga.h = h;
     ga.hi = reinterpret_cast<unsigned int *>(ghi);
     ga.lo = reinterpret_cast<unsigned int *>(glo);
     ga.n8 = M * hidden / 8;
-    hipLaunchKernelGGL(gelu_terms_kernel, dim3(grid1(ga.n8)), dim3(256), 0, st, ga);
+    if (bf16)
+        hipLaunchKernelGGL(gelu_terms_kernel<true>, dim3(grid1(ga.n8)), dim3(256), 0, st, ga);
+    else
+        hipLaunchKernelGGL(gelu_terms_kernel<false>, dim3(grid1(ga.n8)), dim3(256), 0, st, ga);
     if (!hip_ok(hipGetLastError(), "gelu_terms_kernel launch"))
         return false;
     if (defer_y)  // the next norm pass applies x += gate * y

@@ -98,7 +98,8 @@ struct LtPlan {
 
 struct LtDevice {
     hipblasLtHandle_t handle = nullptr;
-    std::map<std::tuple<int, int, int, int64_t, int64_t, int64_t, bool>, std::unique_ptr<LtPlan>>
+    std::map<std::tuple<int, int, int, int64_t, int64_t, int64_t, bool, bool>,
+             std::unique_ptr<LtPlan>>
         plans;
 };
 
@@ -106,8 +107,9 @@ std::mutex g_lt_mu;
 std::map<int, std::unique_ptr<LtDevice>> g_lt;
 
 // alpha_vec: alpha is a device vector over the N output channels (the rows of
-// the column-major product), beta a host scalar.
-LtPlan *lt_plan(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool alpha_vec = false)
+// the column-major product), beta a host scalar.  out_bf16: C/D are bf16.
+LtPlan *lt_plan(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool alpha_vec = false,
+                bool out_bf16 = false)
 {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess)
@@ -122,7 +124,7 @@ LtPlan *lt_plan(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool
     }
     if (!slot->handle)
         return nullptr;
-    auto &pp = slot->plans[std::make_tuple(M, N, K, lda, ldw, ldc, alpha_vec)];
+    auto &pp = slot->plans[std::make_tuple(M, N, K, lda, ldw, ldc, alpha_vec, out_bf16)];
     if (pp)
         return pp->ok ? pp.get() : nullptr;
     pp.reset(new LtPlan);
@@ -144,7 +146,8 @@ LtPlan *lt_plan(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool
                                         sizeof(pmode)) == HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatrixLayoutCreate(&p.lw, HIP_R_16BF, K, N, ldw) == HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, M, lda) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatrixLayoutCreate(&p.lc, out_bf16 ? HIP_R_16BF : HIP_R_32F, N, M, ldc) ==
+            HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
                                               sizeof(ws)) == HIPBLAS_STATUS_SUCCESS &&
@@ -160,7 +163,7 @@ LtPlan *lt_plan(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc, bool
     return p.ok ? &p : nullptr;
 }
 
-bool lt_matmul(LtPlan *p, const void *w, const void *a, float *c, float beta, hipStream_t st,
+bool lt_matmul(LtPlan *p, const void *w, const void *a, void *c, float beta, hipStream_t st,
                const float *alpha_vec = nullptr)
 {
     int dev = 0;
@@ -200,6 +203,20 @@ bool launch_linear_terms(const uint16_t *hi, const uint16_t *lo, const uint16_t 
     if (!lt_matmul(plan, w, hi, c, 0.0f, st))
         return false;
     return !lo || lt_matmul(plan, w, lo, c, 1.0f, st);
+}
+
+bool launch_linear_terms_bf16out(const uint16_t *hi, const uint16_t *w, int64_t ldw, uint16_t *c,
+                                 int64_t ldc, int M, int N, int K, hipStream_t st)
+{
+    if (M <= 0 || N <= 0 || K <= 0 || ldw < K || ldc < N || (ldw % 8) != 0 || (ldc % 8) != 0 ||
+        (reinterpret_cast<uintptr_t>(w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(c) & 15u) != 0 ||
+        (reinterpret_cast<uintptr_t>(hi) & 15u) != 0)
+        return fail("linear: bf16-output GEMM needs positive sizes and 16-byte aligned rows");
+    std::lock_guard<std::mutex> g(g_lt_mu);
+    LtPlan *plan = lt_plan(M, N, K, padded_k(K), ldw, ldc, false, true);
+    if (!plan)
+        return fail("linear: no bf16-output GEMM for this shape");
+    return lt_matmul(plan, w, hi, c, 0.0f, st);
 }
 
 size_t linear_scratch_bytes(int M, int K, bool exact)
