@@ -47,9 +47,11 @@ size_t attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D, b
     return n + round_up(flash_plan(int64_t(B) * H, S_q, S_kv, D).bytes);
 }
 
-bool prepare_kv(const float *k, const float *v, const float *k_norm_w, const float *freqs,
-                void *k_out, void *v_out, int Bk, int S_kv, int H, int D, float eps, bool bf16,
-                hipStream_t st)
+namespace {
+
+// The K row problem of prepare_kv: RMSNorm (+ RoPE) of [Bk, S_kv, H, D] K.
+RowProblem k_rows(const float *k, const float *k_norm_w, const float *freqs, void *k_out, int Bk,
+                  int S_kv, int H, int D, float eps, bool bf16)
 {
     RowProblem pk;
     pk.x = k;
@@ -64,8 +66,13 @@ bool prepare_kv(const float *k, const float *v, const float *k_norm_w, const flo
     pk.eps = eps;
     pk.norm = true;
     pk.out_bf16 = bf16;
-    if (!launch_rows(pk, st))
-        return false;
+    return pk;
+}
+
+// V's part of prepare_kv: packed bf16 V^T, or a copy (f32) unless in place.
+bool prepare_v(const float *v, void *v_out, int Bk, int S_kv, int H, int D, bool bf16,
+               hipStream_t st)
+{
     if (bf16) {
         const int64_t sp = vt_padded_len(S_kv);
         const Strides vts{int64_t(H) * D * sp, int64_t(D) * sp, sp};
@@ -77,6 +84,16 @@ bool prepare_kv(const float *k, const float *v, const float *k_norm_w, const flo
                                      hipMemcpyDeviceToDevice, st),
                       "V copy");
     return true;
+}
+
+}  // namespace
+
+bool prepare_kv(const float *k, const float *v, const float *k_norm_w, const float *freqs,
+                void *k_out, void *v_out, int Bk, int S_kv, int H, int D, float eps, bool bf16,
+                hipStream_t st)
+{
+    return launch_rows(k_rows(k, k_norm_w, freqs, k_out, Bk, S_kv, H, D, eps, bf16), st) &&
+           prepare_v(v, v_out, Bk, S_kv, H, D, bf16, st);
 }
 
 bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
@@ -96,12 +113,13 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     cur += round_up(size_t(B) * S_q * H * D * (in.bf16 ? 2 : 4));
 
     const void *kp = in.k_prep, *vp = in.v_prep;
+    RowProblem pk{};
     if (!prepared) {
         void *kn = cur;
         cur += round_up(prepared_k_bytes(in.Bk, S_kv, H, D, in.bf16));
         void *vt = in.bf16 ? static_cast<void *>(cur) : nullptr;
-        if (!prepare_kv(in.k, in.v, in.k_norm_w, in.freqs, kn, vt, in.Bk, S_kv, H, D, in.eps,
-                        in.bf16, st))
+        pk = k_rows(in.k, in.k_norm_w, in.freqs, kn, in.Bk, S_kv, H, D, in.eps, in.bf16);
+        if (!prepare_v(in.v, vt, in.Bk, S_kv, H, D, in.bf16, st))
             return false;
         kp = kn;
         vp = in.bf16 ? vt : static_cast<const void *>(in.v);
@@ -125,7 +143,8 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     pq.eps = in.eps;
     pq.norm = true;
     pq.out_bf16 = in.bf16;
-    if (!launch_rows(pq, st))
+    // Q rows, and K rows unless prepared, in one launch.
+    if (!(prepared ? launch_rows(pq, st) : launch_rows_pair(pk, pq, st)))
         return false;
 
     const bool bcast = in.Bk == 1 && B > 1;

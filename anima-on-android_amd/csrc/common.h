@@ -158,6 +158,9 @@ struct RowProblem {
     bool out_bf16;  // write bf16 (round to nearest even) instead of f32
 };
 bool launch_rows(const RowProblem &p, hipStream_t st);
+// Both problems in one launch when both take the D == 128 float4 kernel, else
+// two launches.
+bool launch_rows_pair(const RowProblem &p1, const RowProblem &p2, hipStream_t st);
 
 // ---- Composite attention core (attention.hip) ----
 // Prepared K/V layouts: f32 mode K and V f32 [Bk, S_kv, H, D]; bf16 mode K

@@ -154,14 +154,15 @@ __global__ __launch_bounds__(256) void rows_kernel(RowArgs a)
 constexpr int kRows128 = 64;
 constexpr int kPitch128 = 132;
 
-__global__ __launch_bounds__(256) void rows_d128(RowArgs a)
+// Rows [64 * blk, 64 * blk + 64) of problem a.
+__device__ __forceinline__ void rows_d128_block(const RowArgs &a, int64_t blk)
 {
     __shared__ __attribute__((aligned(16))) float xs[kRows128 * kPitch128];
     __shared__ float inv[kRows128];
     __shared__ int spos[kRows128];
     __shared__ int64_t xoff[kRows128], ooff[kRows128];
     const int t = threadIdx.x;
-    const int64_t r0 = int64_t(blockIdx.x) * kRows128;
+    const int64_t r0 = blk * kRows128;
     const int nrows = int(min<int64_t>(kRows128, a.rows - r0));
 
     if (t < nrows) {
@@ -254,7 +255,62 @@ __global__ __launch_bounds__(256) void rows_d128(RowArgs a)
     }
 }
 
+__global__ __launch_bounds__(256) void rows_d128(RowArgs a) { rows_d128_block(a, blockIdx.x); }
+
+// Two row problems in one launch: blocks [0, nblk_a) take a, the rest b.
+__global__ __launch_bounds__(256) void rows_d128_pair(RowArgs a, RowArgs b, int64_t nblk_a)
+{
+    if (int64_t(blockIdx.x) < nblk_a)
+        rows_d128_block(a, blockIdx.x);
+    else
+        rows_d128_block(b, int64_t(blockIdx.x) - nblk_a);
+}
+
+RowArgs row_args(const RowProblem &p)
+{
+    RowArgs a;
+    a.x = p.x;
+    a.out = p.out;
+    a.w = p.w;
+    a.freqs = p.freqs;
+    a.xb = p.xs.b; a.xh = p.xs.h; a.xs = p.xs.s;
+    a.ob = p.os.b; a.oh = p.os.h; a.os = p.os.s;
+    a.rows = int64_t(p.B) * p.S * p.H;
+    a.S = p.S;
+    a.H = p.H;
+    a.D = p.D;
+    a.eps = p.eps;
+    a.norm = p.norm ? 1 : 0;
+    a.out_bf16 = p.out_bf16 ? 1 : 0;
+    a.rows_per_block = kRows128;
+    return a;
+}
+
+// D = 128 with 16-byte aligned rows and operands: the float4 kernel.
+bool d128_eligible(const RowProblem &p)
+{
+    const auto al = [](const void *ptr, unsigned m) {
+        return (reinterpret_cast<uintptr_t>(ptr) & (m - 1)) == 0;
+    };
+    const auto st4 = [](const Strides &x) { return x.b % 4 == 0 && x.h % 4 == 0 && x.s % 4 == 0; };
+    return p.D == 128 && al(p.x, 16) && al(p.out, p.out_bf16 ? 8 : 16) && st4(p.xs) &&
+           st4(p.os) && (!p.w || al(p.w, 16)) && (!p.freqs || al(p.freqs, 16));
+}
+
 }  // namespace
+
+bool launch_rows_pair(const RowProblem &p1, const RowProblem &p2, hipStream_t st)
+{
+    const int64_t r1 = int64_t(p1.B) * p1.S * p1.H, r2 = int64_t(p2.B) * p2.S * p2.H;
+    if (r1 == 0 || r2 == 0 || !d128_eligible(p1) || !d128_eligible(p2))
+        return launch_rows(p1, st) && launch_rows(p2, st);
+    const int64_t n1 = (r1 + kRows128 - 1) / kRows128, n2 = (r2 + kRows128 - 1) / kRows128;
+    if (n1 + n2 > INT32_MAX)
+        return fail("rows kernel: too many rows");
+    hipLaunchKernelGGL(rows_d128_pair, dim3(unsigned(n1 + n2)), dim3(256), 0, st, row_args(p1),
+                       row_args(p2), n1);
+    return hip_ok(hipGetLastError(), "rows_d128_pair launch");
+}
 
 bool launch_rows(const RowProblem &p, hipStream_t st)
 {
@@ -263,27 +319,8 @@ bool launch_rows(const RowProblem &p, hipStream_t st)
         return true;
     if (p.freqs && (p.D & 1))
         return fail("rope: head dim must be even");
-    RowArgs a;
-    a.x = p.x;
-    a.out = p.out;
-    a.w = p.w;
-    a.freqs = p.freqs;
-    a.xb = p.xs.b; a.xh = p.xs.h; a.xs = p.xs.s;
-    a.ob = p.os.b; a.oh = p.os.h; a.os = p.os.s;
-    a.rows = rows;
-    a.S = p.S;
-    a.H = p.H;
-    a.D = p.D;
-    a.eps = p.eps;
-    a.norm = p.norm ? 1 : 0;
-    a.out_bf16 = p.out_bf16 ? 1 : 0;
-
-    const auto al = [](const void *ptr, unsigned m) {
-        return (reinterpret_cast<uintptr_t>(ptr) & (m - 1)) == 0;
-    };
-    const auto st4 = [](const Strides &x) { return x.b % 4 == 0 && x.h % 4 == 0 && x.s % 4 == 0; };
-    if (p.D == 128 && al(p.x, 16) && al(p.out, p.out_bf16 ? 8 : 16) && st4(p.xs) && st4(p.os) &&
-        (!p.w || al(p.w, 16)) && (!p.freqs || al(p.freqs, 16))) {
+    RowArgs a = row_args(p);
+    if (d128_eligible(p)) {
         a.rows_per_block = kRows128;
         const int64_t nblk = (rows + kRows128 - 1) / kRows128;
         if (nblk > INT32_MAX)
