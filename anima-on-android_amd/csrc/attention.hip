@@ -19,9 +19,12 @@ namespace {
 constexpr size_t kAlign = 256;
 size_t round_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
 
-Strides bshd(int S, int H, int D, bool broadcast)
+// [B, S, H, D] view whose token rows are ld elements apart (ld = H*D when
+// dense; wider when q/k/v are column blocks of one [B*S, 3*H*D] projection).
+Strides bshd(int S, int H, int D, bool broadcast, int64_t ld = 0)
 {
-    return Strides{broadcast ? 0 : int64_t(S) * H * D, int64_t(D), int64_t(H) * D};
+    const int64_t row = ld > 0 ? ld : int64_t(H) * D;
+    return Strides{broadcast ? 0 : int64_t(S) * row, int64_t(D), row};
 }
 }  // namespace
 
@@ -51,14 +54,15 @@ namespace {
 
 // The K row problem of prepare_kv: RMSNorm (+ RoPE) of [Bk, S_kv, H, D] K.
 RowProblem k_rows(const float *k, const float *k_norm_w, const float *freqs, void *k_out, int Bk,
-                  int S_kv, int H, int D, float eps, bool bf16)
+                  int S_kv, int H, int D, float eps, bool bf16, int64_t ld = 0)
 {
     RowProblem pk;
     pk.x = k;
     pk.out = k_out;
     pk.w = k_norm_w;
     pk.freqs = freqs;
-    pk.xs = pk.os = bshd(S_kv, H, D, false);
+    pk.xs = bshd(S_kv, H, D, false, ld);
+    pk.os = bshd(S_kv, H, D, false);
     pk.B = Bk;
     pk.S = S_kv;
     pk.H = H;
@@ -71,18 +75,21 @@ RowProblem k_rows(const float *k, const float *k_norm_w, const float *freqs, voi
 
 // V's part of prepare_kv: packed bf16 V^T, or a copy (f32) unless in place.
 bool prepare_v(const float *v, void *v_out, int Bk, int S_kv, int H, int D, bool bf16,
-               hipStream_t st)
+               hipStream_t st, int64_t ld = 0)
 {
     if (bf16) {
         const int64_t sp = vt_padded_len(S_kv);
         const Strides vts{int64_t(H) * D * sp, int64_t(D) * sp, sp};
-        return launch_vt_pack(v, bshd(S_kv, H, D, false), static_cast<uint16_t *>(v_out), vts, Bk,
+        return launch_vt_pack(v, bshd(S_kv, H, D, false, ld), static_cast<uint16_t *>(v_out), vts, Bk,
                               H, S_kv, D, st);
     }
-    if (v_out && v_out != v)
+    if (v_out && v_out != v) {
+        if (ld > 0 && ld != int64_t(H) * D)
+            return fail("prepare_kv: a strided V cannot be copied into a dense cache");
         return hip_ok(hipMemcpyAsync(v_out, v, prepared_v_bytes(Bk, S_kv, H, D, false),
                                      hipMemcpyDeviceToDevice, st),
                       "V copy");
+    }
     return true;
 }
 
@@ -118,8 +125,9 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
         void *kn = cur;
         cur += round_up(prepared_k_bytes(in.Bk, S_kv, H, D, in.bf16));
         void *vt = in.bf16 ? static_cast<void *>(cur) : nullptr;
-        pk = k_rows(in.k, in.k_norm_w, in.freqs, kn, in.Bk, S_kv, H, D, in.eps, in.bf16);
-        if (!prepare_v(in.v, vt, in.Bk, S_kv, H, D, in.bf16, st))
+        pk = k_rows(in.k, in.k_norm_w, in.freqs, kn, in.Bk, S_kv, H, D, in.eps, in.bf16,
+                    in.ld_kv);
+        if (!prepare_v(in.v, vt, in.Bk, S_kv, H, D, in.bf16, st, in.ld_kv))
             return false;
         kp = kn;
         vp = in.bf16 ? vt : static_cast<const void *>(in.v);
@@ -135,7 +143,8 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     pq.out = qn;
     pq.w = in.q_norm_w;
     pq.freqs = in.freqs;
-    pq.xs = pq.os = bshd(S_q, H, D, false);
+    pq.xs = bshd(S_q, H, D, false, in.ld_q);
+    pq.os = bshd(S_q, H, D, false);
     pq.B = B;
     pq.S = S_q;
     pq.H = H;
@@ -159,7 +168,7 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
         const int64_t sp = vt_padded_len(S_kv);
         p.vs = Strides{bcast ? 0 : int64_t(H) * D * sp, int64_t(D) * sp, sp};
     } else {
-        p.vs = bshd(S_kv, H, D, bcast);
+        p.vs = prepared ? bshd(S_kv, H, D, bcast) : bshd(S_kv, H, D, bcast, in.ld_kv);
     }
     p.B = B;
     p.H = H;

@@ -60,6 +60,7 @@ struct LnArgs {
     float *xw;  // x itself, writable (set with res_y)
     unsigned int *hi, *lo;  // [M][kp] bf16 (addressed as pairs); lo may be null
     int64_t kp;
+    int64_t tld;  // term row stride (elements): kp, or 2*kp for [hi | lo] rows
     int64_t M;
     int S, Dm;
     float eps;
@@ -102,8 +103,8 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(LnArgs a)
     const float rstd = 1.0f / sqrtf(wave_sum(sq) / float(a.Dm) + a.eps);
     const float *shift = a.mod + int64_t(b) * a.mod_ld;
     const float *scale = shift + a.Dm;
-    unsigned int *hrow = a.hi + row * (a.kp >> 1);
-    unsigned int *lrow = a.lo ? a.lo + row * (a.kp >> 1) : nullptr;
+    unsigned int *hrow = a.hi + row * (a.tld >> 1);
+    unsigned int *lrow = a.lo ? a.lo + row * (a.tld >> 1) : nullptr;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         const int c = lane + 64 * i;
@@ -190,7 +191,7 @@ size_t attention_block_scratch_bytes(int B, int S, int Dm, int H, int D, int Bk,
 bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t mod_ld,
                         uint16_t *hi, uint16_t *lo, int64_t M, int S, int Dm, float eps,
                         hipStream_t st, float *res_x, const float *res_y, const float *res_gate,
-                        int64_t res_ld)
+                        int64_t res_ld, int64_t tld)
 {
     if (M == 0)
         return true;
@@ -215,6 +216,9 @@ bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t m
     a.hi = reinterpret_cast<unsigned int *>(hi);
     a.lo = reinterpret_cast<unsigned int *>(lo);
     a.kp = linear_terms_ld(Dm);
+    a.tld = tld > 0 ? tld : a.kp;
+    if (a.tld < a.kp || a.tld % 8)
+        return fail("ln_modulate: term rows must be at least the padded width, multiples of 8");
     a.M = M;
     a.S = S;
     a.Dm = Dm;
@@ -292,9 +296,7 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
     // x_m as bf16 terms, then the projections of NumpyAttention.forward
     // (numpy_dit.py:273-281): q from x_m, and k/v from x_m (self) or the
     // cached context projections (cross).
-    if (!launch_ln_modulate(p.x, Dm, p.mod, 3 * int64_t(Dm), hi, lo, M, S, Dm, p.eps, st, p.x,
-                            p.res_y, p.res_y ? p.res_mod + 2 * int64_t(Dm) : nullptr,
-                            3 * int64_t(Dm)))
+    if (!launch_ln_modulate(p.x, Dm, p.mod, 3 * int64_t(Dm), hi, lo, M, S, Dm, p.eps, st))
         return false;
     if (!launch_linear_terms(hi, lo, p.wq, Dm, q, HD, int(M), HD, Dm, st))
         return false;
@@ -329,9 +331,6 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
     // read and write the residual again), or a shape the library GEMM does
     // not take with a per-channel scale: the projection into y, then a
     // residual pass.
-    if (p.defer_y)  // the next sub-layer's norm pass applies x += gate * y
-        return launch_linear(o, HD, p.wo, HD, p.defer_y, Dm, int(M), Dm, HD, !p.bf16, lin, s.lin,
-                             st);
     if (p.bf16 && linear_residual_supported(S, Dm, HD, p.wo, HD, p.x, Dm))
         return launch_linear_residual(o, HD, p.wo, HD, p.x, Dm, p.mod + 2 * int64_t(Dm),
                                       3 * int64_t(Dm), B, S, Dm, HD, lin, s.lin, st);

@@ -112,6 +112,13 @@ bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, 
                    int64_t ldc, int M, int N, int K, bool exact, void *scratch,
                    size_t scratch_bytes, hipStream_t st);
 
+// A split into [hi | lo] rows of 2*linear_terms_ld(K) bf16 (the product with
+// a weight whose rows are [W | W], K' = 2 * linear_terms_ld(K), is then one
+// GEMM: hi.W + lo.W accumulated in f32).  Scratch: linear_scratch_bytes(M, K,
+// true).  Returns the terms.
+uint16_t *launch_split_interleaved(const float *a, int64_t lda, int M, int K, void *scratch,
+                                   size_t scratch_bytes, hipStream_t st);
+
 // The same product on A already split into bf16 terms hi (and lo, or null for
 // one term), rows of linear_terms_ld(K) elements zero-padded past K.
 int64_t linear_terms_ld(int K);
@@ -178,6 +185,9 @@ struct AttnInputs {
     int B = 0, Bk = 0, S_q = 0, S_kv = 0, H = 0, D = 0;
     float eps = 1e-6f;
     bool bf16 = false;
+    // Token-row strides (elements) of q and of the raw k/v: 0 means H*D
+    // (dense); wider when they are column blocks of one fused projection.
+    int64_t ld_q = 0, ld_kv = 0;
 };
 size_t prepared_k_bytes(int Bk, int S_kv, int H, int D, bool bf16);
 size_t prepared_v_bytes(int Bk, int S_kv, int H, int D, bool bf16);
@@ -203,12 +213,6 @@ struct BlockProblem {
     int B = 0, S = 0, Dm = 0, H = 0, D = 0;
     float eps = 1e-6f;
     bool bf16 = false;
-    // Deferred residuals between sub-layers (optional): res_y/res_mod is the
-    // previous sub-layer's output and modulation, applied (x += gate * y) by
-    // this sub-layer's norm pass; with defer_y set, this sub-layer writes its
-    // output projection there and leaves x for the next norm pass.
-    const float *res_y = nullptr, *res_mod = nullptr;
-    float *defer_y = nullptr;
 };
 size_t attention_block_scratch_bytes(int B, int S, int Dm, int H, int D, int Bk, int S_kv,
                                      bool bf16, bool cross);
@@ -218,11 +222,13 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
 // belongs to batch entry r / S, whose shift and scale are mod[b*mod_ld + :Dm]
 // and mod[b*mod_ld + Dm : 2*Dm].
 // res_y != null: first x += gate[b] * res_y (gate at res_gate + b*res_ld,
-// res_y dense [M][Dm]), written back to x (res_x must be x).
+// res_y dense [M][Dm]), written back to x (res_x must be x).  tld: term row
+// stride in elements (0: linear_terms_ld(Dm)); [hi | lo] rows in one buffer
+// use tld = 2 * linear_terms_ld(Dm) and lo = hi + linear_terms_ld(Dm).
 bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t mod_ld,
                         uint16_t *hi, uint16_t *lo, int64_t M, int S, int Dm, float eps,
                         hipStream_t st, float *res_x = nullptr, const float *res_y = nullptr,
-                        const float *res_gate = nullptr, int64_t res_ld = 0);
+                        const float *res_gate = nullptr, int64_t res_ld = 0, int64_t tld = 0);
 // x += gate[b] * y for rows of S per batch entry.
 bool launch_gate_residual(float *x, const float *y, const float *mod, int64_t M, int S, int Dm,
                           hipStream_t st);
@@ -235,15 +241,5 @@ bool launch_silu(const float *x, float *y, int64_t n, hipStream_t st);
 bool launch_layernorm_rows(const float *x, float *y, int64_t M, int D, float eps, hipStream_t st);
 bool launch_softmax_rows(const float *x, float *y, int64_t M, int D, hipStream_t st);
 bool launch_bias_add(float *c, const float *bias, int64_t M, int N, hipStream_t st);
-
-// ---- MLP sub-layer of a DiT block (dit.hip): x += gate[b] * layer2(gelu(
-// layer1(LN(x)*(1+scale[b]) + shift[b]))), mod [B][3][Dm], w1 [hidden][Dm],
-// w2 [Dm][hidden] bf16 bits.
-// res_y/res_mod and defer_y: deferred residuals as in BlockProblem.
-size_t mlp_block_scratch_bytes(int B, int S, int Dm, int hidden, bool bf16);
-bool run_mlp_block(float *x, const float *mod, const uint16_t *w1, const uint16_t *w2, int B,
-                   int S, int Dm, int hidden, float eps, bool bf16, void *scratch,
-                   size_t scratch_bytes, hipStream_t st, const float *res_y = nullptr,
-                   const float *res_mod = nullptr, float *defer_y = nullptr);
 
 }  // namespace anima_hip

@@ -157,9 +157,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvJob *jobs, int B, i
 // g = x * 0.5 * (1 + erf(x / sqrt(2))) of h [M][N] (N % 8 == 0) into hi/lo
 // rows of N bf16.
 struct GeluArgs {
-    const void *h;  // f32, or bf16 (H_BF16)
+    const void *h;  // f32, or bf16 (H_BF16), rows of N
     unsigned int *hi, *lo;
-    int64_t n8;  // M * N / 8
+    int64_t n8;     // M * N / 8
+    int64_t row8;   // N / 8
+    int64_t tld;    // term row stride (elements): N, or 2N for [hi | lo] rows
 };
 
 template <bool H_BF16>
@@ -188,7 +190,9 @@ __global__ __launch_bounds__(256) void gelu_terms_kernel(GeluArgs a)
 #pragma unroll
     for (int e = 0; e < 8; ++e)
         g[e] = x[e] * 0.5f * (1.0f + erff(x[e] * 0.70710678118654752440f));
-    store_terms8(g, a.hi + 4 * i, a.lo ? a.lo + 4 * i : nullptr);
+    const int64_t m = i / a.row8;
+    const int64_t off = (m * a.tld + 8 * (i - m * a.row8)) / 2;
+    store_terms8(g, a.hi + off, a.lo ? a.lo + off : nullptr);
 }
 
 // ---- patch embedding input ------------------------------------------------
@@ -287,6 +291,33 @@ __global__ __launch_bounds__(256) void widen_kernel(const uint16_t *in, float *o
         out[i] = __uint_as_float(uint32_t(in[i]) << 16);
 }
 
+// dst row n = reps copies of src row n, each zero-padded from K to kp
+// elements (kp % 8 == 0): one thread per 8 destination elements.
+struct RepArgs {
+    const uint16_t *src;
+    uint16_t *dst;
+    int64_t ld_src, ld_dst, rows;
+    int K, kp, reps;
+};
+
+__global__ __launch_bounds__(256) void rep_rows_kernel(RepArgs a)
+{
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t per_row = int64_t(a.reps) * a.kp / 8;
+    if (i >= a.rows * per_row)
+        return;
+    const int64_t n = i / per_row;
+    const int col = int(i - n * per_row) * 8;
+    const int k0 = col % a.kp;
+    unsigned short v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        v[e] = k0 + e < a.K ? a.src[n * a.ld_src + k0 + e] : 0;
+    *reinterpret_cast<uint4 *>(a.dst + n * a.ld_dst + col) =
+        uint4{v[0] | (unsigned(v[1]) << 16), v[2] | (unsigned(v[3]) << 16),
+              v[4] | (unsigned(v[5]) << 16), v[6] | (unsigned(v[7]) << 16)};
+}
+
 unsigned grid1(int64_t n) { return unsigned((n + 255) / 256); }
 
 bool launch_gemv(const GemvJob *jobs, int njobs, int maxN, int B, int K, hipStream_t st)
@@ -307,92 +338,7 @@ bool launch_gemv(const GemvJob *jobs, int njobs, int maxN, int B, int K, hipStre
     return hip_ok(hipGetLastError(), "gemv_kernel launch");
 }
 
-// Scratch regions of the MLP sub-layer, 256-byte aligned, in order.
-struct MlpScratch {
-    size_t terms, h, g, y, total;
-};
-
-MlpScratch mlp_scratch(int64_t M, int Dm, int hidden, bool bf16)
-{
-    MlpScratch s{};
-    s.terms = round_up256(size_t(M) * size_t(linear_terms_ld(Dm)) * 2) * (bf16 ? 1 : 2);
-    s.h = round_up256(size_t(M) * hidden * (bf16 ? 2 : 4));  // layer1 output
-    s.g = round_up256(size_t(M) * size_t(linear_terms_ld(hidden)) * 2) * (bf16 ? 1 : 2);
-    s.y = round_up256(size_t(M) * Dm * 4);
-    s.total = s.terms + s.h + s.g + s.y;
-    return s;
-}
-
 }  // namespace
-
-size_t mlp_block_scratch_bytes(int B, int S, int Dm, int hidden, bool bf16)
-{
-    return mlp_scratch(int64_t(B) * S, Dm, hidden, bf16).total;
-}
-
-// The MLP sub-layer of NumpyBlock.forward (numpy_dit.py:249-253) with
-// NumpyMLP (numpy_dit.py:304-317): x += gate[b] * layer2(gelu(layer1(
-// layernorm(x) * (1 + scale[b]) + shift[b]))), mod [B][3][Dm].
-bool run_mlp_block(float *x, const float *mod, const uint16_t *w1, const uint16_t *w2, int B,
-                   int S, int Dm, int hidden, float eps, bool bf16, void *scratch,
-                   size_t scratch_bytes, hipStream_t st, const float *res_y,
-                   const float *res_mod, float *defer_y)
-{
-    const int64_t M = int64_t(B) * S;
-    if (M == 0)
-        return true;
-    if (Dm % 8 || hidden % 8)
-        return fail("mlp_block: the model width and the hidden width must be multiples of 8");
-    if (!x || !mod || !w1 || !w2)
-        return fail("mlp_block: null pointer");
-    const MlpScratch s = mlp_scratch(M, Dm, hidden, bf16);
-    if (!scratch || scratch_bytes < s.total || !aligned16(scratch))
-        return fail("mlp_block: scratch smaller than the size query or not 16-byte aligned");
-    char *cur = static_cast<char *>(scratch);
-    auto take = [&](size_t n) {
-        char *r = cur;
-        cur += n;
-        return r;
-    };
-    uint16_t *hi = reinterpret_cast<uint16_t *>(take(s.terms));
-    uint16_t *lo = bf16 ? nullptr : hi + (s.terms / 2) / sizeof(uint16_t);
-    void *h = take(s.h);
-    uint16_t *ghi = reinterpret_cast<uint16_t *>(take(s.g));
-    uint16_t *glo = bf16 ? nullptr : ghi + (s.g / 2) / sizeof(uint16_t);
-    float *y = reinterpret_cast<float *>(take(s.y));
-
-    // layer1: f32 output in f32 mode; in bf16 mode the product rounds to
-    // bf16 on the way out, halving the round trip through the GELU pass.
-    if (!launch_ln_modulate(x, Dm, mod, 3 * int64_t(Dm), hi, lo, M, S, Dm, eps, st, x, res_y,
-                            res_y ? res_mod + 2 * int64_t(Dm) : nullptr, 3 * int64_t(Dm)))
-        return false;
-    const bool ok1 = bf16 ? launch_linear_terms_bf16out(hi, w1, Dm, static_cast<uint16_t *>(h),
-                                                        hidden, int(M), hidden, Dm, st)
-                          : launch_linear_terms(hi, lo, w1, Dm, static_cast<float *>(h), hidden,
-                                                int(M), hidden, Dm, st);
-    if (!ok1)
-        return false;
-    GeluArgs ga;
-    ga.h = h;
-    ga.hi = reinterpret_cast<unsigned int *>(ghi);
-    ga.lo = reinterpret_cast<unsigned int *>(glo);
-    ga.n8 = M * hidden / 8;
-    if (bf16)
-        hipLaunchKernelGGL(gelu_terms_kernel<true>, dim3(grid1(ga.n8)), dim3(256), 0, st, ga);
-    else
-        hipLaunchKernelGGL(gelu_terms_kernel<false>, dim3(grid1(ga.n8)), dim3(256), 0, st, ga);
-    if (!hip_ok(hipGetLastError(), "gelu_terms_kernel launch"))
-        return false;
-    if (defer_y)  // the next norm pass applies x += gate * y
-        return launch_linear_terms(ghi, glo, w2, hidden, defer_y, Dm, int(M), Dm, hidden, st);
-    // layer2 and the gated residual: fused in bf16 mode (see block.hip).
-    if (bf16 && linear_residual_supported(S, Dm, hidden, w2, hidden, x, Dm))
-        return launch_linear_residual_terms(ghi, w2, hidden, x, Dm, mod + 2 * int64_t(Dm),
-                                            3 * int64_t(Dm), B, S, Dm, hidden, st);
-    if (!launch_linear_terms(ghi, glo, w2, hidden, y, Dm, int(M), Dm, hidden, st))
-        return false;
-    return launch_gate_residual(x, y, mod, M, S, Dm, st);
-}
 
 }  // namespace anima_hip
 
@@ -407,6 +353,12 @@ struct BlockWeights {
     const float *sa_qn = nullptr, *sa_kn = nullptr, *cx_qn = nullptr, *cx_kn = nullptr;
     const uint16_t *ada1[3] = {nullptr, nullptr, nullptr}, *ada2[3] = {nullptr, nullptr, nullptr};
     void *ctx_k = nullptr, *ctx_v = nullptr;  // cross-attention cache (owned)
+    // GEMM-ready weights: q, k and v rows stacked into one [3*H*D] x ld_d
+    // matrix (owned); in f32 mode every weight row repeated as [W | W] so a
+    // layer is one product with [hi | lo] activation rows (owned), in bf16
+    // mode the originals.
+    const uint16_t *w_qkv = nullptr, *w_o = nullptr, *w_cq = nullptr, *w_co = nullptr;
+    const uint16_t *w_fc1 = nullptr, *w_fc2 = nullptr;
 };
 
 }  // namespace
@@ -421,6 +373,8 @@ struct anima_hip_dit {
     const float *t_norm = nullptr;
     const uint16_t *fin_ada1 = nullptr, *fin_ada2 = nullptr, *fin_lin = nullptr;
     int kp_in = 0;                    // padded patch feature count
+    int reps = 1;                     // activation terms per element: 2 (f32), 1 (bf16)
+    int64_t ld_d = 0, ld_hd = 0, ld_hid = 0;  // term/weight row strides of D, H*D, hidden inputs
     // Per-forward vectors (sized for cfg.max_batch), owned.
     float *feat = nullptr, *h1 = nullptr, *h1s = nullptr, *emb = nullptr, *semb = nullptr;
     float *lora = nullptr, *m1 = nullptr, *mods = nullptr;
@@ -480,6 +434,38 @@ void grid_of(int T, int H, int W, int &Hp, int &Wp, int64_t &S)
     S = int64_t(T) * Hp * Wp;
 }
 
+// Arena regions of one sub-layer (kind 0 self-attention, 1 cross-attention,
+// 2 MLP), 256-byte aligned, in order: activation terms, then
+//   self:  qkv [M][3HD] f32, o [M][HD] f32, attention scratch, o's terms;
+//   cross: q [M][HD] f32,    o [M][HD] f32, attention scratch, o's terms;
+//   mlp:   h [M][hidden] (f32, bf16 in bf16 mode), GELU terms [M][ld_hid].
+struct SubLayout {
+    size_t terms, a, b, attn, lin, total;
+};
+
+SubLayout sub_layout(const anima_hip_dit *d, int B, int64_t S, int kind)
+{
+    const anima_hip_dit_config &c = d->cfg;
+    const size_t M = size_t(B) * S, HD = size_t(c.heads) * c.head_dim;
+    SubLayout l{};
+    l.terms = round_up256(M * size_t(d->ld_d) * 2);
+    if (kind == 2) {
+        l.a = round_up256(M * c.mlp_hidden * (d->bf16 ? 2 : 4));
+        l.b = round_up256(M * size_t(d->ld_hid) * 2);
+    } else {
+        l.a = round_up256(M * HD * 4 * (kind == 0 ? 3 : 1));
+        l.b = round_up256(M * HD * 4);
+        l.attn = round_up256(kind == 0 ? attention_scratch_bytes(B, int(S), B, int(S), c.heads,
+                                                                 c.head_dim, d->bf16, false)
+                                       : attention_scratch_bytes(B, int(S), std::max(d->ctx_B, 1),
+                                                                 std::max(d->ctx_S, 1), c.heads,
+                                                                 c.head_dim, d->bf16, true));
+        l.lin = round_up256(M * size_t(linear_terms_ld(int(HD))) * 2 * d->reps);
+    }
+    l.total = l.terms + l.a + l.b + l.attn + l.lin;
+    return l;
+}
+
 // Scratch regions of one forward, 256-byte aligned, in order.
 struct DitScratch {
     size_t x, y, patch, f, arena, total;
@@ -489,18 +475,14 @@ DitScratch dit_scratch(const anima_hip_dit *d, int B, int64_t S)
 {
     const anima_hip_dit_config &c = d->cfg;
     const int64_t M = int64_t(B) * S;
-    const bool bf16 = d->bf16;
     DitScratch s{};
     s.x = round_up256(size_t(M) * c.dim * 4);
     s.y = s.x;
     s.patch = round_up256(size_t(M) * d->kp_in * 2) * 2;
     s.f = round_up256(size_t(M) * 4 * c.out_channels * 4);
-    size_t arena = attention_block_scratch_bytes(B, int(S), c.dim, c.heads, c.head_dim, B, int(S),
-                                                 bf16, false);
-    arena = std::max(arena, attention_block_scratch_bytes(B, int(S), c.dim, c.heads, c.head_dim,
-                                                          std::max(d->ctx_B, 1),
-                                                          std::max(d->ctx_S, 1), bf16, true));
-    arena = std::max(arena, mlp_block_scratch_bytes(B, int(S), c.dim, c.mlp_hidden, bf16));
+    const SubLayout self = sub_layout(d, B, S, 0), cross = sub_layout(d, B, S, 1),
+                    mlp = sub_layout(d, B, S, 2);
+    size_t arena = std::max(self.total, std::max(cross.total, mlp.total));
     arena = std::max(arena, round_up256(size_t(M) * linear_terms_ld(c.dim) * 2) * 2);
     s.arena = round_up256(arena);
     s.total = s.x + s.y + s.patch + s.f + s.arena;
@@ -516,6 +498,111 @@ bool check_cfg(const anima_hip_dit_config &c)
         return fail("dit: invalid configuration (widths multiples of 8, model width <= 4096, "
                     "max_batch 1..4)");
     return true;
+}
+
+// x += gate * y of the pending sub-layer (when pend_y), then LayerNorm +
+// modulate into activation terms: [hi | lo] rows in f32 mode, hi rows in
+// bf16 mode (row stride ld_d either way).
+bool dit_norm(const anima_hip_dit *d, float *x, const float *mod, const float *pend_y,
+              const float *pend_mod, uint16_t *terms, int64_t M, int S, hipStream_t st)
+{
+    const int D = d->cfg.dim;
+    uint16_t *lo = d->reps == 2 ? terms + linear_terms_ld(D) : nullptr;
+    return launch_ln_modulate(x, D, mod, 3 * int64_t(D), terms, lo, M, S, D, 1e-6f, st, x, pend_y,
+                              pend_y ? pend_mod + 2 * int64_t(D) : nullptr, 3 * int64_t(D),
+                              d->ld_d);
+}
+
+// out [M][N] = a . W^T for f32 activations a [M][K]: split into terms here
+// ([hi | lo] rows with the repeated weight in f32 mode), one product.
+bool dit_linear(const anima_hip_dit *d, const float *a, int K, const uint16_t *w, int64_t ld_w,
+                float *out, int N, int64_t M, void *lin, size_t lin_bytes, hipStream_t st)
+{
+    if (d->reps == 2) {
+        const uint16_t *t = launch_split_interleaved(a, K, int(M), K, lin, lin_bytes, st);
+        return t && launch_linear_terms(t, nullptr, w, ld_w, out, N, int(M), N, int(ld_w), st);
+    }
+    return launch_linear(a, K, w, ld_w, out, N, int(M), N, K, false, lin, lin_bytes, st);
+}
+
+// One sub-layer of block bw on the residual stream x (kind as sub_layout),
+// after applying the pending residual; its output projection goes to y.
+bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, float *x,
+                  const float *mod, const float *pend_y, const float *pend_mod, float *y, int B,
+                  int64_t S, const float *freqs, void *arena, hipStream_t st)
+{
+    const anima_hip_dit_config &c = d->cfg;
+    const int D = c.dim, HD = c.heads * c.head_dim;
+    const int64_t M = int64_t(B) * S;
+    const SubLayout l = sub_layout(d, B, S, kind);
+    char *cur = static_cast<char *>(arena);
+    uint16_t *terms = reinterpret_cast<uint16_t *>(cur);
+    char *ra = cur + l.terms, *rb = ra + l.a, *rattn = rb + l.b, *rlin = rattn + l.attn;
+    if (!dit_norm(d, x, mod, pend_y, pend_mod, terms, M, int(S), st))
+        return false;
+    if (kind == 2) {  // NumpyMLP (numpy_dit.py:304-317)
+        const int hid = c.mlp_hidden;
+        const bool ok1 = d->bf16 ? launch_linear_terms_bf16out(terms, bw.w_fc1, d->ld_d,
+                                                               reinterpret_cast<uint16_t *>(ra),
+                                                               hid, int(M), hid, D, st)
+                                 : launch_linear_terms(terms, nullptr, bw.w_fc1, d->ld_d,
+                                                       reinterpret_cast<float *>(ra), hid,
+                                                       int(M), hid, int(d->ld_d), st);
+        if (!ok1)
+            return false;
+        GeluArgs ga;
+        ga.h = ra;
+        ga.hi = reinterpret_cast<unsigned int *>(rb);
+        ga.lo = d->reps == 2 ? ga.hi + linear_terms_ld(hid) / 2 : nullptr;
+        ga.n8 = M * hid / 8;
+        ga.row8 = hid / 8;
+        ga.tld = d->ld_hid;
+        if (d->bf16)
+            hipLaunchKernelGGL(gelu_terms_kernel<true>, dim3(grid1(ga.n8)), dim3(256), 0, st, ga);
+        else
+            hipLaunchKernelGGL(gelu_terms_kernel<false>, dim3(grid1(ga.n8)), dim3(256), 0, st, ga);
+        return hip_ok(hipGetLastError(), "gelu_terms_kernel launch") &&
+               launch_linear_terms(reinterpret_cast<const uint16_t *>(rb), nullptr, bw.w_fc2,
+                                   d->ld_hid, y, D, int(M), D, int(d->ld_hid), st);
+    }
+    // NumpyAttention.forward (numpy_dit.py:268-297): self-attention projects
+    // q, k and v in one product; cross-attention projects q and reads the
+    // block's context cache.
+    float *proj = reinterpret_cast<float *>(ra), *o = reinterpret_cast<float *>(rb);
+    AttnInputs in;
+    in.B = B;
+    in.S_q = int(S);
+    in.H = c.heads;
+    in.D = c.head_dim;
+    in.eps = 1e-6f;
+    in.bf16 = d->bf16;
+    in.out = o;
+    if (kind == 0) {
+        if (!launch_linear_terms(terms, nullptr, bw.w_qkv, d->ld_d, proj, 3 * HD, int(M), 3 * HD,
+                                 int(d->ld_d), st))
+            return false;
+        in.q = proj;
+        in.k = proj + HD;
+        in.v = proj + 2 * HD;
+        in.ld_q = in.ld_kv = 3 * int64_t(HD);
+        in.q_norm_w = bw.sa_qn;
+        in.k_norm_w = bw.sa_kn;
+        in.freqs = freqs;
+        in.Bk = B;
+        in.S_kv = int(S);
+    } else {
+        if (!launch_linear_terms(terms, nullptr, bw.w_cq, d->ld_d, proj, HD, int(M), HD,
+                                 int(d->ld_d), st))
+            return false;
+        in.q = proj;
+        in.q_norm_w = bw.cx_qn;
+        in.k_prep = bw.ctx_k;
+        in.v_prep = bw.ctx_v;
+        in.Bk = d->ctx_B;
+        in.S_kv = d->ctx_S;
+    }
+    return run_attention(in, rattn, st) &&
+           dit_linear(d, o, HD, kind == 0 ? bw.w_o : bw.w_co, d->ld_hd, y, D, M, rlin, l.lin, st);
 }
 
 // The forward pass on B batch entries of the latent x ([B][C][T][H][W] with
@@ -609,48 +696,13 @@ bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, i
     const int64_t mod_stride = int64_t(c.max_batch) * 3 * D;  // one modulation's rows
     const float *pend_mod = nullptr;                           // modulation owning yp
     for (int i = 0; i < c.blocks; ++i) {
-        const BlockWeights &bw = d->blk[i];
-        BlockProblem p;
-        p.x = xr;
-        p.B = B;
-        p.S = int(S);
-        p.Dm = D;
-        p.H = c.heads;
-        p.D = c.head_dim;
-        p.eps = 1e-6f;
-        p.bf16 = d->bf16;
-        p.mod = d->mods + (3 * i + 0) * mod_stride;
-        p.wq = bw.sa_q;
-        p.wk = bw.sa_k;
-        p.wv = bw.sa_v;
-        p.wo = bw.sa_o;
-        p.q_norm_w = bw.sa_qn;
-        p.k_norm_w = bw.sa_kn;
-        p.freqs = freqs;
-        p.res_y = pend_mod ? yp : nullptr;
-        p.res_mod = pend_mod;
-        p.defer_y = yp;
-        if (!run_attention_block(p, arena, s.arena, st))
-            return false;
-        p.res_y = yp;
-        p.res_mod = p.mod;
-        p.mod = d->mods + (3 * i + 1) * mod_stride;
-        p.wq = bw.cx_q;
-        p.wk = p.wv = nullptr;
-        p.wo = bw.cx_o;
-        p.q_norm_w = bw.cx_qn;
-        p.k_norm_w = bw.cx_kn;
-        p.freqs = nullptr;
-        p.k_prep = bw.ctx_k;
-        p.v_prep = bw.ctx_v;
-        p.Bk = d->ctx_B;
-        p.S_kv = d->ctx_S;
-        const float *mlp_mod = d->mods + (3 * i + 2) * mod_stride;
-        if (!run_attention_block(p, arena, s.arena, st) ||
-            !run_mlp_block(xr, mlp_mod, bw.fc1, bw.fc2, B, int(S), D, c.mlp_hidden, 1e-6f,
-                           d->bf16, arena, s.arena, st, yp, p.mod, yp))
-            return false;
-        pend_mod = mlp_mod;
+        for (int kind = 0; kind < 3; ++kind) {
+            const float *mod = d->mods + (3 * i + kind) * mod_stride;
+            if (!dit_sublayer(d, d->blk[i], kind, xr, mod, pend_mod ? yp : nullptr, pend_mod, yp,
+                              B, S, freqs, arena, st))
+                return false;
+            pend_mod = mod;
+        }
     }
 
     // Final layer: LN + modulate (shift, scale) and the output linear.
@@ -868,6 +920,52 @@ anima_hip_dit *anima_hip_dit_create(const anima_hip_dit_config *cfg, const char 
         ok = hip_ok(hipMemcpy(d->jobs, jobs.data(), jobs.size() * sizeof(GemvJob),
                               hipMemcpyHostToDevice),
                     "dit job table upload");
+    }
+    // GEMM-ready weights (see BlockWeights).
+    const int kpD = int(linear_terms_ld(D)), kpHD = int(linear_terms_ld(HD));
+    const int kpH = int(linear_terms_ld(c.mlp_hidden));
+    d->reps = d->bf16 ? 1 : 2;
+    d->ld_d = int64_t(d->reps) * kpD;
+    d->ld_hd = int64_t(d->reps) * kpHD;
+    d->ld_hid = int64_t(d->reps) * kpH;
+    auto repeat = [&](const uint16_t *src, int64_t rows, int K, uint16_t *dst, int64_t ld_dst,
+                      int kp) {
+        RepArgs ra;
+        ra.src = src;
+        ra.dst = dst;
+        ra.ld_src = K;
+        ra.ld_dst = ld_dst;
+        ra.rows = rows;
+        ra.K = K;
+        ra.kp = kp;
+        ra.reps = d->reps;
+        const int64_t n = rows * d->reps * kp / 8;
+        hipLaunchKernelGGL(rep_rows_kernel, dim3(grid1(n)), dim3(256), 0, st, ra);
+        return hip_ok(hipGetLastError(), "rep_rows_kernel launch");
+    };
+    auto prepared = [&](const uint16_t *src, int64_t rows, int K, int kp) -> const uint16_t * {
+        if (d->reps == 1)
+            return src;  // K == kp: the original rows are GEMM-ready
+        uint16_t *w = nullptr;
+        if (!dev_alloc(d, w, size_t(rows) * 2 * kp * 2, "dit repeated weight") ||
+            !repeat(src, rows, K, w, 2 * int64_t(kp), kp))
+            return nullptr;
+        return w;
+    };
+    for (int i = 0; ok && i < c.blocks; ++i) {
+        BlockWeights &b = d->blk[i];
+        uint16_t *qkv = nullptr;
+        ok = dev_alloc(d, qkv, size_t(3) * HD * d->ld_d * 2, "dit q/k/v weight") &&
+             repeat(b.sa_q, HD, D, qkv, d->ld_d, kpD) &&
+             repeat(b.sa_k, HD, D, qkv + int64_t(HD) * d->ld_d, d->ld_d, kpD) &&
+             repeat(b.sa_v, HD, D, qkv + 2 * int64_t(HD) * d->ld_d, d->ld_d, kpD);
+        b.w_qkv = qkv;
+        b.w_o = ok ? prepared(b.sa_o, D, HD, kpHD) : nullptr;
+        b.w_cq = b.w_o ? prepared(b.cx_q, HD, D, kpD) : nullptr;
+        b.w_co = b.w_cq ? prepared(b.cx_o, D, HD, kpHD) : nullptr;
+        b.w_fc1 = b.w_co ? prepared(b.fc1, c.mlp_hidden, D, kpD) : nullptr;
+        b.w_fc2 = b.w_fc1 ? prepared(b.fc2, D, c.mlp_hidden, kpH) : nullptr;
+        ok = ok && b.w_fc2;
     }
     ok = ok && hip_ok(hipStreamSynchronize(st), "dit_create");
     if (!ok) {

@@ -40,6 +40,7 @@ struct SplitArgs {
     int64_t lda;
     unsigned int *hi, *lo;  // [M][Kp] bf16, addressed as bf16 pairs
     int64_t kp;             // padded row length (elements)
+    int64_t rs;             // row stride of hi/lo (elements): kp, or 2*kp for [hi | lo] rows
     int M, K, vec;
     int64_t total;          // M * Kp / 8 chunks
 };
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(256) void split_kernel(SplitArgs a)
         // x - hi is exact in f32 (hi holds the leading bits of x).
         l[e] = pack_pair(x[2 * e] - bf16_lo_value(h[e]), x[2 * e + 1] - bf16_hi_value(h[e]));
     }
-    const int64_t off = (m * a.kp + k0) / 2;
+    const int64_t off = (m * a.rs + k0) / 2;
     *reinterpret_cast<uint4 *>(a.hi + off) = uint4{h[0], h[1], h[2], h[3]};
     if (a.lo)
         *reinterpret_cast<uint4 *>(a.lo + off) = uint4{l[0], l[1], l[2], l[3]};
@@ -205,6 +206,38 @@ bool launch_linear_terms(const uint16_t *hi, const uint16_t *lo, const uint16_t 
     return !lo || lt_matmul(plan, w, lo, c, 1.0f, st);
 }
 
+uint16_t *launch_split_interleaved(const float *a, int64_t lda, int M, int K, void *scratch,
+                                   size_t scratch_bytes, hipStream_t st)
+{
+    const int64_t kp = padded_k(K);
+    if (M <= 0 || K <= 0 || lda < K || !scratch ||
+        scratch_bytes < size_t(M) * size_t(kp) * 4 ||
+        (reinterpret_cast<uintptr_t>(scratch) & 15u) != 0) {
+        fail("split: bad sizes or scratch smaller than 2 terms per element");
+        return nullptr;
+    }
+    SplitArgs sa;
+    sa.a = a;
+    sa.lda = lda;
+    sa.hi = static_cast<unsigned int *>(scratch);
+    sa.lo = sa.hi + kp / 2;  // [hi | lo] in each row
+    sa.kp = kp;
+    sa.rs = 2 * kp;
+    sa.M = M;
+    sa.K = K;
+    sa.vec = (reinterpret_cast<uintptr_t>(a) & 15u) == 0 && lda % 4 == 0;
+    sa.total = int64_t(M) * kp / 8;
+    const int64_t nblk = (sa.total + 255) / 256;
+    if (nblk > INT32_MAX) {
+        fail("split: problem too large for one launch");
+        return nullptr;
+    }
+    hipLaunchKernelGGL(split_kernel, dim3(unsigned(nblk)), dim3(256), 0, st, sa);
+    if (!hip_ok(hipGetLastError(), "split_kernel launch"))
+        return nullptr;
+    return static_cast<uint16_t *>(scratch);
+}
+
 bool launch_linear_terms_bf16out(const uint16_t *hi, const uint16_t *w, int64_t ldw, uint16_t *c,
                                  int64_t ldc, int M, int N, int K, hipStream_t st)
 {
@@ -256,6 +289,7 @@ bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, 
                                                     round_up256(size_t(M) * kp * 2))
                  : nullptr;
     s.kp = kp;
+    s.rs = kp;
     s.M = M;
     s.K = K;
     s.vec = (reinterpret_cast<uintptr_t>(a) & 15u) == 0 && lda % 4 == 0;
@@ -303,6 +337,7 @@ bool launch_linear_residual(const float *a, int64_t lda, const uint16_t *w, int6
     sa.hi = static_cast<unsigned int *>(scratch);
     sa.lo = nullptr;
     sa.kp = kp;
+    sa.rs = kp;
     sa.M = M;
     sa.K = K;
     sa.vec = (reinterpret_cast<uintptr_t>(a) & 15u) == 0 && lda % 4 == 0;
