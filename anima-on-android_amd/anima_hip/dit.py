@@ -193,6 +193,7 @@ class AnimaDiT:
         if self._ctx_host is not None and self._ctx_host.shape == ctx.shape and \
                 np.array_equal(self._ctx_host, ctx):
             return
+        self._ctx_host = None  # the device holds no valid context until this succeeds
         d = self._buf("ctx", ctx.nbytes)
         d.upload(ctx)
         _lib.check(self._lib.anima_hip_dit_set_context_dev(self._h, d.ptr, ctx.shape[0],

@@ -381,7 +381,9 @@ struct anima_hip_dit {
     GemvJob *jobs = nullptr;          // device table: t1, t2, layer-1 x n_ada, layer-2 x n_ada
     int n_ada = 0;
     std::vector<void *> owned;        // device allocations freed at destroy
-    // Context cache state.
+    // Context caches: allocated for alloc_B x alloc_S; valid (a context is
+    // set) only when ctx_B > 0, which set_context clears first and sets last.
+    int alloc_B = 0, alloc_S = 0;
     int ctx_B = 0, ctx_S = 0;
     void *ctx_work = nullptr;
     size_t ctx_work_bytes = 0;
@@ -619,9 +621,9 @@ bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, i
         return fail("dit: latent dimensions must be positive");
     if (!x || !sigma || (!freqs && c.blocks > 0))
         return fail("dit: null pointer");
-    if (c.blocks > 0 && !d->blk[0].ctx_k)
+    if (c.blocks > 0 && d->ctx_B == 0)
         return fail("dit: no text context set (anima_hip_dit_set_context_dev)");
-    if (d->ctx_B != 1 && d->ctx_B != B && c.blocks > 0)
+    if (c.blocks > 0 && d->ctx_B != 1 && d->ctx_B != B)
         return fail("dit: the context batch must be 1 or the forward batch");
     int Hp, Wp;
     int64_t S;
@@ -993,7 +995,9 @@ bool anima_hip_dit_set_context_dev(anima_hip_dit *d, const float *ctx, int Bc, i
     if (M64 > INT32_MAX / 8)
         return fail("dit_set_context: context too long");
     const int M = int(M64);
-    if (Bc != d->ctx_B || S_kv != d->ctx_S) {
+    // No context is valid until every block's cache is rebuilt.
+    d->ctx_B = d->ctx_S = 0;
+    if (Bc != d->alloc_B || S_kv != d->alloc_S) {
         // New cache shape: drain the device before the old caches go.
         if (!hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize"))
             return false;
@@ -1004,7 +1008,7 @@ bool anima_hip_dit_set_context_dev(anima_hip_dit *d, const float *ctx, int Bc, i
                 (void)hipFree(b.ctx_v);
             b.ctx_k = b.ctx_v = nullptr;
         }
-        d->ctx_B = d->ctx_S = 0;
+        d->alloc_B = d->alloc_S = 0;
         for (auto &b : d->blk) {
             if (!hip_ok(hipMalloc(&b.ctx_k, prepared_k_bytes(Bc, S_kv, H, hd, d->bf16)),
                         "dit context K cache") ||
@@ -1012,6 +1016,8 @@ bool anima_hip_dit_set_context_dev(anima_hip_dit *d, const float *ctx, int Bc, i
                         "dit context V cache"))
                 return false;
         }
+        d->alloc_B = Bc;
+        d->alloc_S = S_kv;
     }
     const size_t proj = round_up256(size_t(M) * HD * 4);
     const size_t lin = round_up256(linear_scratch_bytes(M, C, !d->bf16));
