@@ -19,6 +19,7 @@ from . import _lib
 
 F32 = 0
 BF16 = 1
+F32X3 = 2  # f32 operands as bf16 term pairs on bf16 MFMA (three products each)
 
 
 def _f32(a) -> np.ndarray:
@@ -66,7 +67,7 @@ def sdpa_flash(q, k, v, scale=None, is_causal=False) -> np.ndarray:
 
 
 def sdpa(q, k, v, scale=None, is_causal=False, mode=F32) -> np.ndarray:
-    """anima_hip_sdpa: sdpa_flash with an arithmetic mode (F32 or BF16)."""
+    """anima_hip_sdpa: sdpa_flash with an arithmetic mode (F32, BF16 or F32X3)."""
     q, k, v = _f32(q), _f32(k), _f32(v)
     BH, Sq, D = q.shape
     Sk = k.shape[1]

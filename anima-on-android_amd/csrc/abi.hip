@@ -205,8 +205,9 @@ bool finish_call(Runtime &r)
 
 // Shared body of the host-pointer SDPA entries ([BH, S, D] f32 host arrays).
 bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int BH, int S_q,
-               int S_kv, int D, float scale, bool causal, bool bf16)
+               int S_kv, int D, float scale, bool causal, int mode)
 {
+    const bool bf16 = mode == ANIMA_HIP_BF16, x3 = mode == ANIMA_HIP_F32X3;
     if (!check_dims(1, BH, S_q, S_kv, D))
         return false;
     const int64_t nq = int64_t(BH) * S_q * D, nk = int64_t(BH) * S_kv * D;
@@ -214,8 +215,8 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
         return true;
     if (!Q || !out || (nk > 0 && (!K || !V)))
         return fail("sdpa: null pointer");
-    if (bf16 && D != 128)
-        return fail("sdpa: the bf16 mode needs D == 128");
+    if ((bf16 || x3) && D != 128)
+        return fail(std::string("sdpa: the ") + (bf16 ? "bf16" : "f32x3") + " mode needs D == 128");
     Runtime &r = rt();
     const hipStream_t st = r.stream;
     begin_call(r);
@@ -242,18 +243,21 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
     p.D = D;
     p.scale = scale;
     p.causal = causal;
-    if (bf16) {
-        // bf16 copies of Q and K (row kernel without norm/RoPE) and packed V^T.
-        const int64_t sp = vt_padded_len(S_kv);
-        if (!r.q2.reserve(nq * 2, "workspace q bf16") || !r.k2.reserve(nk * 2, "workspace k bf16") ||
-            !r.v2.reserve(size_t(BH) * D * sp * 2, "workspace v^T"))
+    if (bf16 || x3) {
+        // bf16 copies of Q and K (row kernel without norm/RoPE; rows of [hi |
+        // lo] terms in the f32x3 mode) and packed V^T (hi rows, then lo rows).
+        const int64_t sp = vt_padded_len(S_kv), w = x3 ? 2 : 1;
+        if (!r.q2.reserve(nq * 2 * w, "workspace q bf16") ||
+            !r.k2.reserve(nk * 2 * w, "workspace k bf16") ||
+            !r.v2.reserve(size_t(BH) * w * D * sp * 2, "workspace v^T"))
             return false;
         RowProblem c;
         c.x = static_cast<const float *>(r.q.p);
         c.out = r.q2.p;
         c.w = nullptr;
         c.freqs = nullptr;
-        c.xs = c.os = Strides{0, int64_t(S_q) * D, int64_t(D)};
+        c.xs = Strides{0, int64_t(S_q) * D, int64_t(D)};
+        c.os = Strides{0, int64_t(S_q) * D * w, int64_t(D) * w};
         c.B = 1;
         c.S = S_q;
         c.H = BH;
@@ -261,21 +265,28 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
         c.eps = 0.0f;
         c.norm = false;
         c.out_bf16 = true;
+        c.lo_off = x3 ? D : 0;
         RowProblem ck = c;
         ck.x = static_cast<const float *>(r.k.p);
         ck.out = r.k2.p;
-        ck.xs = ck.os = Strides{0, int64_t(S_kv) * D, int64_t(D)};
+        ck.xs = Strides{0, int64_t(S_kv) * D, int64_t(D)};
+        ck.os = Strides{0, int64_t(S_kv) * D * w, int64_t(D) * w};
         ck.S = S_kv;
-        const Strides vts{0, int64_t(D) * sp, sp};
+        const Strides vts{0, w * D * sp, sp};
+        const float *vf = static_cast<const float *>(r.v.p);
+        uint16_t *vt = static_cast<uint16_t *>(r.v2.p);
         if (!launch_rows(c, st) || !launch_rows(ck, st) ||
-            !launch_vt_pack(static_cast<const float *>(r.v.p), p.vs,
-                            static_cast<uint16_t *>(r.v2.p), vts, 1, BH, S_kv, D, st))
+            !(x3 ? launch_vt_pack_terms(vf, p.vs, vt, vts, 1, BH, S_kv, D, st)
+                 : launch_vt_pack(vf, p.vs, vt, vts, 1, BH, S_kv, D, st)))
             return false;
         p.q = r.q2.p;
         p.k = r.k2.p;
         p.v = r.v2.p;
+        p.qs = c.os;
+        p.ks = ck.os;
         p.vs = vts;
-        if (!launch_flash_bf16(p, st, r.scratch.p, part_bytes))
+        if (!(x3 ? launch_flash_x3(p, st, r.scratch.p, part_bytes)
+                 : launch_flash_bf16(p, st, r.scratch.p, part_bytes)))
             return false;
     } else if (!launch_flash_f32(p, st, r.scratch.p, part_bytes)) {
         return false;
@@ -381,7 +392,7 @@ bool anima_rt_run_sdpa_flash(const float *Q, const float *K, const float *V, flo
     std::lock_guard<std::recursive_mutex> g(r.mu);
     if (!ensure_ready(r))
         return false;
-    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale, is_causal, false);
+    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale, is_causal, ANIMA_HIP_F32);
 }
 
 bool anima_rt_run_sdpa(const float *Q, const float *K, const float *V, float *out, int BH,
@@ -392,7 +403,7 @@ bool anima_rt_run_sdpa(const float *Q, const float *K, const float *V, float *ou
     if (!r.user_init)
         return fail("anima_rt_run_sdpa: anima_rt_init() has not been called");
     // The reference multiplies both Q and K by `scale`: softmax(scale^2 QK^T)V.
-    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale * scale, is_causal, false);
+    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale * scale, is_causal, ANIMA_HIP_F32);
 }
 
 bool anima_rt_run_rmsnorm(const float *x, const float *w, float *out, int m, int d, float eps)
@@ -572,9 +583,9 @@ bool anima_hip_sdpa(const float *Q, const float *K, const float *V, float *out, 
     std::lock_guard<std::recursive_mutex> g(r.mu);
     if (!ensure_ready(r))
         return false;
-    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16)
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16 && mode != ANIMA_HIP_F32X3)
         return fail("anima_hip_sdpa: unknown mode " + std::to_string(mode));
-    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale, is_causal, mode == ANIMA_HIP_BF16);
+    return host_sdpa(Q, K, V, out, BH, S_q, S_kv, D, scale, is_causal, mode);
 }
 
 const char *anima_hip_last_error(void) { return t_last_error.c_str(); }
@@ -657,6 +668,56 @@ bool anima_hip_pack_vt_dev(const float *v, uint16_t *vt, int B, int H, int S_kv,
                           pick_stream(stream));
 }
 
+bool anima_hip_flash_x3_dev(const uint16_t *q, const uint16_t *k, const uint16_t *vt, float *o,
+                            int B, int H, int S_q, int S_kv, int D, const int64_t *q_strides,
+                            const int64_t *k_strides, const int64_t *vt_strides,
+                            const int64_t *o_strides, float scale, bool is_causal, void *stream)
+{
+    if (!ready_for_device_call() || !check_dims(B, H, S_q, S_kv, D))
+        return false;
+    if (int64_t(B) * H * S_q * D > 0 && (!q || !o || (S_kv > 0 && (!k || !vt))))
+        return fail("flash_x3_dev: null pointer");
+    const int64_t sp = vt_padded_len(S_kv);
+    FlashProblem p;
+    p.q = q;
+    p.k = k;
+    p.v = vt;
+    p.o = o;
+    // Default strides: rows of 2*D terms, [B, H, S, 2D] contiguous.
+    p.qs = q_strides ? Strides{q_strides[0], q_strides[1], q_strides[2]}
+                     : Strides{int64_t(H) * S_q * 2 * D, int64_t(S_q) * 2 * D, 2 * int64_t(D)};
+    p.ks = k_strides ? Strides{k_strides[0], k_strides[1], k_strides[2]}
+                     : Strides{int64_t(H) * S_kv * 2 * D, int64_t(S_kv) * 2 * D, 2 * int64_t(D)};
+    p.vs = vt_strides ? Strides{vt_strides[0], vt_strides[1], vt_strides[2]}
+                      : Strides{int64_t(H) * 2 * D * sp, 2 * int64_t(D) * sp, sp};
+    p.os = from_array(o_strides, H, S_q, D);
+    p.B = B;
+    p.H = H;
+    p.S_q = S_q;
+    p.S_kv = S_kv;
+    p.D = D;
+    p.scale = scale;
+    p.causal = is_causal;
+    return launch_flash_x3(p, pick_stream(stream));
+}
+
+bool anima_hip_pack_vt_terms_dev(const float *v, uint16_t *vt, int B, int H, int S_kv, int D,
+                                 const int64_t *v_strides, const int64_t *vt_strides,
+                                 void *stream)
+{
+    if (!ready_for_device_call() || !check_dims(B, H, S_kv, S_kv, D))
+        return false;
+    if (int64_t(B) * H * S_kv * D > 0 && (!v || !vt))
+        return fail("pack_vt_terms_dev: null pointer");
+    const int64_t sp = vt_padded_len(S_kv);
+    const Strides ts = vt_strides ? Strides{vt_strides[0], vt_strides[1], vt_strides[2]}
+                                  : Strides{int64_t(H) * 2 * D * sp, 2 * int64_t(D) * sp, sp};
+    if (ts.s != sp)
+        return fail("pack_vt_terms_dev: V^T row stride must equal the padded key count");
+    return launch_vt_pack_terms(v, from_array(v_strides, H, S_kv, D), vt, ts, B, H, S_kv, D,
+                                pick_stream(stream));
+}
+
 bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const float *freqs,
                                int B, int S, int H, int D, const int64_t *x_strides,
                                const int64_t *out_strides, float eps, int flags, void *stream)
@@ -681,7 +742,8 @@ bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const 
     p.D = D;
     p.eps = eps;
     p.norm = (flags & 1) != 0;
-    p.out_bf16 = (flags & 2) != 0;
+    p.out_bf16 = (flags & 6) != 0;
+    p.lo_off = (flags & 4) ? D : 0;  // [hi | lo] term rows
     return launch_rows(p, pick_stream(stream));
 }
 

@@ -98,6 +98,18 @@ __host__ __device__ inline int vt_key_pos(int c)
 bool launch_vt_pack(const float *v, Strides vs, uint16_t *vt, Strides vts, int B, int H,
                     int S_kv, int D, hipStream_t st);
 
+// f32-accurate attention on bf16 MFMA (flash_x3.hip): every f32 operand x as
+// two bf16 terms xh = bf16(x), xl = bf16(x - xh), every product as
+// xh*yh + xh*yl + xl*yh.  q, k: rows of 2*D bf16, [hi | lo], addressed
+// through qs/ks (row starts); v: packed term V^T, per (batch, head) the D hi
+// rows then the D lo rows of the V^T layout above, strides {batch, head,
+// d-row = vt_padded_len(S_kv)}.  D == 128, scale > 0.
+bool launch_flash_x3(const FlashProblem &p, hipStream_t st, void *part = nullptr,
+                     size_t part_bytes = 0);
+// Pack V (f32 view as for launch_vt_pack) into the term V^T layout above.
+bool launch_vt_pack_terms(const float *v, Strides vs, uint16_t *vt, Strides vts, int B, int H,
+                          int S_kv, int D, hipStream_t st);
+
 // C[M,N] = A[M,K] . W[N,K]^T with f32 A/C and bf16 (w_bf16) or f32 W, f32
 // accumulation; leading dimensions in elements.
 bool launch_gemm(const float *a, int64_t lda, const void *w, bool w_bf16, int64_t ldw, float *c,
@@ -163,6 +175,9 @@ struct RowProblem {
     float eps;
     bool norm;      // apply RMSNorm
     bool out_bf16;  // write bf16 (round to nearest even) instead of f32
+    // With out_bf16: 0, or the element offset from each output row to a
+    // second row receiving the lo terms bf16(y - bf16(y)).
+    int64_t lo_off = 0;
 };
 bool launch_rows(const RowProblem &p, hipStream_t st);
 // Both problems in one launch when both take the D == 128 float4 kernel, else

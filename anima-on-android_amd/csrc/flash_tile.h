@@ -1,0 +1,129 @@
+// Device helpers shared by the bf16-MFMA flash kernels (flash_bf16.hip,
+// flash_x3.hip): the global -> LDS DMA copy, ring synchronisation, the
+// 32x32x16 bf16 MFMA, and the per-row reductions of the transposed
+// formulation, where lane l of a wave holds query row l % 32 in every
+// accumulator register and the two lanes l, l^32 share a row.
+#pragma once
+
+#include "common.h"
+
+namespace anima_hip {
+namespace flash_tile {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16;
+
+constexpr int kD = 128;               // head dim of these kernels
+constexpr int kBN = 64;               // keys per tile (== kVtTile)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kVmcnt0 = 0x0F70;       // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15)
+constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold: p <= 2^8
+static_assert(kBN == kVtTile, "V^T padding must match the key tile");
+
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane i
+// of the wave writes bytes [16i, 16i + 16) of the wave-uniform 1 KiB LDS
+// window `lds` (through M0); no VGPRs hold the data.  Completion is counted
+// by vmcnt and waited for explicitly (wait_vmcnt).  Issued from inline asm so
+// that the compiler, which cannot tell ring stages apart, does not put a
+// vmcnt(0) in front of every LDS read of another stage.
+// M0 is declared clobbered; nothing else in these kernels keeps a value in
+// M0 (checked in the generated assembly), so the reserved-register warning
+// does not apply.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const u16 *src, u16 *lds)
+{
+    const unsigned m0 = static_cast<unsigned>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)lds));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(m0), "v"(src)
+                 : "memory", "m0");
+}
+// The same copy addressed as a wave-uniform 64-bit base (SGPRs) plus this
+// lane's 32-bit byte offset, so no per-lane 64-bit address arithmetic runs.
+__device__ __forceinline__ void dma16s(const void *base, unsigned voff, u16 *lds)
+{
+    const unsigned m0 = static_cast<unsigned>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)lds));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(m0), "v"(voff), "s"(base)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 16, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+// Workgroup barrier for the LDS rings: this wave's LDS reads are complete
+// (lgkmcnt(0)), copies still in flight stay in flight (no vmcnt wait, unlike
+// __syncthreads), and the compiler moves no memory access across it.
+__device__ __forceinline__ void ring_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Max of v over the two lanes l and l^32 (the two halves of a query row) with
+// one v_permlane32_swap: r[0] holds the low half in both halves, r[1] the
+// high half.
+__device__ __forceinline__ float row_pair_max(float v)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Key (within a 32-key block) of accumulator register r of a lane in half h
+// (lanes 32h .. 32h+31) of a 32x32 MFMA result.
+__device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// Adds the 8 bf16 values of a P operand to the running sum acc, in f32
+// (v_dot2_f32_bf16 with a vector of ones).
+__device__ __forceinline__ float row_sum8(const bf16x8 &p, float acc)
+{
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 8; i += 2)
+        acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{p[i], p[i + 1]}, one, acc, false);
+    return acc;
+}
+
+// Accumulator registers base .. base+7 as one bf16 MFMA operand (round to
+// nearest even, v_cvt_pk_bf16_f32).
+__device__ __forceinline__ bf16x8 pack8(const f32x16 &s, int base)
+{
+    bf16x8 r;
+    const bf16x2 p0 = __builtin_convertvector(f32x2{s[base + 0], s[base + 1]}, bf16x2);
+    const bf16x2 p1 = __builtin_convertvector(f32x2{s[base + 2], s[base + 3]}, bf16x2);
+    const bf16x2 p2 = __builtin_convertvector(f32x2{s[base + 4], s[base + 5]}, bf16x2);
+    const bf16x2 p3 = __builtin_convertvector(f32x2{s[base + 6], s[base + 7]}, bf16x2);
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+inline bool aligned(const void *ptr, unsigned m)
+{
+    return (reinterpret_cast<uintptr_t>(ptr) & (m - 1)) == 0;
+}
+
+}  // namespace flash_tile
+}  // namespace anima_hip

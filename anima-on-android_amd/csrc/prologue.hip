@@ -12,6 +12,8 @@
 //       out[p + D/2] = f10*y[p] + f11*y[p+D/2]   (two products, one add);
 //   * the RMSNorm -> RoPE -> transpose sequence of NumpyAttention.forward
 //     (numpy_dit.py:285-291) in one pass over HBM.
+// Output as f32, as bf16, or as two bf16 terms hi = bf16(y), lo = bf16(y - hi)
+// (rows lo_off elements apart) for the f32-accurate bf16-MFMA attention.
 //
 // Bit-exactness: one thread owns each row's sum of squares and adds the
 // squares in index order; floating-point contraction is switched off for this
@@ -33,6 +35,7 @@ struct RowArgs {
     const float *freqs;
     int64_t xb, xh, xs, ob, oh, os;
     int64_t rows;      // B*S*H
+    int64_t lo_off;    // bf16 output: offset of the lo-term row, or 0
     int S, H, D, rows_per_block;
     float eps;
     int norm, out_bf16;
@@ -43,6 +46,26 @@ __device__ __forceinline__ unsigned short f32_to_bf16_rne(float f)
     unsigned int u = __float_as_uint(f);
     u += 0x7FFFu + ((u >> 16) & 1u);
     return (unsigned short)(u >> 16);
+}
+
+// Second bf16 term of f: bf16(f - hi), hi = bf16(f) (f - hi is exact in f32).
+__device__ __forceinline__ unsigned short bf16_lo_term(float f, unsigned short hi)
+{
+    return f32_to_bf16_rne(f - __uint_as_float(unsigned(hi) << 16));
+}
+
+// Four consecutive outputs as bf16 hi terms at ob and, when lo_off != 0, lo
+// terms at ob + lo_off.
+__device__ __forceinline__ void store_bf16x4(unsigned short *ob, int64_t lo_off, float v0,
+                                             float v1, float v2, float v3)
+{
+    const unsigned short h0 = f32_to_bf16_rne(v0), h1 = f32_to_bf16_rne(v1),
+                         h2 = f32_to_bf16_rne(v2), h3 = f32_to_bf16_rne(v3);
+    *reinterpret_cast<uint2 *>(ob) = uint2{h0 | (unsigned(h1) << 16), h2 | (unsigned(h3) << 16)};
+    if (lo_off)
+        *reinterpret_cast<uint2 *>(ob + lo_off) =
+            uint2{bf16_lo_term(v0, h0) | (unsigned(bf16_lo_term(v1, h1)) << 16),
+                  bf16_lo_term(v2, h2) | (unsigned(bf16_lo_term(v3, h3)) << 16)};
 }
 
 // Row r (linear over (b, s, h) in that order) -> element offsets.
@@ -141,9 +164,13 @@ __global__ __launch_bounds__(256) void rows_kernel(RowArgs a)
         const int rr = e / D, d = e - rr * D;
         const float v = out_elem(a, xs + rr * pitch, inv[rr], spos[rr], d);
         const int64_t oo = offs[2 * rr + 1] + d;
-        if (a.out_bf16)
-            static_cast<unsigned short *>(a.out)[oo] = f32_to_bf16_rne(v);
-        else
+        if (a.out_bf16) {
+            unsigned short *ob = static_cast<unsigned short *>(a.out);
+            const unsigned short hi = f32_to_bf16_rne(v);
+            ob[oo] = hi;
+            if (a.lo_off)
+                ob[oo + a.lo_off] = bf16_lo_term(v, hi);
+        } else
             static_cast<float *>(a.out)[oo] = v;
     }
 }
@@ -241,12 +268,8 @@ __device__ __forceinline__ void rows_d128_block(const RowArgs &a, int64_t blk)
         const int64_t oo = ooff[rr] + p0;
         if (a.out_bf16) {
             unsigned short *ob = static_cast<unsigned short *>(a.out) + oo;
-            *reinterpret_cast<uint2 *>(ob) =
-                uint2{f32_to_bf16_rne(lo[0]) | (unsigned(f32_to_bf16_rne(lo[1])) << 16),
-                      f32_to_bf16_rne(lo[2]) | (unsigned(f32_to_bf16_rne(lo[3])) << 16)};
-            *reinterpret_cast<uint2 *>(ob + 64) =
-                uint2{f32_to_bf16_rne(hi[0]) | (unsigned(f32_to_bf16_rne(hi[1])) << 16),
-                      f32_to_bf16_rne(hi[2]) | (unsigned(f32_to_bf16_rne(hi[3])) << 16)};
+            store_bf16x4(ob, a.lo_off, lo[0], lo[1], lo[2], lo[3]);
+            store_bf16x4(ob + 64, a.lo_off, hi[0], hi[1], hi[2], hi[3]);
         } else {
             float *of = static_cast<float *>(a.out) + oo;
             *reinterpret_cast<f32x4 *>(of) = lo;
@@ -276,6 +299,7 @@ RowArgs row_args(const RowProblem &p)
     a.xb = p.xs.b; a.xh = p.xs.h; a.xs = p.xs.s;
     a.ob = p.os.b; a.oh = p.os.h; a.os = p.os.s;
     a.rows = int64_t(p.B) * p.S * p.H;
+    a.lo_off = p.out_bf16 ? p.lo_off : 0;
     a.S = p.S;
     a.H = p.H;
     a.D = p.D;
@@ -294,7 +318,8 @@ bool d128_eligible(const RowProblem &p)
     };
     const auto st4 = [](const Strides &x) { return x.b % 4 == 0 && x.h % 4 == 0 && x.s % 4 == 0; };
     return p.D == 128 && al(p.x, 16) && al(p.out, p.out_bf16 ? 8 : 16) && st4(p.xs) &&
-           st4(p.os) && (!p.w || al(p.w, 16)) && (!p.freqs || al(p.freqs, 16));
+           st4(p.os) && (!p.w || al(p.w, 16)) && (!p.freqs || al(p.freqs, 16)) &&
+           (!p.out_bf16 || p.lo_off % 4 == 0);
 }
 
 }  // namespace

@@ -34,8 +34,11 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "anima-on-android_amd"))
 
-PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6}  # MI355X dense MFMA peaks
-MODE = {"f32": 0, "bf16": 1}
+# MI355X dense MFMA peaks.  The f32x3 path issues three bf16 MFMA products per
+# algorithmic product, so its ceiling in algorithmic FLOP/s is a third of the
+# bf16 peak.
+PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6, "f32x3": 2516.6 / 3}
+MODE = {"f32": 0, "bf16": 1, "f32x3": 2}
 PREWARM_S = 2.0  # seconds of untimed steps before the warmup steps of each headline run
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "flash_traffic.json")
 WORKLOAD = "self-attention 4096x4096, B=2 H=16 D=128 (64x64 grid, RMSNorm+3D RoPE)"
@@ -51,9 +54,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--variant", choices=["f32", "bf16"], default="f32",
-                    help="headline arithmetic: f32 MFMA on f32 inputs, or bf16 inputs with f32 "
-                         "accumulation")
+    ap.add_argument("--variant", choices=["f32", "bf16", "f32x3"], default="f32",
+                    help="headline arithmetic: f32 MFMA on f32 inputs, bf16 inputs with f32 "
+                         "accumulation, or f32 inputs as bf16 term pairs on bf16 MFMA")
     ap.add_argument("--cpu-heads", type=int, default=8,
                     help="(batch, head) slices timed single-core for cpu_baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -122,23 +125,31 @@ def headline(c, variant, q, k, v, freqs, ones, steps, warmup):
     """Prologue + flash on the 4096-token workload; per-launch flash timing."""
     torch, lib, _lib = c.torch, c.lib, c._lib
     B, S, H, D = q.shape
-    bf16 = variant == "bf16"
-    qn = torch.empty(q.shape, dtype=torch.bfloat16 if bf16 else torch.float32, device=c.dev)
+    bf16, x3 = variant == "bf16", variant == "f32x3"
+    # f32x3: q/k as rows of [hi | lo] bf16 terms, V^T as hi rows then lo rows.
+    w = 2 if x3 else 1
+    qn = torch.empty((B, S, H, w * D), dtype=torch.float32 if variant == "f32" else torch.bfloat16,
+                     device=c.dev)
     kn = torch.empty_like(qn)
     o = torch.empty_like(q)
     sp = lib.anima_hip_vt_padded_len(S)
-    vt = torch.empty((B, H, D, sp), dtype=torch.bfloat16, device=c.dev) if bf16 else None
+    vt = torch.empty((B, H, w * D, sp), dtype=torch.bfloat16, device=c.dev) if bf16 or x3 else None
     bshd = _lib.strides([S * H * D, D, H * D])  # [B,S,H,D] viewed as [B,H,S,D]
+    terms = _lib.strides([S * H * w * D, w * D, H * w * D])
     scale = ct.c_float(1.0 / math.sqrt(D))
-    flags = 1 | (2 if bf16 else 0)  # RMSNorm (+ bf16 output)
+    flags = 1 | (2 if bf16 else 4 if x3 else 0)  # RMSNorm (+ bf16 output or term rows)
 
     def prologue(x, y):
         _lib.check(lib.anima_hip_qk_prologue_dev(x.data_ptr(), y.data_ptr(), ones.data_ptr(),
-                                                 freqs.data_ptr(), B, S, H, D, bshd, bshd,
+                                                 freqs.data_ptr(), B, S, H, D, bshd, terms,
                                                  ct.c_float(1e-6), flags, c.stp), "qk_prologue")
 
     def flash():
-        if bf16:
+        if x3:
+            ok = lib.anima_hip_flash_x3_dev(qn.data_ptr(), kn.data_ptr(), vt.data_ptr(),
+                                            o.data_ptr(), B, H, S, S, D, terms, terms, None,
+                                            bshd, scale, False, c.stp)
+        elif bf16:
             ok = lib.anima_hip_flash_bf16_dev(qn.data_ptr(), kn.data_ptr(), vt.data_ptr(),
                                               o.data_ptr(), B, H, S, S, D, bshd, bshd, None,
                                               bshd, scale, False, c.stp)
@@ -154,6 +165,9 @@ def headline(c, variant, q, k, v, freqs, ones, steps, warmup):
         if bf16:
             _lib.check(lib.anima_hip_pack_vt_dev(v.data_ptr(), vt.data_ptr(), B, H, S, D, bshd,
                                                  None, c.stp), "pack_vt")
+        elif x3:
+            _lib.check(lib.anima_hip_pack_vt_terms_dev(v.data_ptr(), vt.data_ptr(), B, H, S, D,
+                                                       bshd, None, c.stp), "pack_vt_terms")
         if ev is not None:
             ev[0].record(c.st)
         flash()

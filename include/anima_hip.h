@@ -113,13 +113,18 @@ int anima_hip_version(void);
 
 /* Attention arithmetic modes. */
 enum {
-    ANIMA_HIP_F32 = 0,  /* f32 inputs, f32 MFMA, f32 accumulate            */
-    ANIMA_HIP_BF16 = 1  /* bf16 Q/K/V and P, f32 MFMA accumulate + softmax */
+    ANIMA_HIP_F32 = 0,   /* f32 inputs, f32 MFMA, f32 accumulate            */
+    ANIMA_HIP_BF16 = 1,  /* bf16 Q/K/V and P, f32 MFMA accumulate + softmax */
+    ANIMA_HIP_F32X3 = 2  /* f32 inputs on bf16 MFMA: each operand as two bf16
+                          * terms x = xh + xl (+ <= 2^-17 |x|), each product
+                          * as xh*yh + xh*yl + xl*yh, f32 accumulate and
+                          * softmax (D == 128)                               */
 };
 
 /* anima_rt_run_sdpa_flash with an arithmetic mode: host pointers, same
  * layouts and semantics; mode ANIMA_HIP_F32 is identical to the drop-in,
- * ANIMA_HIP_BF16 rounds Q, K, V (and P) to bf16 for the MFMAs (D == 128). */
+ * ANIMA_HIP_BF16 rounds Q, K, V (and P) to bf16 for the MFMAs, ANIMA_HIP_F32X3
+ * takes them as bf16 term pairs (both D == 128). */
 bool anima_hip_sdpa(const float *Q, const float *K, const float *V, float *out, int BH, int S_q,
                     int S_kv, int D, float scale, bool is_causal, int mode);
 
@@ -153,10 +158,34 @@ int64_t anima_hip_vt_padded_len(int S_kv);
 bool anima_hip_pack_vt_dev(const float *v, uint16_t *vt, int B, int H, int S_kv, int D,
                            const int64_t *v_strides, const int64_t *vt_strides, void *stream);
 
+/* Flash attention on device bf16 term tensors (mode ANIMA_HIP_F32X3): q, k
+ * hold rows of 2*D bf16, [hi | lo] with hi = bf16(x) and lo = bf16(x - hi)
+ * (anima_hip_qk_prologue_dev with flags & 4), the strides giving the row
+ * starts (NULL: [B,H,S,2D] contiguous); vt is V packed by
+ * anima_hip_pack_vt_terms_dev; o is f32.  D must be 128 and scale > 0.  Each
+ * product runs as three bf16 MFMA products (hi*hi + hi*lo + lo*hi) with f32
+ * accumulation; scores and softmax are f32, and P enters as two terms too. */
+bool anima_hip_flash_x3_dev(const uint16_t *q, const uint16_t *k, const uint16_t *vt,
+                            float *o, int B, int H, int S_q, int S_kv, int D,
+                            const int64_t *q_strides, const int64_t *k_strides,
+                            const int64_t *vt_strides, const int64_t *o_strides,
+                            float scale, bool is_causal, void *stream);
+
+/* Pack f32 V into the term V^T layout of anima_hip_flash_x3_dev: per (batch,
+ * head) the [D][anima_hip_vt_padded_len(S_kv)] hi matrix of
+ * anima_hip_pack_vt_dev's layout followed by the same matrix of lo terms
+ * bf16(v - bf16(v)).  vt_strides = {batch, head, d-row}; NULL = contiguous. */
+bool anima_hip_pack_vt_terms_dev(const float *v, uint16_t *vt, int B, int H, int S_kv, int D,
+                                 const int64_t *v_strides, const int64_t *vt_strides,
+                                 void *stream);
+
 /* Fused per-row prologue on device memory: for each row (b, s, h) of x,
  * optional RMSNorm (flags & 1; weight w may be NULL) followed by optional
  * rotate-half RoPE (freqs [S, D/2, 2, 2] or NULL), written through
- * out_strides as f32 or, with flags & 2, bf16 (round to nearest even).
+ * out_strides as f32 or, with flags & 2, bf16 (round to nearest even), or,
+ * with flags & 4, as bf16 terms: hi = bf16(y) at the row, lo = bf16(y - hi) D
+ * elements after it (rows of [hi | lo], the q/k input of
+ * anima_hip_flash_x3_dev).
  * This is NumpyAttention.forward's q/k path (anima_rt/scripts/numpy_dit.py:285-291):
  * RMSNorm (numpy_dit.py:285-286) -> RoPE (:288-289) -> transpose (:291). */
 bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const float *freqs,
