@@ -355,8 +355,30 @@ struct anima_hip_ctx_kv {
     int Bc = 0, S_kv = 0, H = 0, D = 0;
     int device = 0;
     void *k = nullptr;  // prepared K (layout per mode, see AttnInputs)
-    void *v = nullptr;  // prepared V (f32 rows or packed bf16 V^T)
+    void *v = nullptr;  // prepared V (f32 rows or packed bf16 / term V^T)
 };
+
+namespace {
+
+// The attention arithmetic of a public mode value; false with the reason for
+// an unknown mode, or a head dim other than 128 in the bf16 / f32x3 modes.
+bool attn_mode_of(int mode, int D, const char *who, AttnMode &out)
+{
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16 && mode != ANIMA_HIP_F32X3)
+        return fail(std::string(who) + ": unknown mode " + std::to_string(mode));
+    if (mode != ANIMA_HIP_F32 && D != 128)
+        return fail(std::string(who) + ": the bf16 and f32x3 modes need D == 128");
+    out = AttnMode(mode);
+    return true;
+}
+
+// Mode of a size query (unknown modes size as f32; the call itself rejects them).
+AttnMode size_mode(int mode)
+{
+    return mode == ANIMA_HIP_BF16 || mode == ANIMA_HIP_F32X3 ? AttnMode(mode) : kAttnF32;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -768,11 +790,12 @@ bool anima_hip_linear_dev(const float *a, int64_t lda, const uint16_t *w, int64_
 {
     if (!ready_for_device_call())
         return false;
-    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16)
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16 && mode != ANIMA_HIP_F32X3)
         return fail("linear_dev: unknown mode " + std::to_string(mode));
     if (int64_t(M) * N > 0 && (!c || (K > 0 && (!a || !w))))
         return fail("linear_dev: null pointer");
-    return launch_linear(a, lda, w, ldw, c, ldc, M, N, K, mode == ANIMA_HIP_F32, scratch,
+    // The f32x3 mode's projections are the f32 mode's (exact hi + lo terms).
+    return launch_linear(a, lda, w, ldw, c, ldc, M, N, K, mode != ANIMA_HIP_BF16, scratch,
                          scratch_bytes, pick_stream(stream));
 }
 
@@ -781,7 +804,7 @@ size_t anima_hip_attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H
 {
     if (B < 0 || S_q < 0 || Bk < 0 || S_kv < 0 || H < 0 || D < 0)
         return 0;
-    return attention_scratch_bytes(B, S_q, Bk, S_kv, H, D, mode == ANIMA_HIP_BF16, false);
+    return attention_scratch_bytes(B, S_q, Bk, S_kv, H, D, size_mode(mode), false);
 }
 
 bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
@@ -791,14 +814,14 @@ bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
 {
     if (!ready_for_device_call() || !check_dims(B, H, S_q, S_kv, D))
         return false;
-    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16)
-        return fail("attention_dev: unknown mode " + std::to_string(mode));
+    AttnMode am;
+    if (!attn_mode_of(mode, D, "attention_dev", am))
+        return false;
     if (int64_t(B) * S_q * H * D == 0)
         return true;
-    const bool bf16 = mode == ANIMA_HIP_BF16;
     if (!q || !out || !scratch || (S_kv > 0 && (!k || !v)))
         return fail("attention_dev: null pointer");
-    if (scratch_bytes < attention_scratch_bytes(B, S_q, Bk, S_kv, H, D, bf16, false))
+    if (scratch_bytes < attention_scratch_bytes(B, S_q, Bk, S_kv, H, D, am, false))
         return fail("attention_dev: scratch smaller than anima_hip_attention_scratch_bytes()");
     AttnInputs in;
     in.q = q;
@@ -815,7 +838,7 @@ bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
     in.H = H;
     in.D = D;
     in.eps = eps;
-    in.bf16 = bf16;
+    in.mode = am;
     return run_attention(in, scratch, pick_stream(stream));
 }
 
@@ -827,11 +850,9 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
     std::lock_guard<std::recursive_mutex> g(r.mu);
     if (!ensure_ready(r) || !check_dims(B, H, S_q, S_kv, D))
         return false;
-    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16)
-        return fail("anima_hip_attention: unknown mode " + std::to_string(mode));
-    const bool bf16 = mode == ANIMA_HIP_BF16;
-    if (bf16 && D != 128)
-        return fail("anima_hip_attention: the bf16 mode needs D == 128");
+    AttnMode am;
+    if (!attn_mode_of(mode, D, "anima_hip_attention", am))
+        return false;
     if (freqs && S_q != S_kv)
         return fail("anima_hip_attention: RoPE needs S_q == S_kv (self-attention)");
     const int64_t nq = int64_t(B) * S_q * H * D, nk = int64_t(B) * S_kv * H * D;
@@ -841,7 +862,7 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
         return fail("anima_hip_attention: null pointer");
     const hipStream_t st = r.stream;
     begin_call(r);
-    const size_t scratch = attention_scratch_bytes(B, S_q, B, S_kv, H, D, bf16, false);
+    const size_t scratch = attention_scratch_bytes(B, S_q, B, S_kv, H, D, am, false);
     if (!r.q.reserve(f32_bytes(nq), "workspace q") || !r.k.reserve(f32_bytes(nk), "workspace k") ||
         !r.v.reserve(f32_bytes(nk), "workspace v") || !r.o.reserve(f32_bytes(nq), "workspace o") ||
         !r.scratch.reserve(scratch, "workspace scratch"))
@@ -864,7 +885,7 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
     in.H = H;
     in.D = D;
     in.eps = eps;
-    in.bf16 = bf16;
+    in.mode = am;
     if (!run_attention(in, r.scratch.p, st) || !d2h(out, r.o.p, f32_bytes(nq), st))
         return false;
     return finish_call(r);
@@ -882,15 +903,10 @@ anima_hip_ctx_kv *anima_hip_ctx_kv_create(const float *ctx, const uint16_t *wk, 
         fail("ctx_kv_create: all dimensions must be positive");
         return nullptr;
     }
-    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16) {
-        fail("ctx_kv_create: unknown mode " + std::to_string(mode));
+    AttnMode am;
+    if (!attn_mode_of(mode, D, "ctx_kv_create", am))
         return nullptr;
-    }
-    const bool bf16 = mode == ANIMA_HIP_BF16;
-    if (bf16 && D != 128) {
-        fail("ctx_kv_create: the bf16 mode needs D == 128");
-        return nullptr;
-    }
+    const bool bf16 = am == kAttnBF16;
     if (!ctx || !wk || !wv) {
         fail("ctx_kv_create: null pointer");
         return nullptr;
@@ -920,7 +936,8 @@ anima_hip_ctx_kv *anima_hip_ctx_kv_create(const float *ctx, const uint16_t *wk, 
     kv->D = D;
     kv->device = r.device;
     // K/V projections of the context on bf16 MFMA: the context enters as
-    // exact hi + lo bf16 terms in f32 mode, rounded to bf16 in bf16 mode.
+    // exact hi + lo bf16 terms in the f32 and f32x3 modes, rounded to bf16 in
+    // bf16 mode.
     const size_t sb = linear_scratch_bytes(M, C, !bf16);
     bool ok = r.scratch.reserve(sb, "workspace linear") &&
               launch_linear(static_cast<const float *>(r.q.p), C,
@@ -929,17 +946,17 @@ anima_hip_ctx_kv *anima_hip_ctx_kv_create(const float *ctx, const uint16_t *wk, 
               launch_linear(static_cast<const float *>(r.q.p), C,
                             static_cast<const uint16_t *>(r.v.p), C, static_cast<float *>(vf.p),
                             N, M, N, C, !bf16, r.scratch.p, sb, st);
-    if (ok && bf16) {
-        ok = hip_ok(hipMalloc(&kv->k, prepared_k_bytes(Bc, S_kv, H, D, true)), "ctx K cache") &&
-             hip_ok(hipMalloc(&kv->v, prepared_v_bytes(Bc, S_kv, H, D, true)), "ctx V cache") &&
+    if (ok && am != kAttnF32) {
+        ok = hip_ok(hipMalloc(&kv->k, prepared_k_bytes(Bc, S_kv, H, D, am)), "ctx K cache") &&
+             hip_ok(hipMalloc(&kv->v, prepared_v_bytes(Bc, S_kv, H, D, am)), "ctx V cache") &&
              prepare_kv(static_cast<const float *>(kf.p), static_cast<const float *>(vf.p), kw,
-                        nullptr, kv->k, kv->v, Bc, S_kv, H, D, eps, true, st) &&
+                        nullptr, kv->k, kv->v, Bc, S_kv, H, D, eps, am, st) &&
              sync(st);
     } else if (ok) {
         // f32: normalise K in place (each row is staged in LDS before it is
         // rewritten); the two projections become the cache.
         ok = prepare_kv(static_cast<const float *>(kf.p), nullptr, kw, nullptr, kf.p, nullptr, Bc,
-                        S_kv, H, D, eps, false, st) &&
+                        S_kv, H, D, eps, kAttnF32, st) &&
              sync(st);
         if (ok) {
             kv->k = kf.p;
@@ -981,8 +998,8 @@ size_t anima_hip_attention_block_scratch_bytes(const anima_hip_ctx_kv *kv, int B
         return 0;
     if (kv)
         return attention_block_scratch_bytes(B, S, Dm, kv->H, kv->D, kv->Bc, kv->S_kv,
-                                             kv->mode == ANIMA_HIP_BF16, true);
-    return attention_block_scratch_bytes(B, S, Dm, H, D, B, S, mode == ANIMA_HIP_BF16, false);
+                                             AttnMode(kv->mode), true);
+    return attention_block_scratch_bytes(B, S, Dm, H, D, B, S, size_mode(mode), false);
 }
 
 bool anima_hip_attention_block_dev(float *x, const float *mod, const uint16_t *wq,
@@ -996,8 +1013,9 @@ bool anima_hip_attention_block_dev(float *x, const float *mod, const uint16_t *w
         return false;
     if (!check_dims(B, H, S, S, D) || Dm < 0)
         return fail("attention_block_dev: negative dimension");
-    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16)
-        return fail("attention_block_dev: unknown mode " + std::to_string(mode));
+    AttnMode am;
+    if (!attn_mode_of(mode, D, "attention_block_dev", am))
+        return false;
     BlockProblem p;
     p.x = x;
     p.mod = mod;
@@ -1014,7 +1032,7 @@ bool anima_hip_attention_block_dev(float *x, const float *mod, const uint16_t *w
     p.H = H;
     p.D = D;
     p.eps = eps;
-    p.bf16 = mode == ANIMA_HIP_BF16;
+    p.mode = am;
     if (kv) {
         int dev = 0;
         if (!hip_ok(hipGetDevice(&dev), "hipGetDevice"))
@@ -1039,8 +1057,8 @@ size_t anima_hip_cross_attention_scratch_bytes(const anima_hip_ctx_kv *kv, int B
 {
     if (!kv || B < 0 || S_q < 0)
         return 0;
-    return attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D,
-                                   kv->mode == ANIMA_HIP_BF16, true);
+    return attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D, AttnMode(kv->mode),
+                                   true);
 }
 
 bool anima_hip_cross_attention_dev(const float *q, const float *q_norm_w,
@@ -1057,8 +1075,8 @@ bool anima_hip_cross_attention_dev(const float *q, const float *q_norm_w,
         return true;
     if (!q || !out || !scratch)
         return fail("cross_attention_dev: null pointer");
-    const bool bf16 = kv->mode == ANIMA_HIP_BF16;
-    if (scratch_bytes < attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D, bf16, true))
+    const AttnMode am = AttnMode(kv->mode);
+    if (scratch_bytes < attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D, am, true))
         return fail("cross_attention_dev: scratch smaller than "
                     "anima_hip_cross_attention_scratch_bytes()");
     AttnInputs in;
@@ -1074,7 +1092,7 @@ bool anima_hip_cross_attention_dev(const float *q, const float *q_norm_w,
     in.H = kv->H;
     in.D = kv->D;
     in.eps = eps;
-    in.bf16 = bf16;
+    in.mode = am;
     return run_attention(in, scratch, pick_stream(stream));
 }
 
@@ -1096,9 +1114,8 @@ bool anima_hip_cross_attention(const float *q, const float *q_norm_w, const anim
         return fail("cross_attention: null pointer");
     const hipStream_t st = r.stream;
     begin_call(r);
-    const bool bf16 = kv->mode == ANIMA_HIP_BF16;
-    const size_t scratch =
-        attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D, bf16, true);
+    const size_t scratch = attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D,
+                                                   AttnMode(kv->mode), true);
     const float *qw = nullptr;
     if (!r.q.reserve(f32_bytes(nq), "workspace q") || !r.o.reserve(f32_bytes(nq), "workspace o") ||
         !r.scratch.reserve(scratch, "workspace scratch") || !h2d(r.q.p, q, f32_bytes(nq), st) ||

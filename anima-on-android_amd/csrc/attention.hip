@@ -26,67 +26,89 @@ Strides bshd(int S, int H, int D, bool broadcast, int64_t ld = 0)
     const int64_t row = ld > 0 ? ld : int64_t(H) * D;
     return Strides{broadcast ? 0 : int64_t(S) * row, int64_t(D), row};
 }
+
+// Q/K rows of the attention kernels of `mode` in [B, S, H, D] order: f32 or
+// bf16 rows of D, or [hi | lo] term rows of 2D (f32x3).
+Strides bshd_mode(int S, int H, int D, bool broadcast, AttnMode mode)
+{
+    return mode == kAttnF32X3 ? bshd(S, H, 2 * D, broadcast) : bshd(S, H, D, broadcast);
+}
+
+// Packed V^T strides {batch, head, d-row} of the bf16 / f32x3 layouts.
+Strides vt_strides(int S_kv, int H, int D, bool broadcast, AttnMode mode)
+{
+    const int64_t sp = vt_padded_len(S_kv), rows = mode == kAttnF32X3 ? 2 * int64_t(D) : D;
+    return Strides{broadcast ? 0 : int64_t(H) * rows * sp, rows * sp, sp};
+}
+
+// Bytes per Q/K element in the layout of `mode`: f32, one bf16, or two bf16 terms.
+size_t qk_elem_bytes(AttnMode mode) { return mode == kAttnBF16 ? 2 : 4; }
 }  // namespace
 
-size_t prepared_k_bytes(int Bk, int S_kv, int H, int D, bool bf16)
+size_t prepared_k_bytes(int Bk, int S_kv, int H, int D, AttnMode mode)
 {
-    return size_t(Bk) * S_kv * H * D * (bf16 ? 2 : 4);
+    return size_t(Bk) * S_kv * H * D * qk_elem_bytes(mode);
 }
 
-size_t prepared_v_bytes(int Bk, int S_kv, int H, int D, bool bf16)
+size_t prepared_v_bytes(int Bk, int S_kv, int H, int D, AttnMode mode)
 {
-    return bf16 ? size_t(Bk) * H * D * vt_padded_len(S_kv) * 2 : size_t(Bk) * S_kv * H * D * 4;
+    if (mode == kAttnF32)
+        return size_t(Bk) * S_kv * H * D * 4;
+    return size_t(Bk) * H * D * vt_padded_len(S_kv) * (mode == kAttnF32X3 ? 4 : 2);
 }
 
-size_t attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D, bool bf16,
+size_t attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D, AttnMode mode,
                                bool kv_prepared)
 {
-    size_t n = round_up(size_t(B) * S_q * H * D * (bf16 ? 2 : 4));
+    size_t n = round_up(size_t(B) * S_q * H * D * qk_elem_bytes(mode));
     if (!kv_prepared) {
-        n += round_up(prepared_k_bytes(Bk, S_kv, H, D, bf16));
-        if (bf16)
-            n += round_up(prepared_v_bytes(Bk, S_kv, H, D, true));
+        n += round_up(prepared_k_bytes(Bk, S_kv, H, D, mode));
+        if (mode != kAttnF32)
+            n += round_up(prepared_v_bytes(Bk, S_kv, H, D, mode));
     }
     return n + round_up(flash_plan(int64_t(B) * H, S_q, S_kv, D).bytes);
 }
 
 namespace {
 
-// The K row problem of prepare_kv: RMSNorm (+ RoPE) of [Bk, S_kv, H, D] K.
-RowProblem k_rows(const float *k, const float *k_norm_w, const float *freqs, void *k_out, int Bk,
-                  int S_kv, int H, int D, float eps, bool bf16, int64_t ld = 0)
+// The Q or K row problem: RMSNorm (+ RoPE) of [B, S, H, D] rows ld apart,
+// written in the Q/K layout of `mode`.
+RowProblem qk_rows(const float *x, const float *norm_w, const float *freqs, void *out, int B,
+                   int S, int H, int D, float eps, AttnMode mode, int64_t ld = 0)
 {
-    RowProblem pk;
-    pk.x = k;
-    pk.out = k_out;
-    pk.w = k_norm_w;
-    pk.freqs = freqs;
-    pk.xs = bshd(S_kv, H, D, false, ld);
-    pk.os = bshd(S_kv, H, D, false);
-    pk.B = Bk;
-    pk.S = S_kv;
-    pk.H = H;
-    pk.D = D;
-    pk.eps = eps;
-    pk.norm = true;
-    pk.out_bf16 = bf16;
-    return pk;
+    RowProblem p;
+    p.x = x;
+    p.out = out;
+    p.w = norm_w;
+    p.freqs = freqs;
+    p.xs = bshd(S, H, D, false, ld);
+    p.os = bshd_mode(S, H, D, false, mode);
+    p.B = B;
+    p.S = S;
+    p.H = H;
+    p.D = D;
+    p.eps = eps;
+    p.norm = true;
+    p.out_bf16 = mode != kAttnF32;
+    p.lo_off = mode == kAttnF32X3 ? D : 0;
+    return p;
 }
 
-// V's part of prepare_kv: packed bf16 V^T, or a copy (f32) unless in place.
-bool prepare_v(const float *v, void *v_out, int Bk, int S_kv, int H, int D, bool bf16,
+// V's part of prepare_kv: packed (term) V^T, or a copy (f32) unless in place.
+bool prepare_v(const float *v, void *v_out, int Bk, int S_kv, int H, int D, AttnMode mode,
                hipStream_t st, int64_t ld = 0)
 {
-    if (bf16) {
-        const int64_t sp = vt_padded_len(S_kv);
-        const Strides vts{int64_t(H) * D * sp, int64_t(D) * sp, sp};
-        return launch_vt_pack(v, bshd(S_kv, H, D, false, ld), static_cast<uint16_t *>(v_out), vts, Bk,
-                              H, S_kv, D, st);
+    if (mode != kAttnF32) {
+        const Strides vs = bshd(S_kv, H, D, false, ld);
+        const Strides vts = vt_strides(S_kv, H, D, false, mode);
+        uint16_t *vt = static_cast<uint16_t *>(v_out);
+        return mode == kAttnF32X3 ? launch_vt_pack_terms(v, vs, vt, vts, Bk, H, S_kv, D, st)
+                                  : launch_vt_pack(v, vs, vt, vts, Bk, H, S_kv, D, st);
     }
     if (v_out && v_out != v) {
         if (ld > 0 && ld != int64_t(H) * D)
             return fail("prepare_kv: a strided V cannot be copied into a dense cache");
-        return hip_ok(hipMemcpyAsync(v_out, v, prepared_v_bytes(Bk, S_kv, H, D, false),
+        return hip_ok(hipMemcpyAsync(v_out, v, prepared_v_bytes(Bk, S_kv, H, D, kAttnF32),
                                      hipMemcpyDeviceToDevice, st),
                       "V copy");
     }
@@ -96,63 +118,53 @@ bool prepare_v(const float *v, void *v_out, int Bk, int S_kv, int H, int D, bool
 }  // namespace
 
 bool prepare_kv(const float *k, const float *v, const float *k_norm_w, const float *freqs,
-                void *k_out, void *v_out, int Bk, int S_kv, int H, int D, float eps, bool bf16,
-                hipStream_t st)
+                void *k_out, void *v_out, int Bk, int S_kv, int H, int D, float eps,
+                AttnMode mode, hipStream_t st)
 {
-    return launch_rows(k_rows(k, k_norm_w, freqs, k_out, Bk, S_kv, H, D, eps, bf16), st) &&
-           prepare_v(v, v_out, Bk, S_kv, H, D, bf16, st);
+    if (mode != kAttnF32 && D != 128)
+        return fail("prepare_kv: the bf16 and f32x3 modes need D == 128");
+    return launch_rows(qk_rows(k, k_norm_w, freqs, k_out, Bk, S_kv, H, D, eps, mode), st) &&
+           prepare_v(v, v_out, Bk, S_kv, H, D, mode, st);
 }
 
 bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
 {
     const int B = in.B, S_q = in.S_q, S_kv = in.S_kv, H = in.H, D = in.D;
+    const AttnMode mode = in.mode;
     if (int64_t(B) * S_q * H * D == 0)
         return true;
     if (in.Bk != B && in.Bk != 1)
         return fail("attention: K/V batch must be 1 (broadcast) or equal to the query batch");
-    if (in.bf16 && D != 128)
-        return fail("attention: the bf16 mode needs D == 128");
+    if (mode != kAttnF32 && D != 128)
+        return fail("attention: the bf16 and f32x3 modes need D == 128");
     if (in.freqs && S_q != S_kv)
         return fail("attention: RoPE needs S_q == S_kv (self-attention)");
     const bool prepared = in.k_prep != nullptr;
     char *cur = static_cast<char *>(scratch);
     void *qn = cur;
-    cur += round_up(size_t(B) * S_q * H * D * (in.bf16 ? 2 : 4));
+    cur += round_up(size_t(B) * S_q * H * D * qk_elem_bytes(mode));
 
     const void *kp = in.k_prep, *vp = in.v_prep;
     RowProblem pk{};
     if (!prepared) {
         void *kn = cur;
-        cur += round_up(prepared_k_bytes(in.Bk, S_kv, H, D, in.bf16));
-        void *vt = in.bf16 ? static_cast<void *>(cur) : nullptr;
-        pk = k_rows(in.k, in.k_norm_w, in.freqs, kn, in.Bk, S_kv, H, D, in.eps, in.bf16,
-                    in.ld_kv);
-        if (!prepare_v(in.v, vt, in.Bk, S_kv, H, D, in.bf16, st, in.ld_kv))
+        cur += round_up(prepared_k_bytes(in.Bk, S_kv, H, D, mode));
+        void *vt = mode != kAttnF32 ? static_cast<void *>(cur) : nullptr;
+        pk = qk_rows(in.k, in.k_norm_w, in.freqs, kn, in.Bk, S_kv, H, D, in.eps, mode, in.ld_kv);
+        if (!prepare_v(in.v, vt, in.Bk, S_kv, H, D, mode, st, in.ld_kv))
             return false;
         kp = kn;
-        vp = in.bf16 ? vt : static_cast<const void *>(in.v);
-        if (in.bf16)
-            cur += round_up(prepared_v_bytes(in.Bk, S_kv, H, D, true));
+        vp = mode != kAttnF32 ? vt : static_cast<const void *>(in.v);
+        if (mode != kAttnF32)
+            cur += round_up(prepared_v_bytes(in.Bk, S_kv, H, D, mode));
     }
     // Split-KV partials (small problems only).
     void *part = cur;
     const size_t part_bytes = flash_plan(int64_t(B) * H, S_q, S_kv, D).bytes;
 
-    RowProblem pq;
-    pq.x = in.q;
-    pq.out = qn;
-    pq.w = in.q_norm_w;
-    pq.freqs = in.freqs;
-    pq.xs = bshd(S_q, H, D, false, in.ld_q);
-    pq.os = bshd(S_q, H, D, false);
-    pq.B = B;
-    pq.S = S_q;
-    pq.H = H;
-    pq.D = D;
-    pq.eps = in.eps;
-    pq.norm = true;
-    pq.out_bf16 = in.bf16;
     // Q rows, and K rows unless prepared, in one launch.
+    const RowProblem pq =
+        qk_rows(in.q, in.q_norm_w, in.freqs, qn, B, S_q, H, D, in.eps, mode, in.ld_q);
     if (!(prepared ? launch_rows(pq, st) : launch_rows_pair(pk, pq, st)))
         return false;
 
@@ -162,14 +174,13 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     p.k = kp;
     p.v = vp;
     p.o = in.out;
-    p.qs = p.os = bshd(S_q, H, D, false);
-    p.ks = bshd(S_kv, H, D, bcast);
-    if (in.bf16) {
-        const int64_t sp = vt_padded_len(S_kv);
-        p.vs = Strides{bcast ? 0 : int64_t(H) * D * sp, int64_t(D) * sp, sp};
-    } else {
+    p.qs = bshd_mode(S_q, H, D, false, mode);
+    p.os = bshd(S_q, H, D, false);
+    p.ks = bshd_mode(S_kv, H, D, bcast, mode);
+    if (mode != kAttnF32)
+        p.vs = vt_strides(S_kv, H, D, bcast, mode);
+    else
         p.vs = prepared ? bshd(S_kv, H, D, bcast) : bshd(S_kv, H, D, bcast, in.ld_kv);
-    }
     p.B = B;
     p.H = H;
     p.S_q = S_q;
@@ -177,8 +188,14 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     p.D = D;
     p.scale = float(1.0 / std::sqrt(double(D)));
     p.causal = false;
-    return in.bf16 ? launch_flash_bf16(p, st, part, part_bytes)
-                   : launch_flash_f32(p, st, part, part_bytes);
+    switch (mode) {
+    case kAttnBF16:
+        return launch_flash_bf16(p, st, part, part_bytes);
+    case kAttnF32X3:
+        return launch_flash_x3(p, st, part, part_bytes);
+    default:
+        return launch_flash_f32(p, st, part, part_bytes);
+    }
 }
 
 }  // namespace anima_hip

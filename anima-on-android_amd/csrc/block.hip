@@ -163,9 +163,10 @@ struct BlockScratch {
     size_t terms, q, k, v, o, y, attn, lin, total;
 };
 
-BlockScratch block_scratch(int B, int S, int Dm, int H, int D, int Bk, int S_kv, bool bf16,
+BlockScratch block_scratch(int B, int S, int Dm, int H, int D, int Bk, int S_kv, AttnMode mode,
                            bool cross)
 {
+    const bool bf16 = mode == kAttnBF16;
     const size_t M = size_t(B) * S, HD = size_t(H) * D;
     BlockScratch s{};
     s.terms = round_up256(M * size_t(linear_terms_ld(Dm)) * 2) * (bf16 ? 1 : 2);
@@ -174,7 +175,7 @@ BlockScratch block_scratch(int B, int S, int Dm, int H, int D, int Bk, int S_kv,
     s.v = cross ? 0 : s.q;
     s.o = s.q;
     s.y = round_up256(M * size_t(Dm) * 4);
-    s.attn = round_up256(attention_scratch_bytes(B, S, Bk, S_kv, H, D, bf16, cross));
+    s.attn = round_up256(attention_scratch_bytes(B, S, Bk, S_kv, H, D, mode, cross));
     s.lin = round_up256(linear_scratch_bytes(int(M), int(HD), !bf16));
     s.total = s.terms + s.q + s.k + s.v + s.o + s.y + s.attn + s.lin;
     return s;
@@ -183,9 +184,9 @@ BlockScratch block_scratch(int B, int S, int Dm, int H, int D, int Bk, int S_kv,
 }  // namespace
 
 size_t attention_block_scratch_bytes(int B, int S, int Dm, int H, int D, int Bk, int S_kv,
-                                     bool bf16, bool cross)
+                                     AttnMode mode, bool cross)
 {
-    return block_scratch(B, S, Dm, H, D, Bk, S_kv, bf16, cross).total;
+    return block_scratch(B, S, Dm, H, D, Bk, S_kv, mode, cross).total;
 }
 
 bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t mod_ld,
@@ -265,6 +266,7 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
 {
     const int B = p.B, S = p.S, Dm = p.Dm, H = p.H, D = p.D;
     const bool cross = p.k_prep != nullptr;
+    const bool bf16 = p.mode == kAttnBF16;
     const int64_t M = int64_t(B) * S;
     const int HD = H * D;
     if (M == 0)
@@ -274,7 +276,7 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
     if (!p.x || !p.mod || !p.wq || !p.wo || (!cross && (!p.wk || !p.wv)))
         return fail("attention_block: null pointer");
     const BlockScratch s = block_scratch(B, S, Dm, H, D, cross ? p.Bk : B, cross ? p.S_kv : S,
-                                         p.bf16, cross);
+                                         p.mode, cross);
     if (!scratch || scratch_bytes < s.total || !aligned16(scratch))
         return fail("attention_block: scratch smaller than the size query or not 16-byte aligned");
     char *cur = static_cast<char *>(scratch);
@@ -284,7 +286,7 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
         return r;
     };
     uint16_t *hi = reinterpret_cast<uint16_t *>(take(s.terms));
-    uint16_t *lo = p.bf16 ? nullptr : hi + (s.terms / 2) / sizeof(uint16_t);
+    uint16_t *lo = bf16 ? nullptr : hi + (s.terms / 2) / sizeof(uint16_t);
     float *q = reinterpret_cast<float *>(take(s.q));
     float *k = reinterpret_cast<float *>(take(s.k));
     float *v = reinterpret_cast<float *>(take(s.v));
@@ -321,7 +323,7 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
     in.H = H;
     in.D = D;
     in.eps = p.eps;
-    in.bf16 = p.bf16;
+    in.mode = p.mode;
     if (!run_attention(in, attn, st))
         return false;
 
@@ -331,10 +333,10 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
     // read and write the residual again), or a shape the library GEMM does
     // not take with a per-channel scale: the projection into y, then a
     // residual pass.
-    if (p.bf16 && linear_residual_supported(S, Dm, HD, p.wo, HD, p.x, Dm))
+    if (bf16 && linear_residual_supported(S, Dm, HD, p.wo, HD, p.x, Dm))
         return launch_linear_residual(o, HD, p.wo, HD, p.x, Dm, p.mod + 2 * int64_t(Dm),
                                       3 * int64_t(Dm), B, S, Dm, HD, lin, s.lin, st);
-    if (!launch_linear(o, HD, p.wo, HD, y, Dm, int(M), Dm, HD, !p.bf16, lin, s.lin, st))
+    if (!launch_linear(o, HD, p.wo, HD, y, Dm, int(M), Dm, HD, !bf16, lin, s.lin, st))
         return false;
     return launch_gate_residual(p.x, y, p.mod, M, S, Dm, st);
 }

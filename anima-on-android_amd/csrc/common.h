@@ -185,8 +185,13 @@ bool launch_rows(const RowProblem &p, hipStream_t st);
 bool launch_rows_pair(const RowProblem &p1, const RowProblem &p2, hipStream_t st);
 
 // ---- Composite attention core (attention.hip) ----
+// Arithmetic of the attention kernels; the values of the public
+// ANIMA_HIP_F32 / ANIMA_HIP_BF16 / ANIMA_HIP_F32X3.
+enum AttnMode : int { kAttnF32 = 0, kAttnBF16 = 1, kAttnF32X3 = 2 };
 // Prepared K/V layouts: f32 mode K and V f32 [Bk, S_kv, H, D]; bf16 mode K
-// bf16 [Bk, S_kv, H, D] and V packed bf16 V^T [Bk, H, D, vt_padded_len(S_kv)].
+// bf16 [Bk, S_kv, H, D] and V packed bf16 V^T [Bk, H, D, vt_padded_len(S_kv)];
+// f32x3 mode K term rows [Bk, S_kv, H, 2D] ([hi | lo]) and V packed term V^T
+// [Bk, H, 2D, vt_padded_len(S_kv)].
 struct AttnInputs {
     const float *q = nullptr;         // [B, S_q, H, D] f32 projections
     const float *q_norm_w = nullptr;  // [D] or null
@@ -199,18 +204,18 @@ struct AttnInputs {
     float *out = nullptr;             // [B, S_q, H, D] f32
     int B = 0, Bk = 0, S_q = 0, S_kv = 0, H = 0, D = 0;
     float eps = 1e-6f;
-    bool bf16 = false;
+    AttnMode mode = kAttnF32;
     // Token-row strides (elements) of q and of the raw k/v: 0 means H*D
     // (dense); wider when they are column blocks of one fused projection.
     int64_t ld_q = 0, ld_kv = 0;
 };
-size_t prepared_k_bytes(int Bk, int S_kv, int H, int D, bool bf16);
-size_t prepared_v_bytes(int Bk, int S_kv, int H, int D, bool bf16);
-size_t attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D, bool bf16,
+size_t prepared_k_bytes(int Bk, int S_kv, int H, int D, AttnMode mode);
+size_t prepared_v_bytes(int Bk, int S_kv, int H, int D, AttnMode mode);
+size_t attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D, AttnMode mode,
                                bool kv_prepared);
 bool prepare_kv(const float *k, const float *v, const float *k_norm_w, const float *freqs,
-                void *k_out, void *v_out, int Bk, int S_kv, int H, int D, float eps, bool bf16,
-                hipStream_t st);
+                void *k_out, void *v_out, int Bk, int S_kv, int H, int D, float eps,
+                AttnMode mode, hipStream_t st);
 bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st);
 
 // ---- Attention sub-block of a DiT block on the resident residual stream
@@ -227,10 +232,12 @@ struct BlockProblem {
     int Bk = 0, S_kv = 0;
     int B = 0, S = 0, Dm = 0, H = 0, D = 0;
     float eps = 1e-6f;
-    bool bf16 = false;
+    // Attention arithmetic; the projections take exact hi + lo bf16 terms of
+    // their f32 activations unless the mode is bf16 (activations rounded).
+    AttnMode mode = kAttnF32;
 };
 size_t attention_block_scratch_bytes(int B, int S, int Dm, int H, int D, int Bk, int S_kv,
-                                     bool bf16, bool cross);
+                                     AttnMode mode, bool cross);
 bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_bytes, hipStream_t st);
 // LayerNorm (no affine) + AdaLN modulation of rows of x, written as the bf16
 // terms (hi, and lo unless null) of the projection GEMM's input.  Row r

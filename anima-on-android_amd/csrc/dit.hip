@@ -365,7 +365,8 @@ struct BlockWeights {
 
 struct anima_hip_dit {
     anima_hip_dit_config cfg{};
-    bool bf16 = false;
+    bool bf16 = false;          // activations of the linear layers rounded to bf16
+    AttnMode attn = kAttnF32;   // attention arithmetic
     int device = 0;
     std::vector<BlockWeights> blk;
     const uint16_t *x_emb = nullptr;  // [D][kp_in] zero-padded copy (owned)
@@ -458,10 +459,10 @@ SubLayout sub_layout(const anima_hip_dit *d, int B, int64_t S, int kind)
         l.a = round_up256(M * HD * 4 * (kind == 0 ? 3 : 1));
         l.b = round_up256(M * HD * 4);
         l.attn = round_up256(kind == 0 ? attention_scratch_bytes(B, int(S), B, int(S), c.heads,
-                                                                 c.head_dim, d->bf16, false)
+                                                                 c.head_dim, d->attn, false)
                                        : attention_scratch_bytes(B, int(S), std::max(d->ctx_B, 1),
                                                                  std::max(d->ctx_S, 1), c.heads,
-                                                                 c.head_dim, d->bf16, true));
+                                                                 c.head_dim, d->attn, true));
         l.lin = round_up256(M * size_t(linear_terms_ld(int(HD))) * 2 * d->reps);
     }
     l.total = l.terms + l.a + l.b + l.attn + l.lin;
@@ -577,7 +578,7 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
     in.H = c.heads;
     in.D = c.head_dim;
     in.eps = 1e-6f;
-    in.bf16 = d->bf16;
+    in.mode = d->attn;
     in.out = o;
     if (kind == 0) {
         if (!launch_linear_terms(terms, nullptr, bw.w_qkv, d->ld_d, proj, 3 * HD, int(M), 3 * HD,
@@ -751,8 +752,12 @@ anima_hip_dit *anima_hip_dit_create(const anima_hip_dit_config *cfg, const char 
     }
     if (!check_cfg(*cfg))
         return nullptr;
-    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16) {
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_BF16 && mode != ANIMA_HIP_F32X3) {
         fail("dit_create: unknown mode " + std::to_string(mode));
+        return nullptr;
+    }
+    if (mode != ANIMA_HIP_F32 && cfg->head_dim != 128) {
+        fail("dit_create: the bf16 and f32x3 modes need head_dim 128");
         return nullptr;
     }
     if (n < 0 || (n > 0 && (!names || !ptrs || !dtypes || !shapes))) {
@@ -764,6 +769,7 @@ anima_hip_dit *anima_hip_dit_create(const anima_hip_dit_config *cfg, const char 
     auto *d = new anima_hip_dit;
     d->cfg = *cfg;
     d->bf16 = mode == ANIMA_HIP_BF16;
+    d->attn = AttnMode(mode);
     (void)hipGetDevice(&d->device);
     const anima_hip_dit_config &c = d->cfg;
     const int D = c.dim, HD = c.heads * c.head_dim;
@@ -1010,9 +1016,9 @@ bool anima_hip_dit_set_context_dev(anima_hip_dit *d, const float *ctx, int Bc, i
         }
         d->alloc_B = d->alloc_S = 0;
         for (auto &b : d->blk) {
-            if (!hip_ok(hipMalloc(&b.ctx_k, prepared_k_bytes(Bc, S_kv, H, hd, d->bf16)),
+            if (!hip_ok(hipMalloc(&b.ctx_k, prepared_k_bytes(Bc, S_kv, H, hd, d->attn)),
                         "dit context K cache") ||
-                !hip_ok(hipMalloc(&b.ctx_v, prepared_v_bytes(Bc, S_kv, H, hd, d->bf16)),
+                !hip_ok(hipMalloc(&b.ctx_v, prepared_v_bytes(Bc, S_kv, H, hd, d->attn)),
                         "dit context V cache"))
                 return false;
         }
@@ -1038,16 +1044,19 @@ bool anima_hip_dit_set_context_dev(anima_hip_dit *d, const float *ctx, int Bc, i
     void *ls = static_cast<char *>(d->ctx_work) + 2 * proj;
     // Per block: K = k_norm(ctx Wk^T), V = ctx Wv^T (numpy_dit.py:277-286),
     // prepared once for every later forward.
+    // f32 mode: K normalised in place in the cache, V projected straight
+    // into it; bf16 / f32x3: projections in the workspace, then packed.
+    const bool packed = d->attn != kAttnF32;
     for (auto &b : d->blk) {
-        float *ko = d->bf16 ? kf : static_cast<float *>(b.ctx_k);
-        float *vo = d->bf16 ? vf : static_cast<float *>(b.ctx_v);
+        float *ko = packed ? kf : static_cast<float *>(b.ctx_k);
+        float *vo = packed ? vf : static_cast<float *>(b.ctx_v);
         if (!launch_linear(ctx, C, b.cx_k, C, ko, HD, M, HD, C, !d->bf16, ls, lin, st) ||
             !launch_linear(ctx, C, b.cx_v, C, vo, HD, M, HD, C, !d->bf16, ls, lin, st))
             return false;
-        const bool ok = d->bf16 ? prepare_kv(kf, vf, b.cx_kn, nullptr, b.ctx_k, b.ctx_v, Bc, S_kv,
-                                             H, hd, 1e-6f, true, st)
-                                : prepare_kv(ko, nullptr, b.cx_kn, nullptr, b.ctx_k, nullptr, Bc,
-                                             S_kv, H, hd, 1e-6f, false, st);
+        const bool ok = packed ? prepare_kv(kf, vf, b.cx_kn, nullptr, b.ctx_k, b.ctx_v, Bc, S_kv,
+                                            H, hd, 1e-6f, d->attn, st)
+                               : prepare_kv(ko, nullptr, b.cx_kn, nullptr, b.ctx_k, nullptr, Bc,
+                                            S_kv, H, hd, 1e-6f, kAttnF32, st);
         if (!ok)
             return false;
     }

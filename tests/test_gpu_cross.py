@@ -97,6 +97,15 @@ def test_config2_cross_attention_cached_kv(Bc):
     finally:
         cache.close()
 
+    cache = rt.ContextKV(ctx, wk, wv, ones, heads=16, head_dim=128, mode=rt.F32X3)
+    try:
+        out = cache.attend(q, ones)
+        err = float(np.abs(out - ref).max())
+        print(f"config2 Bc={Bc} f32x3 max_abs={err:.3e}", flush=True)
+        assert err <= TOL
+    finally:
+        cache.close()
+
 
 def test_cross_attention_errors():
     rng = np.random.default_rng(1)
@@ -110,8 +119,9 @@ def test_cross_attention_errors():
         assert np.isfinite(out).all()
     finally:
         cache.close()
-    with pytest.raises(AnimaHipError, match="D == 128"):
-        rt.ContextKV(ctx, w, w, None, heads=2, head_dim=64, mode=rt.BF16)
+    for mode in (rt.BF16, rt.F32X3):
+        with pytest.raises(AnimaHipError, match="D == 128"):
+            rt.ContextKV(ctx, w, w, None, heads=2, head_dim=64, mode=mode)
 
 
 def test_config5_rectangular_6144_sampled_heads():
@@ -123,7 +133,8 @@ def test_config5_rectangular_6144_sampled_heads():
     f = generate_rope_freqs(96, 64)
     ones = np.ones(D, np.float32)
     for mode, check in [(rt.F32, lambda o, r: float(np.abs(o - r).max()) <= TOL),
-                        (rt.BF16, lambda o, r: rel_err(o, r) <= REL)]:
+                        (rt.BF16, lambda o, r: rel_err(o, r) <= REL),
+                        (rt.F32X3, lambda o, r: float(np.abs(o - r).max()) <= TOL)]:
         out = rt.attention(q, k, v, ones, ones, f, mode=mode)
         for b, h in [(0, 7), (1, 2)]:
             ref = oracle.attention_dataflow(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, h:h + 1],
@@ -133,8 +144,12 @@ def test_config5_rectangular_6144_sampled_heads():
             assert check(out[b, :, h], ref[0, :, 0])
     # cross 6144 x 512 (no RoPE), K/V [B, 512, H, D]
     kc, vc = randn(rng, B, 512, H, D), randn(rng, B, 512, H, D)
-    out = rt.attention(q, kc, vc, ones, ones, None)
+    outs = {mode: rt.attention(q, kc, vc, ones, ones, None, mode=mode)
+            for mode in (rt.F32, rt.F32X3)}
     for b, h in [(0, 9), (1, 0)]:
         ref = oracle.attention_dataflow(q[b:b + 1, :, h:h + 1], kc[b:b + 1, :, h:h + 1],
                                         vc[b:b + 1, :, h:h + 1], ones, ones, None)
-        assert float(np.abs(out[b, :, h] - ref[0, :, 0]).max()) <= TOL
+        for mode, out in outs.items():
+            err = float(np.abs(out[b, :, h] - ref[0, :, 0]).max())
+            print(f"config5 cross mode={mode} b={b} h={h} max_abs={err:.3e}", flush=True)
+            assert err <= TOL

@@ -9,7 +9,9 @@ bit-identical to the reference's on the fixture.
 Tolerances, normwise over the output (max |out - ref| / max |ref|):
   f32 mode  1e-4 (every linear layer runs on exact hi+lo bf16 terms, per
             element <= 2^-16 relative; LayerNorm sums in another order;
-            device exp/erf/cos/sin round within a few ulp);
+            device exp/erf/cos/sin round within a few ulp); the same for the
+            f32x3 mode, whose attention takes its f32 operands as bf16 term
+            pairs (~1e-5 relative);
   bf16 mode 3e-2 (activations rounded to bf16 before every linear layer and
             attention, as the 2e-2 attention path tolerance compounds over
             the blocks).
@@ -30,7 +32,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "golden"))
 import dit_weights  # noqa: E402
 
-TOL = {rt.F32: 1e-4, rt.BF16: 3e-2}
+TOL = {rt.F32: 1e-4, rt.BF16: 3e-2, rt.F32X3: 1e-4}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -71,7 +73,7 @@ def _err(out, ref):
     return float(np.abs(out - ref).max() / np.abs(ref).max())
 
 
-@pytest.mark.parametrize("mode", [rt.F32, rt.BF16])
+@pytest.mark.parametrize("mode", [rt.F32, rt.BF16, rt.F32X3])
 def test_forward_matches_reference(gold, mode):
     g, cfg, w = gold
     print(f"dit forward mode={mode} cfg={cfg}", flush=True)
@@ -85,7 +87,7 @@ def test_forward_matches_reference(gold, mode):
     np.testing.assert_array_equal(again, out)  # deterministic, cache reused
 
 
-@pytest.mark.parametrize("mode", [rt.F32, rt.BF16])
+@pytest.mark.parametrize("mode", [rt.F32, rt.BF16, rt.F32X3])
 def test_sampler_matches_reference(gold, mode):
     g, cfg, w = gold
     print(f"dit euler mode={mode}", flush=True)
@@ -126,7 +128,7 @@ def test_full_width_block_vs_oracle():
     ref = oracle.dit_forward(x, sigma, ctx, w, 1, 16, 128,
                              sdpa=lambda a, b, c: oracle.flash_sdpa(a, b, c, threads=8))
     table, keep = _device_table(w)
-    for mode in (rt.F32, rt.BF16):
+    for mode in (rt.F32, rt.BF16, rt.F32X3):
         with AnimaDiT(table, DiTConfig.anima_2b(blocks=1), mode) as m:
             err = _err(m.forward(x, sigma, ctx), ref)
         print(f"  mode {mode}: normwise error {err:.3e}", flush=True)

@@ -153,3 +153,27 @@ def test_x3_deterministic():
     q, k, v = randn(rng, 2, 700, 128), randn(rng, 2, 900, 128), randn(rng, 2, 900, 128)
     a = rt.sdpa(q, k, v, mode=rt.F32X3)
     np.testing.assert_array_equal(a, rt.sdpa(q, k, v, mode=rt.F32X3))
+
+
+def test_x3_attention_core_config1_and_config3_sampled_heads():
+    """The fused attention core (anima_hip_attention: RMSNorm + RoPE prologue
+    writing term rows, term V^T pack, f32x3 flash) at 256 tokens and at the
+    4096-token, B=2, H=16 workload; two (batch, head) slices of the latter
+    against the oracle."""
+    ones = np.ones(128, np.float32)
+    rng = np.random.default_rng(1001)
+    q, k, v = randn(rng, 1, 256, 16, 128), randn(rng, 1, 256, 16, 128), randn(rng, 1, 256, 16, 128)
+    f = generate_rope_freqs(16, 16)
+    out = rt.attention(q, k, v, ones, ones, f, mode=rt.F32X3)
+    check(out, oracle.attention_dataflow(q, k, v, ones, ones, f), "attention config1")
+
+    rng = np.random.default_rng(3003)
+    B, S, H, D = 2, 4096, 16, 128
+    q, k, v = randn(rng, B, S, H, D), randn(rng, B, S, H, D), randn(rng, B, S, H, D)
+    f = generate_rope_freqs(64, 64)
+    out = rt.attention(q, k, v, ones, ones, f, mode=rt.F32X3)
+    assert np.isfinite(out).all()
+    for b, h in [(0, 3), (1, 14)]:
+        ref = oracle.attention_dataflow(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, h:h + 1],
+                                        v[b:b + 1, :, h:h + 1], ones, ones, f)
+        check(out[b, :, h], ref[0, :, 0], f"config3 b={b} h={h}")
