@@ -8,16 +8,21 @@ in NumpyDiT's [B,S,H,D] layout, already resident in HBM.
 
 One step = the whole device-resident hot path over that batch:
   prologue(q) + prologue(k)   per-head RMSNorm (w=1, eps 1e-6) + 3D RoPE
-  [bf16 variant: V -> packed bf16 V^T]
+  [bf16 / f32x3: V -> packed V^T]
   flash attention             softmax(QK^T/sqrt(D)) V, output in [B,S,H,D]
 FLOPs per step = 4*B*H*S_q*S_kv*D (softmax and prologue not counted).
 
-Prints ONE JSON line on stdout (progress goes to stderr).  `roofline` covers
-the flash kernel alone: its average duration is measured with HIP events
-recorded on the stream it is launched on, around every launch in the timed
-region.  The other variant (bf16 vs f32), the remaining configurations
-(256-token self-attention, cached 256x512 cross-attention, 6144-token
-self+cross, and one full 28-block denoise step) are reported beside it.
+Arithmetic variants: f32x3 (the headline by default) keeps f32 accuracy
+(max-abs 1e-4 tolerance) by taking every f32 operand as two bf16 terms and
+every product as three bf16 MFMA products; f32 runs the f32 MFMA; bf16 rounds
+the inputs to bf16.  Prints ONE JSON line on stdout (progress goes to
+stderr).  `roofline` covers the flash kernel alone: its average duration is
+measured with HIP events recorded on the stream it is launched on, around
+every launch in the timed region; the f32x3 kernel's peak is a third of the
+bf16 MFMA peak, so its `frac` is the bf16 MFMA pipe's utilisation.  The other
+variants and the remaining configurations (256-token self-attention, cached
+256x512 cross-attention, 6144-token self+cross, one full 28-block denoise
+step and one whole-DiT sampler step) are reported beside it.
 `cpu_baseline` times anima_rt's own flash attention (the reference built from
 source in oracle/_ref when present, else the bit-identical C restatement) on a
 bounded sample of the same heads on this host's CPU.
@@ -38,7 +43,16 @@ sys.path.insert(0, os.path.join(ROOT, "anima-on-android_amd"))
 # algorithmic product, so its ceiling in algorithmic FLOP/s is a third of the
 # bf16 peak.
 PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6, "f32x3": 2516.6 / 3}
+PEAK_BASIS = {"f32": "f32 dense MFMA peak (v_mfma_f32_32x32x2_f32)",
+              "bf16": "bf16 dense MFMA peak (v_mfma_f32_32x32x16_bf16)",
+              "f32x3": "bf16 dense MFMA peak / 3: every f32 product runs as three bf16 MFMA "
+                       "products (hi*hi + hi*lo + lo*hi) on v_mfma_f32_32x32x16_bf16"}
 MODE = {"f32": 0, "bf16": 1, "f32x3": 2}
+VARIANTS = ("f32x3", "f32", "bf16")
+STEP = {"f32": "qk prologue (RMSNorm+RoPE) x2 + flash attention",
+        "bf16": "qk prologue (RMSNorm+RoPE, bf16 out) x2 + V^T bf16 pack + flash attention",
+        "f32x3": "qk prologue (RMSNorm+RoPE, bf16 hi/lo term rows) x2 + V^T term pack + flash "
+                 "attention"}
 PREWARM_S = 2.0  # seconds of untimed steps before the warmup steps of each headline run
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "flash_traffic.json")
 WORKLOAD = "self-attention 4096x4096, B=2 H=16 D=128 (64x64 grid, RMSNorm+3D RoPE)"
@@ -54,9 +68,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--variant", choices=["f32", "bf16", "f32x3"], default="f32",
-                    help="headline arithmetic: f32 MFMA on f32 inputs, bf16 inputs with f32 "
-                         "accumulation, or f32 inputs as bf16 term pairs on bf16 MFMA")
+    ap.add_argument("--variant", choices=list(VARIANTS), default="f32x3",
+                    help="headline arithmetic: f32x3 (f32 inputs as bf16 term pairs on bf16 "
+                         "MFMA, f32 accuracy), f32 (f32 MFMA), or bf16 (bf16 inputs, f32 "
+                         "accumulation)")
     ap.add_argument("--cpu-heads", type=int, default=8,
                     help="(batch, head) slices timed single-core for cpu_baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -205,6 +220,7 @@ def headline(c, variant, q, k, v, freqs, ones, steps, warmup):
         "value": flops / (ms_step * 1e-3) / 1e12, "ms_per_step": ms_step,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
+                     "peak_basis": PEAK_BASIS[variant],
                      "traffic": traffic_for(f"flash_{variant}_d128"),
                      "kernel": f"flash_{variant}_d128", "avg_launch_ms": round(ms_flash, 4),
                      "flops_per_launch": flops},
@@ -262,9 +278,9 @@ def cross_attention_timer(c, mode, cache, B, S_q, seed, H=16, D=128):
 
 
 def other_configs(c, cpu_rate):
-    """Configs 1, 2, 5 and the 28-block denoise step, both arithmetic modes."""
+    """Configs 1, 2, 5 and the 28-block denoise step, every arithmetic mode."""
     out = {}
-    for variant in ("f32", "bf16"):
+    for variant in VARIANTS:
         mode = MODE[variant]
         res = {}
         run, fl = self_attention_timer(c, mode, 1, 256, (16, 16), 101)
@@ -511,6 +527,22 @@ def dropin_call(c, host, B, H, S, D, iters=3):
                     "the uploads and the download" % iters}
 
 
+def normalized_qk(c, q, k, freqs, ones):
+    """q, k after the f32 RMSNorm + RoPE prologue (the CPU baseline's inputs)."""
+    torch, lib, _lib = c.torch, c.lib, c._lib
+    B, S, H, D = q.shape
+    bshd = _lib.strides([S * H * D, D, H * D])
+    out = []
+    for x in (q, k):
+        y = torch.empty_like(x)
+        _lib.check(lib.anima_hip_qk_prologue_dev(x.data_ptr(), y.data_ptr(), ones.data_ptr(),
+                                                 freqs.data_ptr(), B, S, H, D, bshd, bshd,
+                                                 ct.c_float(1e-6), 1, c.stp), "qk_prologue")
+        out.append(y)
+    torch.cuda.synchronize()
+    return out
+
+
 def cpu_baseline(qn, kn, v, B, H, S, D, heads):
     """anima_rt flash attention on `heads` (b, h) slices, one core, plus the
     same per-head work spread over this host's cores."""
@@ -586,7 +618,7 @@ def main():
     c = Ctx(torch, lib, _lib)
 
     if args.sampler_step:
-        res = {v: sampler_step(c, MODE[v]) for v in ("bf16", "f32")}
+        res = {v: sampler_step(c, MODE[v]) for v in ("bf16", "f32x3", "f32")}
         print(json.dumps({"config": "c4_sampler_step_full_dit", "latent": [1, 16, 128, 128],
                           "results": res}), flush=True)
         return
@@ -605,31 +637,40 @@ def main():
         torch.cuda.synchronize()
         dst.copy_(src)
         torch.cuda.synchronize()
-        for variant in ("f32", "bf16"):
+        for variant in VARIANTS:
             headline(c, variant, q, k, v, freqs, ones, 2, 1)
         log("[bench] pmc pass done")
         return
 
     main_res = headline(c, args.variant, q, k, v, freqs, ones, args.steps, args.warmup)
+    # f32 RMSNorm+RoPE outputs for the CPU baseline: the f32 variant's own.
+    qk_f32 = (main_res["qn"], main_res["kn"]) if args.variant == "f32" else None
+    del main_res["qn"], main_res["kn"]
     variants = {}
     if not args.headline_only:
-        other = "bf16" if args.variant == "f32" else "f32"
-        r = headline(c, other, q, k, v, freqs, ones, args.steps, args.warmup)
-        variants[other] = {"value": round(r["value"], 2), "unit": "TFLOP/s",
-                           "ms_per_step": round(r["ms_per_step"], 4), "dtype": other,
-                           "pct_mfma_peak": round(100 * r["value"] / PEAK_TFLOPS[other], 2),
-                           "roofline": r["roofline"]}
-        del r
+        for other in VARIANTS:
+            if other == args.variant:
+                continue
+            r = headline(c, other, q, k, v, freqs, ones, args.steps, args.warmup)
+            variants[other] = {"value": round(r["value"], 2), "unit": "TFLOP/s",
+                               "ms_per_step": round(r["ms_per_step"], 4), "dtype": other,
+                               "pct_mfma_peak": round(100 * r["value"] / PEAK_TFLOPS[other], 2),
+                               "roofline": r["roofline"]}
+            if other == "f32":
+                qk_f32 = (r["qn"], r["kn"])
+            del r
 
     dropin = None if args.headline_only else dropin_call(c, host, B, H, S, D)
 
     cpu = multi = None
     if not args.no_cpu_baseline:
-        cpu, multi = cpu_baseline(main_res["qn"], main_res["kn"], v, B, H, S, D, args.cpu_heads)
+        if qk_f32 is None:
+            qk_f32 = normalized_qk(c, q, k, freqs, ones)
+        cpu, multi = cpu_baseline(qk_f32[0], qk_f32[1], v, B, H, S, D, args.cpu_heads)
+    qk_f32 = None
 
     configs = None
     if not args.headline_only:
-        del main_res["qn"], main_res["kn"]
         torch.cuda.empty_cache()
         configs = other_configs(c, cpu["value"] if cpu else None)
 
@@ -643,11 +684,9 @@ def main():
         "dtype": args.variant,
         "data": "synthetic (seeded N(0,1) q/k/v projections, unit RMSNorm weights)",
         "config": {"workload": WORKLOAD, "B": B, "H": H, "S_q": S, "S_kv": S, "D": D,
-                   "step": "qk prologue (RMSNorm+RoPE) x2 "
-                           + ("+ V^T bf16 pack " if args.variant == "bf16" else "")
-                           + "+ flash attention",
-                   "mfma": "v_mfma_f32_32x32x16_bf16" if args.variant == "bf16"
-                   else "v_mfma_f32_32x32x2_f32"},
+                   "step": STEP[args.variant],
+                   "mfma": "v_mfma_f32_32x32x2_f32" if args.variant == "f32"
+                   else "v_mfma_f32_32x32x16_bf16"},
         "pct_mfma_peak": round(100.0 * value / peak, 2),
         "roofline": main_res["roofline"],
         "cpu_baseline": cpu,
