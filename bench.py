@@ -48,6 +48,7 @@ PEAK_BASIS = {"f32": "f32 dense MFMA peak (v_mfma_f32_32x32x2_f32)",
               "f32x3": "bf16 dense MFMA peak / 3: every f32 product runs as three bf16 MFMA "
                        "products (hi*hi + hi*lo + lo*hi) on v_mfma_f32_32x32x16_bf16"}
 MODE = {"f32": 0, "bf16": 1, "f32x3": 2}
+KERNEL = {"f32": "flash_f32_d128", "bf16": "flash_bf16_d128", "f32x3": "flash_x3_d128"}
 VARIANTS = ("f32x3", "f32", "bf16")
 STEP = {"f32": "qk prologue (RMSNorm+RoPE) x2 + flash attention",
         "bf16": "qk prologue (RMSNorm+RoPE, bf16 out) x2 + V^T bf16 pack + flash attention",
@@ -221,8 +222,8 @@ def headline(c, variant, q, k, v, freqs, ones, steps, warmup):
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "peak_basis": PEAK_BASIS[variant],
-                     "traffic": traffic_for(f"flash_{variant}_d128"),
-                     "kernel": f"flash_{variant}_d128", "avg_launch_ms": round(ms_flash, 4),
+                     "traffic": traffic_for(KERNEL[variant]),
+                     "kernel": KERNEL[variant], "avg_launch_ms": round(ms_flash, 4),
                      "flops_per_launch": flops},
         "qn": qn, "kn": kn,
     }
