@@ -19,7 +19,7 @@ import numpy as np
 
 from . import _lib
 from .rope import generate_rope_freqs
-from .rt import BF16, F32
+from .rt import BF16, F32, F32X3
 
 DTYPE_CODES = {"F32": 0, "F16": 1, "BF16": 2}
 ADA_HIDDEN = 256  # hidden width of every AdaLN modulation MLP
@@ -124,7 +124,9 @@ class AnimaDiT:
     weights: an ``rt.Weights`` store (device copies are made on demand: linear
     weights as bf16 bits, norm weights widened to f32), or a dict
     name -> (device pointer, dtype string, shape) of tensors already on the
-    device, which must outlive the model.  mode: ``rt.F32`` or ``rt.BF16``."""
+    device, which must outlive the model.  mode: ``rt.F32`` (f32 MFMA attention), ``rt.F32X3``
+    (attention on bf16 term pairs, the same f32 tolerance) or ``rt.BF16``; the linear layers take
+    exact hi + lo bf16 terms except in ``rt.BF16``."""
 
     def __init__(self, weights, config: DiTConfig | None = None, mode=F32):
         self._lib = _lib.load()
@@ -267,4 +269,4 @@ class AnimaDiT:
             pass
 
 
-__all__ = ["AnimaDiT", "DiTConfig", "DeviceArray", "weight_shapes", "F32", "BF16"]
+__all__ = ["AnimaDiT", "DiTConfig", "DeviceArray", "weight_shapes", "F32", "F32X3", "BF16"]

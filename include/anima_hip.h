@@ -203,8 +203,9 @@ bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, 
  * like the reference) and f32 output c, on device memory.  Replaces the
  * projections of NumpyAttention.forward (anima_rt/scripts/numpy_dit.py:273-281,
  * 294-296), computed there by anima_rt/vulkan/gemm_bf16.comp:25-57.
- *   mode ANIMA_HIP_F32:  a enters as two bf16 terms hi + lo (per-element
- *                        representation error <= 2^-16 |a|), f32 accumulation;
+ *   mode ANIMA_HIP_F32 (and ANIMA_HIP_F32X3, the same here): a enters as two
+ *                        bf16 terms hi + lo (per-element representation
+ *                        error <= 2^-16 |a|), f32 accumulation;
  *   mode ANIMA_HIP_BF16: a is rounded to bf16 (<= 2^-8 |a|).
  * scratch: anima_hip_linear_scratch_bytes(M, K, mode) bytes of device memory,
  * 16-byte aligned; nothing is allocated.  Shapes without a library solution
@@ -233,7 +234,8 @@ bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
  * per-head RMSNorm weights [D], optional RoPE table [S_q, D/2, 2, 2]
  * (self-attention only; requires S_q == S_kv), scale 1/sqrt(D), no mask.
  * Writes out [B,S_q,H,D], i.e. the [B*S_q, H*D] input of output_proj.
- * mode: ANIMA_HIP_F32 or ANIMA_HIP_BF16. */
+ * mode: ANIMA_HIP_F32, ANIMA_HIP_F32X3 or ANIMA_HIP_BF16 (the last two need
+ * D == 128). */
 bool anima_hip_attention(const float *q, const float *k, const float *v,
                          const float *q_norm_w, const float *k_norm_w, const float *freqs,
                          float *out, int B, int S_q, int S_kv, int H, int D, float eps,
@@ -249,7 +251,9 @@ bool anima_hip_attention(const float *q, const float *k, const float *v,
  * ctx: [Bc, S_kv, C] f32 host; Wk, Wv: [H*D, C] bf16 bit patterns (the
  * safetensors [out_features, in_features] layout); k_norm_w: [D] or NULL.
  * Bc = 1 serves every query batch (both CFG branches share one context);
- * otherwise Bc must equal the query batch.  Returns NULL on failure. */
+ * otherwise Bc must equal the query batch.  mode: ANIMA_HIP_F32,
+ * ANIMA_HIP_F32X3 or ANIMA_HIP_BF16 (projections on exact hi+lo terms except
+ * in bf16 mode).  Returns NULL on failure. */
 typedef struct anima_hip_ctx_kv anima_hip_ctx_kv;
 
 anima_hip_ctx_kv *anima_hip_ctx_kv_create(const float *ctx, const uint16_t *wk, const uint16_t *wv,
@@ -283,7 +287,8 @@ bool anima_hip_cross_attention_dev(const float *q, const float *q_norm_w,
  * context cache (wk, wv, k_norm_w and freqs unused; H, D and mode must match
  * the cache).  LayerNorm has no affine parameters, as the reference calls it.
  * mode ANIMA_HIP_F32: projections on exact hi+lo bf16 terms and the f32
- * attention path; ANIMA_HIP_BF16: bf16 activations throughout.  Dm and H*D
+ * attention path; ANIMA_HIP_F32X3: the same projections and the f32x3
+ * attention; ANIMA_HIP_BF16: bf16 activations throughout.  Dm and H*D
  * must be multiples of 8, Dm <= 4096.  scratch: device memory of
  * anima_hip_attention_block_scratch_bytes(kv, B, S, Dm, H, D, mode) bytes,
  * 16-byte aligned; nothing is allocated.  Asynchronous on `stream`. */
@@ -360,8 +365,10 @@ void anima_hip_dit_default_config(anima_hip_dit_config *cfg);
  * [out, in]; norm weights F32 or BF16 (widened like the reference).  The
  * pointers are borrowed and must stay valid for the model's life (the weight
  * store's anima_hip_weights_device copies do).  mode: ANIMA_HIP_F32 (f32
- * activations, exact hi+lo bf16 GEMM terms, f32 attention) or ANIMA_HIP_BF16
- * (bf16 activations and attention inputs).  NULL on error. */
+ * activations, exact hi+lo bf16 GEMM terms, f32 attention), ANIMA_HIP_F32X3
+ * (the same with attention on bf16 term pairs; head_dim 128) or
+ * ANIMA_HIP_BF16 (bf16 activations and attention inputs; head_dim 128).
+ * NULL on error. */
 anima_hip_dit *anima_hip_dit_create(const anima_hip_dit_config *cfg, const char *const *names,
                                     const void *const *ptrs, const int *dtypes,
                                     const int64_t *shapes, int n, int mode);
