@@ -32,6 +32,7 @@
 
 #include "anima_hip.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -78,6 +79,11 @@ __device__ __forceinline__ void store_terms8(const float (&v)[8], unsigned int *
 // ---- timestep features -------------------------------------------------
 struct TimestepArgs {
     float sigma[kMaxBatch];
+    // When set, every batch entry takes sigma_dev[*step] instead (the
+    // sampler's per-step value, read on the device so that one captured
+    // step serves every step).
+    const float *sigma_dev;
+    const int *step;
     float *out;  // [B][D]
     int D;
 };
@@ -92,7 +98,8 @@ __global__ __launch_bounds__(256) void timestep_kernel(TimestepArgs a)
     const int j = i < half ? i : i - half;
     // exponent = -log(10000) * arange(half, float32) / float(half), in float32.
     const float e = (-9.21034037197618f * float(j)) / float(half);
-    const float arg = a.sigma[b] * expf(e);
+    const float sigma = a.sigma_dev ? a.sigma_dev[*a.step] : a.sigma[b];
+    const float arg = sigma * expf(e);
     a.out[int64_t(b) * a.D + i] = i < half ? cosf(arg) : sinf(arg);
 }
 
@@ -264,7 +271,11 @@ struct EulerArgs {
     float *x;
     int64_t n, S;  // C*Hi*Wi; tokens per branch
     int Cout, Hi, Wi, Wp;
-    float cfg, dt;
+    float cfg;
+    // dt = sigmas[step + 1] - sigmas[step], rounded once from the exact
+    // difference like the reference's float64 subtraction.
+    const float *sigmas;
+    const int *step;
 };
 
 __global__ __launch_bounds__(256) void cfg_euler_kernel(EulerArgs a)
@@ -280,7 +291,16 @@ __global__ __launch_bounds__(256) void cfg_euler_kernel(EulerArgs a)
     const float vu = a.f[m * 4 * a.Cout + col];
     const float vc = a.f[(a.S + m) * 4 * a.Cout + col];
     const float v = vu + a.cfg * (vc - vu);
-    a.x[i] = a.x[i] + v * a.dt;
+    const int st = *a.step;
+    const float dt = float(double(a.sigmas[st + 1]) - double(a.sigmas[st]));
+    a.x[i] = a.x[i] + v * dt;
+}
+
+// The sampler's device step counter: set to `value`, or advanced by one.
+__global__ void step_kernel(int *step, int value, int advance)
+{
+    if (threadIdx.x == 0 && blockIdx.x == 0)
+        *step = advance ? *step + 1 : value;
 }
 
 // bf16 bit patterns -> f32 (the reference's widening of norm weights).
@@ -388,6 +408,30 @@ struct anima_hip_dit {
     int ctx_B = 0, ctx_S = 0;
     void *ctx_work = nullptr;
     size_t ctx_work_bytes = 0;
+    // Sampler: the sigmas of a run on the device (capacity sig_cap), staged
+    // through pinned host memory (reused once sig_ev has completed), the step
+    // counter, and one captured Euler step (graph) for the buffers in
+    // `graph_key`, replayed for every step after the first.
+    float *sig_dev = nullptr, *sig_host = nullptr;
+    int sig_cap = 0;
+    hipEvent_t sig_ev = nullptr;
+    int *step_dev = nullptr;
+    hipStream_t cap_stream = nullptr;
+    hipGraphExec_t graph = nullptr;
+    struct GraphKey {
+        const void *latent, *freqs, *scratch, *sig;
+        size_t scratch_bytes;
+        int H, W;
+        float cfg;
+        unsigned gen;
+        bool operator==(const GraphKey &o) const
+        {
+            return latent == o.latent && freqs == o.freqs && scratch == o.scratch &&
+                   sig == o.sig && scratch_bytes == o.scratch_bytes && H == o.H && W == o.W &&
+                   cfg == o.cfg && gen == o.gen;
+        }
+    } graph_key{};
+    unsigned gen = 0;  // advanced whenever the context caches move
 };
 
 namespace {
@@ -407,6 +451,16 @@ void dit_free(anima_hip_dit *d)
     }
     if (d->ctx_work)
         (void)hipFree(d->ctx_work);
+    if (d->graph)
+        (void)hipGraphExecDestroy(d->graph);
+    if (d->cap_stream)
+        (void)hipStreamDestroy(d->cap_stream);
+    if (d->sig_dev)
+        (void)hipFree(d->sig_dev);
+    if (d->sig_host)
+        (void)hipHostFree(d->sig_host);
+    if (d->sig_ev)
+        (void)hipEventDestroy(d->sig_ev);
     delete d;
 }
 
@@ -613,7 +667,8 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
 // in the `f` region of the scratch (returned through f_out).
 bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, int B, int T,
              int H, int W, const float *freqs, void *scratch, size_t scratch_bytes,
-             hipStream_t st, float **f_out)
+             hipStream_t st, float **f_out, const float *sigma_dev = nullptr,
+             const int *step_dev = nullptr)
 {
     const anima_hip_dit_config &c = d->cfg;
     if (B < 1 || B > c.max_batch)
@@ -650,6 +705,8 @@ bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, i
     TimestepArgs ta;
     for (int b = 0; b < kMaxBatch; ++b)
         ta.sigma[b] = b < B ? sigma[b] : 0.0f;
+    ta.sigma_dev = sigma_dev;
+    ta.step = step_dev;
     ta.out = d->feat;
     ta.D = D;
     hipLaunchKernelGGL(timestep_kernel, dim3(grid1(D), unsigned(B)), dim3(256), 0, st, ta);
@@ -904,7 +961,8 @@ anima_hip_dit *anima_hip_dit_create(const anima_hip_dit_config *cfg, const char 
          dev_alloc(d, d->lora, size_t(MB) * 3 * D * 4, "dit vectors") &&
          dev_alloc(d, d->m1, size_t(d->n_ada) * MB * kAdaHidden * 4, "dit vectors") &&
          dev_alloc(d, d->mods, size_t(d->n_ada) * MB * 3 * D * 4, "dit vectors") &&
-         dev_alloc(d, d->jobs, size_t(nj) * sizeof(GemvJob), "dit job table");
+         dev_alloc(d, d->jobs, size_t(nj) * sizeof(GemvJob), "dit job table") &&
+         dev_alloc(d, d->step_dev, sizeof(int), "dit step counter");
     if (ok) {
         // The job table holds the batch strides of max_batch-sized buffers;
         // a forward on B <= max_batch rows uses the first B of each.
@@ -1024,6 +1082,7 @@ bool anima_hip_dit_set_context_dev(anima_hip_dit *d, const float *ctx, int Bc, i
         }
         d->alloc_B = Bc;
         d->alloc_S = S_kv;
+        ++d->gen;  // a captured sampler step holds the old cache addresses
     }
     const size_t proj = round_up256(size_t(M) * HD * 4);
     const size_t lin = round_up256(linear_scratch_bytes(M, C, !d->bf16));
@@ -1115,15 +1174,53 @@ bool anima_hip_dit_euler_dev(anima_hip_dit *d, float *latent, const float *sigma
                     "(unconditional, conditional)");
     if (d->cfg.in_channels != d->cfg.out_channels)
         return fail("dit_euler: the latent needs as many output channels as input channels");
+    if (steps == 0)
+        return true;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     int Hp, Wp;
     int64_t S;
     grid_of(1, H, W, Hp, Wp, S);
-    for (int i = 0; i < steps; ++i) {
-        // CFG batch [uncond, cond] of the same latent (sampling.py:124-130).
-        const float sig[2] = {sigmas[i], sigmas[i]};
+
+    // The run's sigmas to the device, through pinned staging that the
+    // previous run's copy has finished reading.
+    const int n_sig = steps + 1;
+    if (d->sig_ev && !hip_ok(hipEventSynchronize(d->sig_ev), "hipEventSynchronize"))
+        return false;
+    if (n_sig > d->sig_cap) {
+        if (!hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize"))
+            return false;
+        if (d->sig_dev)
+            (void)hipFree(d->sig_dev);
+        if (d->sig_host)
+            (void)hipHostFree(d->sig_host);
+        d->sig_dev = d->sig_host = nullptr;
+        d->sig_cap = 0;
+        const int cap = std::max(n_sig, 64);
+        if (!hip_ok(hipMalloc(&d->sig_dev, size_t(cap) * 4), "dit sigma buffer") ||
+            !hip_ok(hipHostMalloc(&d->sig_host, size_t(cap) * 4, hipHostMallocDefault),
+                    "dit sigma staging"))
+            return false;
+        d->sig_cap = cap;
+        ++d->gen;  // the captured step holds the old sigma buffer
+    }
+    if (!d->sig_ev && !hip_ok(hipEventCreateWithFlags(&d->sig_ev, hipEventDisableTiming),
+                              "hipEventCreate"))
+        return false;
+    std::copy(sigmas, sigmas + n_sig, d->sig_host);
+    if (!hip_ok(hipMemcpyAsync(d->sig_dev, d->sig_host, size_t(n_sig) * 4,
+                               hipMemcpyHostToDevice, st),
+                "sigma upload") ||
+        !hip_ok(hipEventRecord(d->sig_ev, st), "hipEventRecord"))
+        return false;
+
+    // One Euler step on stream s: the CFG batch [uncond, cond] of the same
+    // latent at sigmas[step] (sampling.py:124-130), the update, and the
+    // counter advanced for the next step.
+    const float unused[2] = {0.0f, 0.0f};
+    auto step = [&](hipStream_t s) {
         float *f = nullptr;
-        if (!dit_run(d, latent, 0, sig, 2, 1, H, W, freqs, scratch, scratch_bytes, st, &f))
+        if (!dit_run(d, latent, 0, unused, 2, 1, H, W, freqs, scratch, scratch_bytes, s, &f,
+                     d->sig_dev, d->step_dev))
             return false;
         EulerArgs ea;
         ea.f = f;
@@ -1135,11 +1232,75 @@ bool anima_hip_dit_euler_dev(anima_hip_dit *d, float *latent, const float *sigma
         ea.Wp = Wp;
         ea.n = int64_t(ea.Cout) * H * W;
         ea.cfg = cfg;
-        ea.dt = float(double(sigmas[i + 1]) - double(sigmas[i]));
-        hipLaunchKernelGGL(cfg_euler_kernel, dim3(grid1(ea.n)), dim3(256), 0, st, ea);
-        if (!hip_ok(hipGetLastError(), "cfg_euler_kernel launch"))
+        ea.sigmas = d->sig_dev;
+        ea.step = d->step_dev;
+        hipLaunchKernelGGL(cfg_euler_kernel, dim3(grid1(ea.n)), dim3(256), 0, s, ea);
+        hipLaunchKernelGGL(step_kernel, dim3(1), dim3(64), 0, s, d->step_dev, 0, 1);
+        return hip_ok(hipGetLastError(), "cfg_euler_kernel launch");
+    };
+    hipLaunchKernelGGL(step_kernel, dim3(1), dim3(64), 0, st, d->step_dev, 0, 0);
+    // The first step runs directly (it also creates every GEMM plan the
+    // step needs); the rest replay one captured step, recorded on the
+    // model's own stream, then launched on the caller's.
+    if (!step(st))
+        return false;
+    if (steps == 1)
+        return true;
+    const anima_hip_dit::GraphKey key{latent, freqs, scratch, d->sig_dev, scratch_bytes, H, W,
+                                      cfg, d->gen};
+    if (!(d->graph && d->graph_key == key)) {
+        if (d->graph) {
+            if (!hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize"))
+                return false;
+            (void)hipGraphExecDestroy(d->graph);
+            d->graph = nullptr;
+        }
+        if (!d->cap_stream &&
+            !hip_ok(hipStreamCreateWithFlags(&d->cap_stream, hipStreamNonBlocking),
+                    "hipStreamCreate"))
             return false;
+        hipGraph_t g = nullptr;
+        if (!hip_ok(hipStreamBeginCapture(d->cap_stream, hipStreamCaptureModeThreadLocal),
+                    "hipStreamBeginCapture"))
+            return false;
+        const bool recorded = step(d->cap_stream);
+        const hipError_t e = hipStreamEndCapture(d->cap_stream, &g);
+        bool ok = recorded && hip_ok(e, "hipStreamEndCapture");
+        // Only kernel launches may be replayed: a library call that recorded
+        // a memset or copy node leaves the remaining steps to run directly.
+        bool kernels_only = ok;
+        if (ok) {
+            size_t n = 0;
+            ok = hip_ok(hipGraphGetNodes(g, nullptr, &n), "hipGraphGetNodes");
+            std::vector<hipGraphNode_t> nodes(n);
+            ok = ok && hip_ok(hipGraphGetNodes(g, nodes.data(), &n), "hipGraphGetNodes");
+            for (size_t i = 0; ok && i < n; ++i) {
+                hipGraphNodeType t;
+                ok = hip_ok(hipGraphNodeGetType(nodes[i], &t), "hipGraphNodeGetType");
+                kernels_only = kernels_only && t == hipGraphNodeTypeKernel;
+            }
+            kernels_only = kernels_only && ok;
+        }
+        if (ok && kernels_only)
+            ok = hip_ok(hipGraphInstantiate(&d->graph, g, nullptr, nullptr, 0),
+                        "hipGraphInstantiate");
+        if (g)
+            (void)hipGraphDestroy(g);
+        if (!ok) {
+            d->graph = nullptr;
+            return false;
+        }
+        if (!kernels_only) {
+            for (int i = 1; i < steps; ++i)
+                if (!step(st))
+                    return false;
+            return true;
+        }
+        d->graph_key = key;
     }
+    for (int i = 1; i < steps; ++i)
+        if (!hip_ok(hipGraphLaunch(d->graph, st), "hipGraphLaunch"))
+            return false;
     return true;
 }
 
