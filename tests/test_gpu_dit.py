@@ -109,18 +109,23 @@ def test_sampler_matches_reference(gold, mode):
 def test_sampler_graph_replays_match_host_loop(gold, mode):
     """anima_hip_dit_euler_dev runs its first step directly and replays one
     captured step (a HIP graph) for the rest.  Every replay must equal the
-    reference's host loop over forward: two runs of 5 and 3 steps with
-    different sigmas (the second replays the cached graph from its second
-    step), with direct forwards and host synchronisation in between."""
+    reference's host loop over forward: runs of 5 and 3 steps with different
+    sigmas (the second replays the cached graph), then a run whose longer
+    context moves the caches (the step is captured again), with direct
+    forwards and host synchronisation in between."""
     g, cfg, w = gold
     table, keep = _device_table(w)
     noise, c_c, c_u = g["smp_noise"], g["smp_ctx_cond"], g["smp_ctx_uncond"]
+    # The third run's context is 3 tokens longer: its caches move, so the
+    # captured step must be recorded again.
+    longer = [np.concatenate([c, c[:, :3]], axis=1) for c in (c_c, c_u)]
     with AnimaDiT(table, _config(cfg), mode) as m:
-        for n, shift in ((5, 1.0), (3, 3.0)):
+        for n, shift, (cc, cu) in ((5, 1.0, (c_c, c_u)), (3, 3.0, (c_c, c_u)),
+                                   (3, 2.0, longer)):
             sig = oracle.z_image_sigmas(n, 1.0, shift)
-            print(f"dit graph mode={mode} steps={n}", flush=True)
-            dev = m.sample(noise, sig, c_c, c_u, 5.0)
-            host = oracle.euler_sample(m.forward, noise, sig, c_c, c_u, 5.0)
+            print(f"dit graph mode={mode} steps={n} ctx={cc.shape[1]}", flush=True)
+            dev = m.sample(noise, sig, cc, cu, 5.0)
+            host = oracle.euler_sample(m.forward, noise, sig, cc, cu, 5.0)
             np.testing.assert_array_equal(dev, host)
             assert np.isfinite(dev).all() and not np.array_equal(dev, noise)
 
