@@ -428,6 +428,16 @@ bool launch_flash_x3(const FlashProblem &p, hipStream_t st, void *part, size_t p
     const int64_t sp = vt_padded_len(p.S_kv);
     if (p.vs.s != sp)
         return fail("flash_x3: V^T row stride must equal the padded key count");
+    // Every Q/K row is read as 2*D elements ([hi | lo]): a row stride below
+    // that (e.g. a dense row of D values) would read past the tensor's end.
+    const auto rows_fit = [](const Strides &x) {
+        for (const int64_t v : {x.b, x.h, x.s})
+            if (v != 0 && (v < 0 || v < kRow))
+                return false;
+        return true;
+    };
+    if (!rows_fit(p.qs) || !rows_fit(p.ks))
+        return fail("flash_x3: q/k strides must leave 2*D = 256 elements per row (hi | lo terms)");
     const auto s8 = [](const Strides &x) { return x.b % 8 == 0 && x.h % 8 == 0 && x.s % 8 == 0; };
     if (!aligned(p.q, 16) || !aligned(p.k, 16) || !aligned(p.v, 16) || !aligned(p.o, 16) ||
         !s8(p.qs) || !s8(p.ks) || !s8(p.vs) || p.os.b % 4 || p.os.h % 4 || p.os.s % 4)

@@ -148,6 +148,21 @@ def test_x3_device_entries_match_host_path():
     np.testing.assert_array_equal(vt[:, :, D:], full_lo)
 
 
+def test_x3_device_entry_rejects_dense_row_strides():
+    """Term rows hold 2*D values; strides of dense D-value rows are refused
+    before any launch (the lo half would be read past the tensor's end)."""
+    lib = _lib.load()
+    B, H, S, D = 1, 2, 64, 128
+    buf = DevBuf(B * H * S * 2 * D * 2)
+    o = DevBuf(B * H * S * D * 4)
+    sp = lib.anima_hip_vt_padded_len(S)
+    vt = DevBuf(B * H * 2 * D * sp * 2)
+    dense = _lib.strides([H * S * D, S * D, D])
+    ok = lib.anima_hip_flash_x3_dev(buf.addr, buf.addr, vt.addr, o.addr, B, H, S, S, D, dense,
+                                    None, None, None, ct.c_float(0.1), False, None)
+    assert not ok and "256 elements per row" in _lib.last_error()
+
+
 def test_x3_deterministic():
     rng = np.random.default_rng(5)
     q, k, v = randn(rng, 2, 700, 128), randn(rng, 2, 900, 128), randn(rng, 2, 900, 128)
