@@ -438,6 +438,11 @@ bool launch_flash_x3(const FlashProblem &p, hipStream_t st, void *part, size_t p
     };
     if (!rows_fit(p.qs) || !rows_fit(p.ks))
         return fail("flash_x3: q/k strides must leave 2*D = 256 elements per row (hi | lo terms)");
+    // Each (batch, head) of the term V^T holds 2*D rows of Sp keys.
+    for (const int64_t v : {p.vs.b, p.vs.h})
+        if (v != 0 && (v < 0 || v < int64_t(2 * kD) * vt_padded_len(p.S_kv)))
+            return fail("flash_x3: V^T batch/head strides must leave 2*D rows of the padded key "
+                        "count per head");
     const auto s8 = [](const Strides &x) { return x.b % 8 == 0 && x.h % 8 == 0 && x.s % 8 == 0; };
     if (!aligned(p.q, 16) || !aligned(p.k, 16) || !aligned(p.v, 16) || !aligned(p.o, 16) ||
         !s8(p.qs) || !s8(p.ks) || !s8(p.vs) || p.os.b % 4 || p.os.h % 4 || p.os.s % 4)

@@ -161,6 +161,11 @@ def test_x3_device_entry_rejects_dense_row_strides():
     ok = lib.anima_hip_flash_x3_dev(buf.addr, buf.addr, vt.addr, o.addr, B, H, S, S, D, dense,
                                     None, None, None, ct.c_float(0.1), False, None)
     assert not ok and "256 elements per row" in _lib.last_error()
+    terms = _lib.strides([H * S * 2 * D, S * 2 * D, 2 * D])
+    bf16_vt = _lib.strides([H * D * sp, D * sp, sp])  # the bf16 layout: D rows per head
+    ok = lib.anima_hip_flash_x3_dev(buf.addr, buf.addr, vt.addr, o.addr, B, H, S, S, D, terms,
+                                    terms, bf16_vt, None, ct.c_float(0.1), False, None)
+    assert not ok and "2*D rows" in _lib.last_error()
 
 
 def test_x3_deterministic():
