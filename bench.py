@@ -304,6 +304,15 @@ def other_configs(c, cpu_rate):
         cache.close()
         c.torch.cuda.empty_cache()
 
+        # Config 3 at one GPU's share of a 2-GPU split (design only beyond
+        # one GPU): one CFG branch (B=1) or half the heads (H=8), the whole
+        # attention call (prologues, V^T pack, flash).
+        for key, b_, h_ in (("c3_share_cfg_split_B1", 1, 16), ("c3_share_head_split_H8", 2, 8)):
+            run, fl = self_attention_timer(c, mode, b_, 4096, (64, 64), 301, H=h_)
+            ms = c.time(run, 10, 2)
+            res[key] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 2)}
+        c.torch.cuda.empty_cache()
+
         res["c4_denoise_step_28_blocks"] = denoise_step(c, mode)
         res["proj_gemm_8192x2048x2048"] = projection_gemm(c, mode)
         res["c4_denoise_step_28_blocks_attention_sublayers"] = denoise_step_blocks(c, mode)
