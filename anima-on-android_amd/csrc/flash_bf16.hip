@@ -66,9 +66,10 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     const int col = lane & 31;
     const int half = lane >> 5;
 
-    const int sp = blockIdx.x % a.split.n;
-    const int qt = (blockIdx.x / a.split.n) % a.n_qtiles;
-    const int bh = (blockIdx.x / a.split.n) / a.n_qtiles;
+    const int blk = xcd_major_block();
+    const int sp = blk % a.split.n;
+    const int qt = (blk / a.split.n) % a.n_qtiles;
+    const int bh = (blk / a.split.n) / a.n_qtiles;
     const int b = bh / a.H;
     const int h = bh - b * a.H;
     const int q_tile0 = qt * BM;

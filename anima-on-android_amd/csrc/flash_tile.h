@@ -120,6 +120,22 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16 &s, int base)
     return r;
 }
 
+// Logical id of this workgroup, XCD-major.  The dispatcher hands workgroup i
+// to XCD i % 8, so consecutive ids land on different XCDs and every XCD ends
+// up streaming every (batch, head)'s K/V from HBM.  Renumbered so that the
+// workgroups of one XCD take one contiguous range of ids, the query tiles of
+// a (batch, head), which read the same K/V tiles at about the same time, run
+// on one XCD and share its L2.  A bijection on [0, gridDim.x) for every grid
+// size (the first n % 8 XCDs take one id more), so only locality depends on
+// the dispatch order, never the result.
+constexpr unsigned kXcds = 8;
+__device__ __forceinline__ int xcd_major_block()
+{
+    const unsigned n = gridDim.x, i = blockIdx.x, x = i % kXcds;
+    const unsigned q = n / kXcds, r = n % kXcds;
+    return int(x * q + (x < r ? x : r) + i / kXcds);
+}
+
 inline bool aligned(const void *ptr, unsigned m)
 {
     return (reinterpret_cast<uintptr_t>(ptr) & (m - 1)) == 0;
