@@ -53,6 +53,13 @@ class DevBuf:
         _ok(hip().hipMemcpy(b.addr, arr.ctypes.data, arr.nbytes, _H2D), "hipMemcpy H2D")
         return b
 
+    def put(self, arr, offset):
+        """Copy `arr` to bytes [offset, offset + arr.nbytes) of the buffer."""
+        arr = np.ascontiguousarray(arr)
+        assert 0 <= offset and offset + arr.nbytes <= self.nbytes
+        _ok(hip().hipMemcpy(self.addr + offset, arr.ctypes.data, arr.nbytes, _H2D),
+            "hipMemcpy H2D")
+
     def get(self, shape, dtype=np.float32):
         out = np.empty(shape, dtype)
         assert out.nbytes <= self.nbytes
