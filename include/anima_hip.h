@@ -16,6 +16,8 @@
  *   - Host-pointer entry points (Part 1, anima_hip_attention*,
  *     anima_hip_ctx_kv_create) copy to the GPU, run, copy back and return
  *     when the output is complete.  They are serialised by a library mutex.
+ *     Copies of 4 MiB and more pass through pinned staging buffers, with
+ *     the host memcpy split over the caller and up to 3 library threads.
  *   - "_dev" entry points take device pointers and a hipStream_t (passed as
  *     void*; NULL = HIP's default stream) and are asynchronous: they only
  *     enqueue work on that stream.
