@@ -283,6 +283,9 @@ struct Runtime {
     DevBuf q, k, v, o, w0, w1, fr, q2, k2, v2, scratch;
     CallTimer timer;
     Staging staging;
+    // Second stream and events of the host SDPA's two-group pipeline.
+    hipStream_t cstream = nullptr;
+    hipEvent_t up_ev[2] = {nullptr, nullptr}, done_ev[2] = {nullptr, nullptr};
 };
 
 Runtime &rt()
@@ -308,6 +311,20 @@ bool ensure_ready(Runtime &r)
         if (!hip_ok(hipEventCreate(&e), "hipEventCreate"))
             return false;
     r.ready = true;
+    return true;
+}
+
+// The compute stream (default priority, like every stream here) and the
+// events of the host SDPA pipeline, created at its first use.
+bool ensure_pipeline(Runtime &r)
+{
+    if (r.cstream)
+        return true;
+    if (!hip_ok(hipStreamCreateWithFlags(&r.cstream, hipStreamNonBlocking), "hipStreamCreate"))
+        return false;
+    for (hipEvent_t *e : {&r.up_ev[0], &r.up_ev[1], &r.done_ev[0], &r.done_ev[1]})
+        if (!hip_ok(hipEventCreateWithFlags(e, hipEventDisableTiming), "hipEventCreate"))
+            return false;
     return true;
 }
 
@@ -419,6 +436,85 @@ bool finish_call(Runtime &r)
     return true;
 }
 
+// Kernels of the host-pointer SDPA for heads [h0, h0 + nh) of the uploaded
+// [BH, S, D] f32 workspace arrays, on stream st: the f32 flash kernel, or the
+// bf16 / f32x3 operand passes (Q and K rows, packed V^T) and their kernel.
+bool sdpa_heads(Runtime &r, int64_t h0, int nh, int S_q, int S_kv, int D, float scale, bool causal,
+                int mode, hipStream_t st)
+{
+    const bool bf16 = mode == ANIMA_HIP_BF16, x3 = mode == ANIMA_HIP_F32X3;
+    const size_t part_bytes = flash_plan(nh, S_q, S_kv, D).bytes;
+    FlashProblem p;
+    p.q = static_cast<const float *>(r.q.p) + h0 * S_q * D;
+    p.k = static_cast<const float *>(r.k.p) + h0 * S_kv * D;
+    p.v = static_cast<const float *>(r.v.p) + h0 * S_kv * D;
+    p.o = static_cast<float *>(r.o.p) + h0 * S_q * D;
+    p.qs = p.os = contiguous(nh, S_q, D);
+    p.ks = p.vs = contiguous(nh, S_kv, D);
+    p.B = 1;
+    p.H = nh;
+    p.S_q = S_q;
+    p.S_kv = S_kv;
+    p.D = D;
+    p.scale = scale;
+    p.causal = causal;
+    if (!bf16 && !x3)
+        return launch_flash_f32(p, st, r.scratch.p, part_bytes);
+    // bf16 copies of Q and K (row kernel without norm/RoPE; rows of [hi | lo]
+    // terms in the f32x3 mode) and packed V^T (hi rows, then lo rows).
+    const int64_t sp = vt_padded_len(S_kv), w = x3 ? 2 : 1;
+    RowProblem c;
+    c.x = static_cast<const float *>(p.q);
+    c.out = static_cast<uint16_t *>(r.q2.p) + h0 * S_q * D * w;
+    c.w = nullptr;
+    c.freqs = nullptr;
+    c.xs = Strides{0, int64_t(S_q) * D, int64_t(D)};
+    c.os = Strides{0, int64_t(S_q) * D * w, int64_t(D) * w};
+    c.B = 1;
+    c.S = S_q;
+    c.H = nh;
+    c.D = D;
+    c.eps = 0.0f;
+    c.norm = false;
+    c.out_bf16 = true;
+    c.lo_off = x3 ? D : 0;
+    RowProblem ck = c;
+    ck.x = static_cast<const float *>(p.k);
+    ck.out = static_cast<uint16_t *>(r.k2.p) + h0 * S_kv * D * w;
+    ck.xs = Strides{0, int64_t(S_kv) * D, int64_t(D)};
+    ck.os = Strides{0, int64_t(S_kv) * D * w, int64_t(D) * w};
+    ck.S = S_kv;
+    const Strides vts{0, w * D * sp, sp};
+    const float *vf = static_cast<const float *>(p.v);
+    uint16_t *vt = static_cast<uint16_t *>(r.v2.p) + h0 * w * D * sp;
+    if (!launch_rows(c, st) || !launch_rows(ck, st) ||
+        !(x3 ? launch_vt_pack_terms(vf, p.vs, vt, vts, 1, nh, S_kv, D, st)
+             : launch_vt_pack(vf, p.vs, vt, vts, 1, nh, S_kv, D, st)))
+        return false;
+    p.q = c.out;
+    p.k = ck.out;
+    p.v = vt;
+    p.qs = c.os;
+    p.ks = ck.os;
+    p.vs = vts;
+    return x3 ? launch_flash_x3(p, st, r.scratch.p, part_bytes)
+              : launch_flash_bf16(p, st, r.scratch.p, part_bytes);
+}
+
+// Head groups of a host-pointer SDPA.  Two when the copies are large and
+// half the heads still fill the GPU (flash_plan keeps 8-wave workgroups and
+// no key split): the second half's upload then overlaps the first half's
+// kernels on the runtime's compute stream, and the first half's output comes
+// back while the second half computes.
+int sdpa_groups(int BH, int S_q, int S_kv, int D)
+{
+    const int64_t bytes = int64_t(BH) * (2 * int64_t(S_q) + 2 * int64_t(S_kv)) * D * 4;
+    if (BH < 2 || BH % 2 != 0 || bytes < (int64_t(64) << 20))
+        return 1;
+    const FlashPlan half = flash_plan(BH / 2, S_q, S_kv, D);
+    return half.waves == 8 && half.splits == 1 ? 2 : 1;
+}
+
 // Shared body of the host-pointer SDPA entries ([BH, S, D] f32 host arrays).
 bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int BH, int S_q,
                int S_kv, int D, float scale, bool causal, int mode)
@@ -436,79 +532,41 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
     Runtime &r = rt();
     const hipStream_t st = r.stream;
     begin_call(r);
+    const int G = sdpa_groups(BH, S_q, S_kv, D), nh = BH / G;
     if (!r.q.reserve(f32_bytes(nq), "workspace Q") || !r.o.reserve(f32_bytes(nq), "workspace O") ||
-        !r.k.reserve(f32_bytes(nk), "workspace K") || !r.v.reserve(f32_bytes(nk), "workspace V"))
+        !r.k.reserve(f32_bytes(nk), "workspace K") || !r.v.reserve(f32_bytes(nk), "workspace V") ||
+        !r.scratch.reserve(flash_plan(nh, S_q, S_kv, D).bytes, "workspace split-KV partials"))
         return false;
-    if (!h2d(r.q.p, Q, f32_bytes(nq), st) || !h2d(r.k.p, K, f32_bytes(nk), st) ||
-        !h2d(r.v.p, V, f32_bytes(nk), st))
-        return false;
-    const size_t part_bytes = flash_plan(BH, S_q, S_kv, D).bytes;
-    if (!r.scratch.reserve(part_bytes, "workspace split-KV partials"))
-        return false;
-    FlashProblem p;
-    p.q = r.q.p;
-    p.k = r.k.p;
-    p.v = r.v.p;
-    p.o = static_cast<float *>(r.o.p);
-    p.qs = p.os = contiguous(BH, S_q, D);
-    p.ks = p.vs = contiguous(BH, S_kv, D);
-    p.B = 1;
-    p.H = BH;
-    p.S_q = S_q;
-    p.S_kv = S_kv;
-    p.D = D;
-    p.scale = scale;
-    p.causal = causal;
     if (bf16 || x3) {
-        // bf16 copies of Q and K (row kernel without norm/RoPE; rows of [hi |
-        // lo] terms in the f32x3 mode) and packed V^T (hi rows, then lo rows).
-        const int64_t sp = vt_padded_len(S_kv), w = x3 ? 2 : 1;
+        const int64_t w = x3 ? 2 : 1;
         if (!r.q2.reserve(nq * 2 * w, "workspace q bf16") ||
             !r.k2.reserve(nk * 2 * w, "workspace k bf16") ||
-            !r.v2.reserve(size_t(BH) * w * D * sp * 2, "workspace v^T"))
+            !r.v2.reserve(size_t(BH) * w * D * vt_padded_len(S_kv) * 2, "workspace v^T"))
             return false;
-        RowProblem c;
-        c.x = static_cast<const float *>(r.q.p);
-        c.out = r.q2.p;
-        c.w = nullptr;
-        c.freqs = nullptr;
-        c.xs = Strides{0, int64_t(S_q) * D, int64_t(D)};
-        c.os = Strides{0, int64_t(S_q) * D * w, int64_t(D) * w};
-        c.B = 1;
-        c.S = S_q;
-        c.H = BH;
-        c.D = D;
-        c.eps = 0.0f;
-        c.norm = false;
-        c.out_bf16 = true;
-        c.lo_off = x3 ? D : 0;
-        RowProblem ck = c;
-        ck.x = static_cast<const float *>(r.k.p);
-        ck.out = r.k2.p;
-        ck.xs = Strides{0, int64_t(S_kv) * D, int64_t(D)};
-        ck.os = Strides{0, int64_t(S_kv) * D * w, int64_t(D) * w};
-        ck.S = S_kv;
-        const Strides vts{0, w * D * sp, sp};
-        const float *vf = static_cast<const float *>(r.v.p);
-        uint16_t *vt = static_cast<uint16_t *>(r.v2.p);
-        if (!launch_rows(c, st) || !launch_rows(ck, st) ||
-            !(x3 ? launch_vt_pack_terms(vf, p.vs, vt, vts, 1, BH, S_kv, D, st)
-                 : launch_vt_pack(vf, p.vs, vt, vts, 1, BH, S_kv, D, st)))
-            return false;
-        p.q = r.q2.p;
-        p.k = r.k2.p;
-        p.v = r.v2.p;
-        p.qs = c.os;
-        p.ks = ck.os;
-        p.vs = vts;
-        if (!(x3 ? launch_flash_x3(p, st, r.scratch.p, part_bytes)
-                 : launch_flash_bf16(p, st, r.scratch.p, part_bytes)))
-            return false;
-    } else if (!launch_flash_f32(p, st, r.scratch.p, part_bytes)) {
-        return false;
     }
-    if (!d2h(out, r.o.p, f32_bytes(nq), st))
+    if (G > 1 && !ensure_pipeline(r))
         return false;
+    const hipStream_t cs = G > 1 ? r.cstream : st;
+    const int64_t gq = int64_t(nh) * S_q * D, gk = int64_t(nh) * S_kv * D;  // elements per group
+    for (int g = 0; g < G; ++g) {
+        if (!h2d(static_cast<float *>(r.q.p) + g * gq, Q + g * gq, f32_bytes(gq), st) ||
+            !h2d(static_cast<float *>(r.k.p) + g * gk, K + g * gk, f32_bytes(gk), st) ||
+            !h2d(static_cast<float *>(r.v.p) + g * gk, V + g * gk, f32_bytes(gk), st))
+            return false;
+        if (G > 1 && !(hip_ok(hipEventRecord(r.up_ev[g], st), "hipEventRecord") &&
+                       hip_ok(hipStreamWaitEvent(cs, r.up_ev[g], 0), "hipStreamWaitEvent")))
+            return false;
+        if (!sdpa_heads(r, int64_t(g) * nh, nh, S_q, S_kv, D, scale, causal, mode, cs))
+            return false;
+        if (G > 1 && !hip_ok(hipEventRecord(r.done_ev[g], cs), "hipEventRecord"))
+            return false;
+    }
+    for (int g = 0; g < G; ++g) {
+        if (G > 1 && !hip_ok(hipStreamWaitEvent(st, r.done_ev[g], 0), "hipStreamWaitEvent"))
+            return false;
+        if (!d2h(out + g * gq, static_cast<float *>(r.o.p) + g * gq, f32_bytes(gq), st))
+            return false;
+    }
     return finish_call(r);
 }
 
@@ -618,9 +676,17 @@ void anima_rt_destroy(void)
     for (DevBuf *b : {&r.q, &r.k, &r.v, &r.o, &r.w0, &r.w1, &r.fr, &r.q2, &r.k2, &r.v2, &r.scratch})
         b->release();
     r.staging.release();
-    for (hipEvent_t &e : r.timer.ev) {
-        (void)hipEventDestroy(e);
-        e = nullptr;
+    if (r.cstream)
+        (void)hipStreamSynchronize(r.cstream);
+    for (hipEvent_t *e : {&r.timer.ev[0], &r.timer.ev[1], &r.timer.ev[2], &r.timer.ev[3],
+                          &r.up_ev[0], &r.up_ev[1], &r.done_ev[0], &r.done_ev[1]}) {
+        if (*e)
+            (void)hipEventDestroy(*e);
+        *e = nullptr;
+    }
+    if (r.cstream) {
+        (void)hipStreamDestroy(r.cstream);
+        r.cstream = nullptr;
     }
     (void)hipStreamDestroy(r.stream);
     r.stream = nullptr;
