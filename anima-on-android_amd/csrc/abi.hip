@@ -1149,32 +1149,62 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
         return fail("anima_hip_attention: null pointer");
     const hipStream_t st = r.stream;
     begin_call(r);
-    const size_t scratch = attention_scratch_bytes(B, S_q, B, S_kv, H, D, am, false);
+    // Two batch groups, like the SDPA's head groups, when the copies are
+    // large and half the batch still fills the GPU: the second half's upload
+    // overlaps the first half's kernels.
+    const int64_t bytes = 2 * f32_bytes(nq) + 2 * f32_bytes(nk);
+    const FlashPlan half = flash_plan(int64_t(B / 2) * H, S_q, S_kv, D);
+    const int G = B % 2 == 0 && bytes >= (int64_t(64) << 20) && half.waves == 8 &&
+                          half.splits == 1
+                      ? 2
+                      : 1;
+    const int Bg = B / G;
+    const size_t scratch = attention_scratch_bytes(Bg, S_q, Bg, S_kv, H, D, am, false);
     if (!r.q.reserve(f32_bytes(nq), "workspace q") || !r.k.reserve(f32_bytes(nk), "workspace k") ||
         !r.v.reserve(f32_bytes(nk), "workspace v") || !r.o.reserve(f32_bytes(nq), "workspace o") ||
         !r.scratch.reserve(scratch, "workspace scratch"))
         return false;
+    if (G > 1 && !ensure_pipeline(r))
+        return false;
+    const hipStream_t cs = G > 1 ? r.cstream : st;
     AttnInputs in;
-    if (!h2d(r.q.p, q, f32_bytes(nq), st) || !h2d(r.k.p, k, f32_bytes(nk), st) ||
-        !h2d(r.v.p, v, f32_bytes(nk), st) ||
-        !upload_optional(r.w0, q_norm_w, D, "workspace q_norm", st, in.q_norm_w) ||
+    if (!upload_optional(r.w0, q_norm_w, D, "workspace q_norm", st, in.q_norm_w) ||
         !upload_optional(r.w1, k_norm_w, D, "workspace k_norm", st, in.k_norm_w) ||
         !upload_optional(r.fr, freqs, size_t(S_q) * D * 2, "workspace freqs", st, in.freqs))
         return false;
-    in.q = static_cast<const float *>(r.q.p);
-    in.k = static_cast<const float *>(r.k.p);
-    in.v = static_cast<const float *>(r.v.p);
-    in.out = static_cast<float *>(r.o.p);
-    in.B = B;
-    in.Bk = B;
+    in.B = Bg;
+    in.Bk = Bg;
     in.S_q = S_q;
     in.S_kv = S_kv;
     in.H = H;
     in.D = D;
     in.eps = eps;
     in.mode = am;
-    if (!run_attention(in, r.scratch.p, st) || !d2h(out, r.o.p, f32_bytes(nq), st))
-        return false;
+    const int64_t gq = nq / G, gk = nk / G;  // elements per group
+    for (int g = 0; g < G; ++g) {
+        float *qd = static_cast<float *>(r.q.p) + g * gq, *kd = static_cast<float *>(r.k.p) + g * gk;
+        float *vd = static_cast<float *>(r.v.p) + g * gk;
+        if (!h2d(qd, q + g * gq, f32_bytes(gq), st) || !h2d(kd, k + g * gk, f32_bytes(gk), st) ||
+            !h2d(vd, v + g * gk, f32_bytes(gk), st))
+            return false;
+        if (G > 1 && !(hip_ok(hipEventRecord(r.up_ev[g], st), "hipEventRecord") &&
+                       hip_ok(hipStreamWaitEvent(cs, r.up_ev[g], 0), "hipStreamWaitEvent")))
+            return false;
+        in.q = qd;
+        in.k = kd;
+        in.v = vd;
+        in.out = static_cast<float *>(r.o.p) + g * gq;
+        if (!run_attention(in, r.scratch.p, cs))
+            return false;
+        if (G > 1 && !hip_ok(hipEventRecord(r.done_ev[g], cs), "hipEventRecord"))
+            return false;
+    }
+    for (int g = 0; g < G; ++g) {
+        if (G > 1 && !hip_ok(hipStreamWaitEvent(st, r.done_ev[g], 0), "hipStreamWaitEvent"))
+            return false;
+        if (!d2h(out + g * gq, static_cast<float *>(r.o.p) + g * gq, f32_bytes(gq), st))
+            return false;
+    }
     return finish_call(r);
 }
 
