@@ -328,6 +328,22 @@ bool ensure_pipeline(Runtime &r)
     return true;
 }
 
+// Drains both runtime streams when a host-pointer call returns early after
+// enqueuing work, so that no kernel of a failed call still reads or writes
+// the shared workspace when the next call uploads into it.
+struct DrainOnError {
+    Runtime &r;
+    bool done = false;
+    ~DrainOnError()
+    {
+        if (done || !r.stream)
+            return;
+        (void)hipStreamSynchronize(r.stream);
+        if (r.cstream)
+            (void)hipStreamSynchronize(r.cstream);
+    }
+};
+
 // Context check for the device-pointer entries: the mutex is held only to
 // create the context once, never across the launches themselves.
 bool ready_for_device_call()
@@ -547,6 +563,7 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
     if (G > 1 && !ensure_pipeline(r))
         return false;
     const hipStream_t cs = G > 1 ? r.cstream : st;
+    DrainOnError drain{r};
     const int64_t gq = int64_t(nh) * S_q * D, gk = int64_t(nh) * S_kv * D;  // elements per group
     for (int g = 0; g < G; ++g) {
         if (!h2d(static_cast<float *>(r.q.p) + g * gq, Q + g * gq, f32_bytes(gq), st) ||
@@ -567,6 +584,7 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
         if (!d2h(out + g * gq, static_cast<float *>(r.o.p) + g * gq, f32_bytes(gq), st))
             return false;
     }
+    drain.done = true;
     return finish_call(r);
 }
 
@@ -1167,6 +1185,7 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
     if (G > 1 && !ensure_pipeline(r))
         return false;
     const hipStream_t cs = G > 1 ? r.cstream : st;
+    DrainOnError drain{r};
     AttnInputs in;
     if (!upload_optional(r.w0, q_norm_w, D, "workspace q_norm", st, in.q_norm_w) ||
         !upload_optional(r.w1, k_norm_w, D, "workspace k_norm", st, in.k_norm_w) ||
@@ -1205,6 +1224,7 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
         if (!d2h(out + g * gq, static_cast<float *>(r.o.p) + g * gq, f32_bytes(gq), st))
             return false;
     }
+    drain.done = true;
     return finish_call(r);
 }
 
