@@ -276,6 +276,10 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
         // (registers 2q, 2q+1 of those 8), into ph/pl; the row sums add the
         // terms.
         bf16x8 ph[2], pl[2];
+        // This tile's row sums start from zero and join l, l2 once per tile:
+        // over millions of keys a running sum fed one pair at a time rounds
+        // away its smallest terms.
+        float t = 0.0f, t2 = 0.0f;
         auto p_pair = [&](int i, int q) {
             const f32x16 &s = i < 2 ? s0 : s1;
             const int r = 8 * (i & 1) + 2 * q;
@@ -288,8 +292,8 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
             ph[i & 1][2 * q + 1] = hi[1];
             pl[i & 1][2 * q] = lo[0];
             pl[i & 1][2 * q + 1] = lo[1];
-            l = __builtin_amdgcn_fdot2_f32_bf16(hi, one, l, false);
-            l2 = __builtin_amdgcn_fdot2_f32_bf16(lo, one, l2, false);
+            t = __builtin_amdgcn_fdot2_f32_bf16(hi, one, t, false);
+            t2 = __builtin_amdgcn_fdot2_f32_bf16(lo, one, t2, false);
         };
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -314,6 +318,9 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+
+        l += t;
+        l2 += t2;
 
         // Tile j+1's copies (this iteration's) complete, then visible to all.
         wait_vmcnt<0>();
