@@ -294,12 +294,12 @@ def other_configs(c, cpu_rate):
         res = {}
         run, fl = self_attention_timer(c, mode, 1, 256, (16, 16), 101)
         ms = c.time(run, 50, 5)
-        res["c1_self256_B1"] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 2)}
+        res["self256_B1"] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 2)}
 
         cache = context_cache(c, mode, 1, 202)
         run, fl = cross_attention_timer(c, mode, cache, 2, 256, 203)
         ms = c.time(run, 50, 5)
-        res["c2_cross256x512_B2_cached"] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 2)}
+        res["cross256x512_B2_cached"] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 2)}
         cache.close()
 
         run_s, fl_s = self_attention_timer(c, mode, 2, 6144, (96, 64), 501)
@@ -307,24 +307,24 @@ def other_configs(c, cpu_rate):
         run_x, fl_x = cross_attention_timer(c, mode, cache, 2, 6144, 503)
         ms_s = c.time(run_s, 10, 2)
         ms_x = c.time(run_x, 10, 2)
-        res["c5_self6144_96x64_B2"] = {"ms": round(ms_s, 4), "tflops": round(fl_s / ms_s / 1e9, 2)}
-        res["c5_cross6144x512_B2"] = {"ms": round(ms_x, 4), "tflops": round(fl_x / ms_x / 1e9, 2)}
+        res["self6144_96x64_B2"] = {"ms": round(ms_s, 4), "tflops": round(fl_s / ms_s / 1e9, 2)}
+        res["cross6144x512_B2"] = {"ms": round(ms_x, 4), "tflops": round(fl_x / ms_x / 1e9, 2)}
         cache.close()
         c.torch.cuda.empty_cache()
 
-        # Config 3 at one GPU's share of a 2-GPU split (design only beyond
-        # one GPU): one CFG branch (B=1) or half the heads (H=8), the whole
-        # attention call (prologues, V^T pack, flash).
-        for key, b_, h_ in (("c3_share_cfg_split_B1", 1, 16), ("c3_share_head_split_H8", 2, 8)):
+        # The 4096-token self-attention at one GPU's share of a 2-GPU split
+        # (design only beyond one GPU): one CFG branch (B=1) or half the heads
+        # (H=8), the whole attention call (prologues, V^T pack, flash).
+        for key, b_, h_ in (("self4096_share_cfg_split_B1", 1, 16), ("self4096_share_head_split_H8", 2, 8)):
             run, fl = self_attention_timer(c, mode, b_, 4096, (64, 64), 301, H=h_)
             ms = c.time(run, 10, 2)
             res[key] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 2)}
         c.torch.cuda.empty_cache()
 
-        res["c4_denoise_step_28_blocks"] = denoise_step(c, mode)
+        res["denoise_step_28_blocks"] = denoise_step(c, mode)
         res["proj_gemm_8192x2048x2048"] = projection_gemm(c, mode)
-        res["c4_denoise_step_28_blocks_attention_sublayers"] = denoise_step_blocks(c, mode)
-        res["c4_sampler_step_full_dit"] = sampler_step(c, mode)
+        res["denoise_step_28_blocks_attention_sublayers"] = denoise_step_blocks(c, mode)
+        res["sampler_step_full_dit"] = sampler_step(c, mode)
         out[variant] = res
         log(f"[bench] configs {variant}: " + json.dumps(res))
     if cpu_rate:
@@ -640,7 +640,7 @@ def main():
 
     if args.sampler_step:
         res = {v: sampler_step(c, MODE[v]) for v in ("bf16", "f32x3", "f32")}
-        print(json.dumps({"config": "c4_sampler_step_full_dit", "latent": [1, 16, 128, 128],
+        print(json.dumps({"config": "sampler_step_full_dit", "latent": [1, 16, 128, 128],
                           "results": res}), flush=True)
         return
 

@@ -64,7 +64,7 @@ def test_bf16_rejects_other_head_dims():
         rt.sdpa(q, q, q, mode=rt.BF16)
 
 
-def test_bf16_config1_and_fp64():
+def test_bf16_self_attention_256_and_fp64():
     rng = np.random.default_rng(1001)
     B, S, H, D = 1, 256, 16, 128
     q, k, v = randn(rng, B, S, H, D), randn(rng, B, S, H, D), randn(rng, B, S, H, D)
@@ -73,11 +73,11 @@ def test_bf16_config1_and_fp64():
     out = rt.attention(q, k, v, ones, ones, f, mode=rt.BF16)
     ref = oracle.attention_dataflow(q, k, v, ones, ones, f)
     err = rel_err(out, ref)
-    print(f"bf16 config1 rel err {err:.3e}", flush=True)
+    print(f"bf16 256 tokens rel err {err:.3e}", flush=True)
     assert err <= REL
 
 
-def test_bf16_config3_full_size_sampled_heads():
+def test_bf16_self_attention_4096_sampled_heads():
     """B=2, H=16, S=4096: full problem on the GPU, two slices vs the oracle."""
     rng = np.random.default_rng(3003)
     B, S, H, D = 2, 4096, 16, 128
@@ -90,7 +90,7 @@ def test_bf16_config3_full_size_sampled_heads():
         ref = oracle.attention_dataflow(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, h:h + 1],
                                         v[b:b + 1, :, h:h + 1], ones, ones, f)
         err = rel_err(out[b, :, h], ref[0, :, 0])
-        print(f"bf16 config3 b={b} h={h} rel err {err:.3e}", flush=True)
+        print(f"bf16 4096 tokens b={b} h={h} rel err {err:.3e}", flush=True)
         assert err <= REL
 
 

@@ -49,7 +49,7 @@ def test_gemm_bf16_golden_and_shapes():
                                atol=2e-5)
 
 
-def _config2(seed=2002, Bc=1):
+def _cross_256x512(seed=2002, Bc=1):
     """B=2 CFG, Sq=256 latent tokens, Sk=512 context tokens, 16 heads x 128.
     x ~ N(0,1) [2,256,2048]; ctx ~ N(0,0.5) [Bc,512,1024]; Wq/Wk/Wv bf16 ~ N(0,0.02)."""
     rng = np.random.default_rng(seed)
@@ -62,8 +62,8 @@ def _config2(seed=2002, Bc=1):
 
 
 @pytest.mark.parametrize("Bc", [1, 2])
-def test_config2_cross_attention_cached_kv(Bc):
-    x, ctx, wq, wk, wv = _config2(Bc=Bc)
+def test_cross_attention_256x512_cached_kv(Bc):
+    x, ctx, wq, wk, wv = _cross_256x512(Bc=Bc)
     ones = np.ones(128, np.float32)
     # Oracle: projections with anima_rt's bf16 GEMM, then NumpyAttention's
     # norm -> SDPA dataflow (no RoPE for cross-attention).
@@ -81,7 +81,7 @@ def test_config2_cross_attention_cached_kv(Bc):
     try:
         out = cache.attend(q, ones)
         err = float(np.abs(out - ref).max())
-        print(f"config2 Bc={Bc} f32 max_abs={err:.3e}", flush=True)
+        print(f"cross 256x512 Bc={Bc} f32 max_abs={err:.3e}", flush=True)
         assert err <= TOL
         # The cache is reused: a second call (next denoise step) is identical.
         np.testing.assert_array_equal(cache.attend(q, ones), out)
@@ -92,7 +92,7 @@ def test_config2_cross_attention_cached_kv(Bc):
     try:
         out = cache.attend(q, ones)
         err = rel_err(out, ref)
-        print(f"config2 Bc={Bc} bf16 rel={err:.3e}", flush=True)
+        print(f"cross 256x512 Bc={Bc} bf16 rel={err:.3e}", flush=True)
         assert err <= REL
     finally:
         cache.close()
@@ -101,7 +101,7 @@ def test_config2_cross_attention_cached_kv(Bc):
     try:
         out = cache.attend(q, ones)
         err = float(np.abs(out - ref).max())
-        print(f"config2 Bc={Bc} f32x3 max_abs={err:.3e}", flush=True)
+        print(f"cross 256x512 Bc={Bc} f32x3 max_abs={err:.3e}", flush=True)
         assert err <= TOL
     finally:
         cache.close()
@@ -124,7 +124,7 @@ def test_cross_attention_errors():
             rt.ContextKV(ctx, w, w, None, heads=2, head_dim=64, mode=mode)
 
 
-def test_config5_rectangular_6144_sampled_heads():
+def test_rectangular_96x64_grid_6144_tokens_sampled_heads():
     """B=2, H=16, S=6144 (96x64 grid, rectangular RoPE) self-attention and
     cross-attention 6144x512; two (batch, head) slices of each vs the oracle."""
     rng = np.random.default_rng(5005)
@@ -139,7 +139,7 @@ def test_config5_rectangular_6144_sampled_heads():
         for b, h in [(0, 7), (1, 2)]:
             ref = oracle.attention_dataflow(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, h:h + 1],
                                             v[b:b + 1, :, h:h + 1], ones, ones, f)
-            print(f"config5 self mode={mode} b={b} h={h} "
+            print(f"6144 tokens self mode={mode} b={b} h={h} "
                   f"max_abs={np.abs(out[b, :, h] - ref[0, :, 0]).max():.3e}", flush=True)
             assert check(out[b, :, h], ref[0, :, 0])
     # cross 6144 x 512 (no RoPE), K/V [B, 512, H, D]
@@ -151,5 +151,5 @@ def test_config5_rectangular_6144_sampled_heads():
                                         vc[b:b + 1, :, h:h + 1], ones, ones, None)
         for mode, out in outs.items():
             err = float(np.abs(out[b, :, h] - ref[0, :, 0]).max())
-            print(f"config5 cross mode={mode} b={b} h={h} max_abs={err:.3e}", flush=True)
+            print(f"6144 tokens cross mode={mode} b={b} h={h} max_abs={err:.3e}", flush=True)
             assert err <= TOL

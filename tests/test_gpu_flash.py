@@ -101,7 +101,7 @@ def test_flash_generic_head_dims(d):
     assert np.abs(out - ref).max() <= TOL
 
 
-def test_config1_self_attention_256():
+def test_self_attention_256_tokens():
     """B=1, H=16, S=256 (16x16 grid), N(0,1) q/k/v, RMSNorm(w=1) + RoPE."""
     rng = np.random.default_rng(1001)
     B, S, H, D = 1, 256, 16, 128
@@ -135,7 +135,7 @@ def test_attention_prologue_bit_exact_pieces():
     np.testing.assert_array_equal(r.run_rope(xn, f), oracle.numpy_rope(xn, f))
 
 
-def test_config3_full_size_sampled_heads():
+def test_self_attention_4096_tokens_sampled_heads():
     """B=2, H=16, S=4096 (64x64 grid): the whole problem runs on the GPU; two
     of the 32 independent (batch, head) slices are checked against the oracle
     and all outputs are finite and within the per-dim range of V."""
@@ -153,7 +153,7 @@ def test_config3_full_size_sampled_heads():
                                         v[b:b + 1, :, h:h + 1], ones, ones, f,
                                         sdpa=lambda a, bb, c: oracle.flash_sdpa(a, bb, c))
         err = np.abs(out[b, :, h] - ref[0, :, 0]).max()
-        print(f"config3 head b={b} h={h} max_abs={err:.3e}", flush=True)
+        print(f"4096 tokens head b={b} h={h} max_abs={err:.3e}", flush=True)
         assert err <= TOL
 
 

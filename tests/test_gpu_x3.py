@@ -72,7 +72,7 @@ def test_x3_rejects_other_head_dims():
         rt.sdpa(q, q, q, mode=rt.F32X3)
 
 
-def test_x3_config1_against_reference_and_fp64():
+def test_x3_self_attention_256_against_reference_and_fp64():
     """B=1, H=16, S=256, N(0,1) q/k/v after RMSNorm(w=1) + RoPE (16x16 grid)."""
     rng = np.random.default_rng(1001)
     B, S, H, D = 1, 256, 16, 128
@@ -83,8 +83,8 @@ def test_x3_config1_against_reference_and_fp64():
     kn = oracle.numpy_rope(oracle.rmsnorm(k, ones), f).transpose(0, 2, 1, 3).reshape(H, S, D)
     vt = v.transpose(0, 2, 1, 3).reshape(H, S, D)
     out = rt.sdpa(qn, kn, vt, mode=rt.F32X3)
-    check(out, oracle.flash_sdpa(qn, kn, vt), "config1 vs reference")
-    check(out, oracle.sdpa_fp64(qn, kn, vt), "config1 vs fp64")
+    check(out, oracle.flash_sdpa(qn, kn, vt), "256 tokens vs reference")
+    check(out, oracle.sdpa_fp64(qn, kn, vt), "256 tokens vs fp64")
 
 
 def test_x3_error_scales_with_v():
@@ -175,7 +175,7 @@ def test_x3_deterministic():
     np.testing.assert_array_equal(a, rt.sdpa(q, k, v, mode=rt.F32X3))
 
 
-def test_x3_attention_core_config1_and_config3_sampled_heads():
+def test_x3_attention_core_256_and_4096_tokens_sampled_heads():
     """The fused attention core (anima_hip_attention: RMSNorm + RoPE prologue
     writing term rows, term V^T pack, f32x3 flash) at 256 tokens and at the
     4096-token, B=2, H=16 workload; two (batch, head) slices of the latter
@@ -185,7 +185,7 @@ def test_x3_attention_core_config1_and_config3_sampled_heads():
     q, k, v = randn(rng, 1, 256, 16, 128), randn(rng, 1, 256, 16, 128), randn(rng, 1, 256, 16, 128)
     f = generate_rope_freqs(16, 16)
     out = rt.attention(q, k, v, ones, ones, f, mode=rt.F32X3)
-    check(out, oracle.attention_dataflow(q, k, v, ones, ones, f), "attention config1")
+    check(out, oracle.attention_dataflow(q, k, v, ones, ones, f), "attention 256 tokens")
 
     rng = np.random.default_rng(3003)
     B, S, H, D = 2, 4096, 16, 128
@@ -196,4 +196,4 @@ def test_x3_attention_core_config1_and_config3_sampled_heads():
     for b, h in [(0, 3), (1, 14)]:
         ref = oracle.attention_dataflow(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, h:h + 1],
                                         v[b:b + 1, :, h:h + 1], ones, ones, f)
-        check(out[b, :, h], ref[0, :, 0], f"config3 b={b} h={h}")
+        check(out[b, :, h], ref[0, :, 0], f"4096 tokens b={b} h={h}")
