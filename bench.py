@@ -78,6 +78,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true",
                     help="skip the other variant and the extra configurations")
+    ap.add_argument("--sampler-latent", type=int, default=128,
+                    help="latent height = width of --sampler-step (128: 1024x1024 output, "
+                         "32: 256x256)")
     ap.add_argument("--sampler-step", action="store_true",
                     help="only the whole-DiT Euler/CFG sampler step at 1024x1024, both modes; "
                          "prints one JSON line of its own")
@@ -639,8 +642,9 @@ def main():
     c = Ctx(torch, lib, _lib)
 
     if args.sampler_step:
-        res = {v: sampler_step(c, MODE[v]) for v in ("bf16", "f32x3", "f32")}
-        print(json.dumps({"config": "sampler_step_full_dit", "latent": [1, 16, 128, 128],
+        n = args.sampler_latent
+        res = {v: sampler_step(c, MODE[v], H=n, W=n) for v in ("bf16", "f32x3", "f32")}
+        print(json.dumps({"config": "sampler_step_full_dit", "latent": [1, 16, n, n],
                           "results": res}), flush=True)
         return
 
