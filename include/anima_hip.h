@@ -231,6 +231,25 @@ bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
                              float *out, void *scratch, size_t scratch_bytes, int B, int S_q,
                              int Bk, int S_kv, int H, int D, float eps, int mode, void *stream);
 
+/* anima_hip_attention_dev without scratch and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc).  Same arguments, kernels and results as
+ * anima_hip_attention_dev; the scratch is a static device array of
+ * ANIMA_HIP_STATIC_SCRATCH_BYTES that each GPU holds from the first call
+ * made on it until the process ends.  A problem whose
+ * anima_hip_attention_scratch_bytes() exceeds that size is rejected (false,
+ * with a message) before anything is enqueued; 192 MiB covers the
+ * 1024x1024 image's self-attention (B = 2, 4096 tokens, 16 x 128) in every
+ * mode.  Every call on one GPU shares its array, so calls that overlap on
+ * one GPU (other streams or threads) race: the caller serialises them.
+ * Asynchronous on `stream`. */
+#define ANIMA_HIP_STATIC_SCRATCH_BYTES (192u * 1024u * 1024u)
+bool anima_hip_attention_static_dev(const float *q, const float *k, const float *v,
+                                    const float *q_norm_w, const float *k_norm_w,
+                                    const float *freqs, float *out, int B, int S_q, int Bk,
+                                    int S_kv, int H, int D, float eps, int mode, void *stream);
+
 /* One-call core of NumpyAttention.forward (numpy_dit.py:283-294) on host
  * memory: q [B,S_q,H,D], k/v [B,S_kv,H,D] (the projections), optional
  * per-head RMSNorm weights [D], optional RoPE table [S_q, D/2, 2, 2]

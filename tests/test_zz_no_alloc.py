@@ -1,0 +1,121 @@
+"""anima_hip_attention_static_dev, the attention core whose scratch is a
+static device array (the entry for callers that cannot allocate), against
+anima_hip_attention_dev with caller scratch on the same inputs.
+
+The two entries run the same kernels on the same inputs, so their outputs
+must agree bit for bit: on two calls in a row, the second one smaller (so it
+reuses scratch that the first call left filled), in every arithmetic mode.
+The smaller call also goes through split-KV partials, which live in the
+static array too, and is held to the oracle's tolerance (max-abs 1e-4 for
+the f32 and f32x3 modes, normwise 2e-2 for bf16).  A problem beyond the
+static size is refused with a message before anything is launched.
+"""
+import ctypes as ct
+
+import numpy as np
+import pytest
+
+import oracle
+from anima_hip import _lib, rt
+from anima_hip.rope import generate_rope_freqs
+
+pytestmark = pytest.mark.gpu
+
+H, D = 16, 128
+STATIC_BYTES = 192 * 1024 * 1024
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    rt.init()
+
+
+def _case(seed, B, S_q, Bk, S_kv, grid):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, S_q, H, D), dtype=np.float32)
+    k = rng.standard_normal((Bk, S_kv, H, D), dtype=np.float32)
+    v = rng.standard_normal((Bk, S_kv, H, D), dtype=np.float32)
+    qw, kw = (rng.uniform(0.5, 1.5, D).astype(np.float32) for _ in range(2))
+    freqs = generate_rope_freqs(*grid) if grid else None
+    return q, k, v, qw, kw, freqs
+
+
+class _Dev:
+    """Device copies of one case's inputs plus an output buffer."""
+
+    def __init__(self, q, k, v, qw, kw, freqs):
+        from devmem import DevBuf
+        self.q, self.k, self.v = DevBuf.of(q), DevBuf.of(k), DevBuf.of(v)
+        self.qw, self.kw = DevBuf.of(qw), DevBuf.of(kw)
+        self.fr = DevBuf.of(freqs) if freqs is not None else None
+        self.out = DevBuf.of(np.full(q.shape, np.nan, np.float32))
+        self.shape = q.shape
+
+    def args(self):
+        return (self.q.addr, self.k.addr, self.v.addr, self.qw.addr, self.kw.addr,
+                self.fr.addr if self.fr else None, self.out.addr)
+
+
+def _with_scratch(dev, B, S_q, Bk, S_kv, mode):
+    from devmem import DevBuf
+    lib = _lib.load()
+    n = lib.anima_hip_attention_scratch_bytes(B, S_q, Bk, S_kv, H, D, mode)
+    scratch = DevBuf(n)
+    print(f"  attention_dev B={B} S_q={S_q} Bk={Bk} S_kv={S_kv} mode={mode} scratch={n}",
+          flush=True)
+    q, k, v, qw, kw, fr, out = dev.args()
+    ok = lib.anima_hip_attention_dev(q, k, v, qw, kw, fr, out, scratch.addr, n, B, S_q, Bk,
+                                     S_kv, H, D, ct.c_float(1e-6), mode, None)
+    _lib.check(ok, "attention_dev")
+    res = dev.out.get(dev.shape)
+    scratch.close()
+    return res, n
+
+
+def _static(dev, B, S_q, Bk, S_kv, mode):
+    lib = _lib.load()
+    print(f"  attention_static_dev B={B} S_q={S_q} Bk={Bk} S_kv={S_kv} mode={mode}", flush=True)
+    q, k, v, qw, kw, fr, out = dev.args()
+    ok = lib.anima_hip_attention_static_dev(q, k, v, qw, kw, fr, out, B, S_q, Bk, S_kv, H, D,
+                                            ct.c_float(1e-6), mode, None)
+    _lib.check(ok, "attention_static_dev")
+    return dev.out.get(dev.shape)
+
+
+@pytest.mark.parametrize("mode", [rt.F32, rt.F32X3, rt.BF16])
+def test_static_scratch_matches_caller_scratch(mode):
+    # Call 1: self-attention, B=2, 1024 tokens (32 x 32 RoPE grid), 8-wave
+    # grid.  Call 2: one batch entry of 256 query tokens against 512 keys
+    # (no RoPE), which splits the key range through scratch partials.
+    calls = [(2, 1024, 2, 1024, (32, 32)), (1, 256, 1, 512, None)]
+    for i, (B, S_q, Bk, S_kv, grid) in enumerate(calls):
+        q, k, v, qw, kw, freqs = _case(7000 + 10 * i + mode, B, S_q, Bk, S_kv, grid)
+        dev = _Dev(q, k, v, qw, kw, freqs)
+        ref, n = _with_scratch(dev, B, S_q, Bk, S_kv, mode)
+        assert 0 < n <= STATIC_BYTES
+        out = _static(dev, B, S_q, Bk, S_kv, mode)
+        assert np.isfinite(out).all()
+        assert np.array_equal(out, ref), f"call {i}: static scratch differs from caller scratch"
+        if i == 1:
+            orc = oracle.attention_dataflow(q, k, v, qw, kw, None)
+            err = float(np.abs(out - orc).max())
+            rel = err / float(np.abs(orc).max())
+            print(f"  vs oracle: max_abs={err:.3e} normwise={rel:.3e}", flush=True)
+            assert (rel <= 2e-2) if mode == rt.BF16 else (err <= 1e-4)
+
+
+def test_static_scratch_refuses_oversized_problem():
+    # B=2, 6144 tokens in f32x3 needs 288 MiB of scratch.  The buffers are
+    # full size, so even a launch would stay in bounds; the entry must
+    # refuse before launching and leave the output untouched.
+    lib = _lib.load()
+    B, S = 2, 6144
+    need = lib.anima_hip_attention_scratch_bytes(B, S, B, S, H, D, rt.F32X3)
+    assert need > STATIC_BYTES
+    z = np.zeros((B, S, H, D), np.float32)
+    dev = _Dev(z, z, z, np.ones(D, np.float32), np.ones(D, np.float32), None)
+    ok = lib.anima_hip_attention_static_dev(*dev.args(), B, S, B, S, H, D, ct.c_float(1e-6),
+                                            rt.F32X3, None)
+    assert not ok
+    assert "static" in _lib.last_error()
+    assert np.isnan(dev.out.get(dev.shape)).all()
