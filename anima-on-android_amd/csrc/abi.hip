@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cmath>
 #include <condition_variable>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -38,6 +39,15 @@ bool hip_ok(hipError_t e, const char *what)
 
 namespace {
 
+// Failure injection for tests of the error path: while the environment
+// variable ANIMA_HIP_FAIL_ALLOC is set to 1, every growth of a host-entry
+// workspace buffer fails as an out-of-memory hipMalloc would.
+bool injected_alloc_failure()
+{
+    const char *e = std::getenv("ANIMA_HIP_FAIL_ALLOC");
+    return e && e[0] == '1' && e[1] == '\0';
+}
+
 // Grow-only device buffer.
 struct DevBuf {
     void *p = nullptr;
@@ -48,6 +58,8 @@ struct DevBuf {
             return true;
         release();
         const size_t want = std::max<size_t>(bytes, 256);
+        if (injected_alloc_failure())
+            return fail(std::string(what) + ": out of memory (injected by ANIMA_HIP_FAIL_ALLOC)");
         if (!hip_ok(hipMalloc(&p, want), what)) {
             p = nullptr;
             return false;
@@ -952,6 +964,10 @@ bool anima_hip_flash_bf16_dev(const uint16_t *q, const uint16_t *k, const uint16
                               const int64_t *k_strides, const int64_t *vt_strides,
                               const int64_t *o_strides, float scale, bool is_causal, void *stream)
 {
+    // The kernel folds the scale into exp2's argument and takes the row max
+    // on raw scores, which needs scale > 0 (NaN and infinities are refused).
+    if (!(scale > 0.0f) || !std::isfinite(scale))
+        return fail("flash_bf16_dev: scale must be positive and finite");
     if (!ready_for_device_call() || !check_dims(B, H, S_q, S_kv, D))
         return false;
     if (int64_t(B) * H * S_q * D > 0 && (!q || !o || (S_kv > 0 && (!k || !vt))))
@@ -1000,6 +1016,10 @@ bool anima_hip_flash_x3_dev(const uint16_t *q, const uint16_t *k, const uint16_t
                             const int64_t *k_strides, const int64_t *vt_strides,
                             const int64_t *o_strides, float scale, bool is_causal, void *stream)
 {
+    // The kernel folds the scale into exp2's argument and takes the row max
+    // on raw scores, which needs scale > 0 (NaN and infinities are refused).
+    if (!(scale > 0.0f) || !std::isfinite(scale))
+        return fail("flash_x3_dev: scale must be positive and finite");
     if (!ready_for_device_call() || !check_dims(B, H, S_q, S_kv, D))
         return false;
     if (int64_t(B) * H * S_q * D > 0 && (!q || !o || (S_kv > 0 && (!k || !vt))))

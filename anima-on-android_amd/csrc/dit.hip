@@ -415,6 +415,11 @@ struct anima_hip_dit {
     float *sig_dev = nullptr, *sig_host = nullptr;
     int sig_cap = 0;
     hipEvent_t sig_ev = nullptr;
+    // Recorded on the caller's stream after each run's last launch; the next
+    // run's stream waits on it before it overwrites the sigmas and the step
+    // counter, so runs on different streams follow one another on the device.
+    hipEvent_t run_ev = nullptr;
+    bool run_recorded = false;
     int *step_dev = nullptr;
     hipStream_t cap_stream = nullptr;
     hipGraphExec_t graph = nullptr;
@@ -461,6 +466,8 @@ void dit_free(anima_hip_dit *d)
         (void)hipHostFree(d->sig_host);
     if (d->sig_ev)
         (void)hipEventDestroy(d->sig_ev);
+    if (d->run_ev)
+        (void)hipEventDestroy(d->run_ev);
     delete d;
 }
 
@@ -1206,6 +1213,19 @@ bool anima_hip_dit_euler_dev(anima_hip_dit *d, float *latent, const float *sigma
     if (!d->sig_ev && !hip_ok(hipEventCreateWithFlags(&d->sig_ev, hipEventDisableTiming),
                               "hipEventCreate"))
         return false;
+    if (!d->run_ev && !hip_ok(hipEventCreateWithFlags(&d->run_ev, hipEventDisableTiming),
+                              "hipEventCreate"))
+        return false;
+    // The previous run (possibly on another stream) still reads the sigma
+    // buffer and the step counter until its last replay ends.
+    if (d->run_recorded && !hip_ok(hipStreamWaitEvent(st, d->run_ev, 0), "hipStreamWaitEvent"))
+        return false;
+    // From the upload on, every exit marks the end of this run's work on st.
+    struct RunEnd {
+        anima_hip_dit *d;
+        hipStream_t st;
+        ~RunEnd() { d->run_recorded = hipEventRecord(d->run_ev, st) == hipSuccess; }
+    } run_end{d, st};
     std::copy(sigmas, sigmas + n_sig, d->sig_host);
     if (!hip_ok(hipMemcpyAsync(d->sig_dev, d->sig_host, size_t(n_sig) * 4,
                                hipMemcpyHostToDevice, st),

@@ -453,7 +453,7 @@ bool launch_flash_bf16(const FlashProblem &p, hipStream_t st, void *part, size_t
         return true;
     if (p.D != kD)
         return fail("flash_bf16: head dim must be 128 (got " + std::to_string(p.D) + ")");
-    if (!(p.scale > 0.0f))
+    if (!(p.scale > 0.0f) || !std::isfinite(p.scale))
         return fail("flash_bf16: scale must be positive");
     const int64_t sp = vt_padded_len(p.S_kv);
     if (p.vs.s != sp)

@@ -12,6 +12,7 @@
 // "net." prefix, linear weights stay bf16 bit patterns, and other weights
 // can be widened to f32 (bf16 bits << 16, as phone_pipeline_nd.py:37-40 does).
 #include "common.h"
+#include "safetensors_header.h"
 
 #include <fcntl.h>
 #include <sys/mman.h>
@@ -28,168 +29,10 @@
 namespace anima_hip {
 namespace {
 
-// Codes as the reference's vk_weight_add takes them (phone_pipeline_nd.py:31).
-enum : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
-
-int dtype_code(const std::string &s)
-{
-    if (s == "F32")
-        return kF32;
-    if (s == "F16")
-        return kF16;
-    if (s == "BF16")
-        return kBF16;
-    return -1;
-}
-
-int dtype_bytes(int code) { return code == kF32 ? 4 : 2; }
-
-// A small JSON reader for the safetensors header: objects, strings, integers
-// and arrays; anything else in a value (floats, booleans, null) is skipped.
-class Json {
-public:
-    Json(const char *p, const char *end) : p_(p), end_(end) {}
-
-    bool ok() const { return err_.empty(); }
-    const std::string &error() const { return err_; }
-
-    void ws()
-    {
-        while (p_ < end_ && (*p_ == ' ' || *p_ == '\t' || *p_ == '\n' || *p_ == '\r'))
-            ++p_;
-    }
-    bool peek(char c)
-    {
-        ws();
-        return p_ < end_ && *p_ == c;
-    }
-    bool expect(char c)
-    {
-        ws();
-        if (p_ < end_ && *p_ == c) {
-            ++p_;
-            return true;
-        }
-        return bad(std::string("expected '") + c + "'");
-    }
-    bool string(std::string &out)
-    {
-        if (!expect('"'))
-            return false;
-        out.clear();
-        while (p_ < end_ && *p_ != '"') {
-            char c = *p_++;
-            if (c == '\\') {
-                if (p_ >= end_)
-                    break;
-                c = *p_++;
-                switch (c) {
-                case 'n': c = '\n'; break;
-                case 't': c = '\t'; break;
-                case 'r': c = '\r'; break;
-                case 'b': c = '\b'; break;
-                case 'f': c = '\f'; break;
-                case 'u':  // keep the escape as text; names here are ASCII
-                    out += "\\u";
-                    continue;
-                default: break;
-                }
-            }
-            out += c;
-        }
-        if (p_ >= end_)
-            return bad("unterminated string");
-        ++p_;
-        return true;
-    }
-    bool integer(int64_t &v)
-    {
-        ws();
-        bool neg = false;
-        if (p_ < end_ && *p_ == '-') {
-            neg = true;
-            ++p_;
-        }
-        if (p_ >= end_ || *p_ < '0' || *p_ > '9')
-            return bad("expected an integer");
-        v = 0;
-        while (p_ < end_ && *p_ >= '0' && *p_ <= '9') {
-            if (v > (INT64_MAX - 9) / 10)
-                return bad("integer overflow");
-            v = v * 10 + (*p_++ - '0');
-        }
-        if (neg)
-            v = -v;
-        return true;
-    }
-    bool int_array(std::vector<int64_t> &out)
-    {
-        out.clear();
-        if (!expect('['))
-            return false;
-        if (peek(']'))
-            return expect(']');
-        for (;;) {
-            int64_t v;
-            if (!integer(v))
-                return false;
-            out.push_back(v);
-            if (peek(','))
-                expect(',');
-            else
-                return expect(']');
-        }
-    }
-    // Skip any JSON value.
-    bool skip()
-    {
-        ws();
-        if (p_ >= end_)
-            return bad("unexpected end");
-        if (*p_ == '"') {
-            std::string s;
-            return string(s);
-        }
-        if (*p_ == '{' || *p_ == '[') {
-            const char close = *p_ == '{' ? '}' : ']';
-            const bool obj = *p_ == '{';
-            ++p_;
-            if (peek(close))
-                return expect(close);
-            for (;;) {
-                if (obj) {
-                    std::string k;
-                    if (!string(k) || !expect(':'))
-                        return false;
-                }
-                if (!skip())
-                    return false;
-                if (peek(','))
-                    expect(',');
-                else
-                    return expect(close);
-            }
-        }
-        while (p_ < end_ && *p_ != ',' && *p_ != '}' && *p_ != ']')
-            ++p_;
-        return true;
-    }
-    bool at_end()
-    {
-        ws();
-        return p_ >= end_;
-    }
-
-private:
-    bool bad(const std::string &m)
-    {
-        if (err_.empty())
-            err_ = m;
-        return false;
-    }
-    const char *p_, *end_;
-    std::string err_;
-};
+using st::dtype_bytes;
+using st::kBF16;
+using st::kF16;
+using st::kF32;
 
 }  // namespace
 }  // namespace anima_hip
@@ -235,91 +78,22 @@ std::string strip_prefix(const std::string &n)
 
 bool parse_header(anima_hip_weights &w, const char *p, const char *end, size_t data_len)
 {
-    Json js(p, end);
-    if (!js.expect('{'))
-        return fail("weights: header is not a JSON object: " + js.error());
-    if (!js.peek('}')) {
-        for (;;) {
-            std::string key;
-            if (!js.string(key) || !js.expect(':'))
-                return fail("weights: bad header entry: " + js.error());
-            if (key == "__metadata__") {
-                if (!js.skip())
-                    return fail("weights: bad __metadata__: " + js.error());
-            } else {
-                anima_hip_weights::Tensor t;
-                t.name = key;
-                std::vector<int64_t> offs;
-                bool has_dtype = false, has_shape = false, has_offs = false;
-                if (!js.expect('{'))
-                    return fail("weights: tensor '" + key + "' is not an object");
-                if (!js.peek('}')) {
-                    for (;;) {
-                        std::string f;
-                        if (!js.string(f) || !js.expect(':'))
-                            return fail("weights: bad field in '" + key + "': " + js.error());
-                        if (f == "dtype") {
-                            std::string d;
-                            if (!js.string(d))
-                                return fail("weights: bad dtype of '" + key + "'");
-                            t.dtype = dtype_code(d);
-                            if (t.dtype < 0)
-                                return fail("weights: tensor '" + key + "' has unsupported dtype " + d);
-                            has_dtype = true;
-                        } else if (f == "shape") {
-                            if (!js.int_array(t.shape))
-                                return fail("weights: bad shape of '" + key + "': " + js.error());
-                            has_shape = true;
-                        } else if (f == "data_offsets") {
-                            if (!js.int_array(offs) || offs.size() != 2)
-                                return fail("weights: bad data_offsets of '" + key + "'");
-                            has_offs = true;
-                        } else if (!js.skip()) {
-                            return fail("weights: bad field in '" + key + "': " + js.error());
-                        }
-                        if (js.peek(','))
-                            js.expect(',');
-                        else if (!js.expect('}'))
-                            return fail("weights: bad tensor entry '" + key + "': " + js.error());
-                        else
-                            break;
-                    }
-                } else {
-                    js.expect('}');
-                }
-                if (!has_dtype || !has_shape || !has_offs)
-                    return fail("weights: tensor '" + key + "' lacks dtype, shape or data_offsets");
-                int64_t n = 1;
-                for (int64_t d : t.shape) {
-                    if (d < 0 || (d > 0 && n > INT64_MAX / d))
-                        return fail("weights: bad shape of '" + key + "'");
-                    n *= d;
-                }
-                if (offs[0] < 0 || offs[1] < offs[0] || size_t(offs[1]) > data_len)
-                    return fail("weights: data_offsets of '" + key + "' lie outside the file");
-                t.begin = size_t(offs[0]);
-                t.bytes = size_t(offs[1] - offs[0]);
-                if (t.bytes != size_t(n) * dtype_bytes(t.dtype))
-                    return fail("weights: '" + key + "' holds " + std::to_string(t.bytes) +
-                                " bytes, its dtype and shape need " +
-                                std::to_string(size_t(n) * dtype_bytes(t.dtype)));
-                const size_t idx = w.tensors.size();
-                w.index[t.name] = idx;
-                w.index.emplace(strip_prefix(t.name), idx);
-                w.tensors.push_back(std::move(t));
-            }
-            if (js.peek(','))
-                js.expect(',');
-            else if (!js.expect('}'))
-                return fail("weights: bad header: " + js.error());
-            else
-                break;
-        }
-    } else {
-        js.expect('}');
+    std::vector<st::Entry> entries;
+    std::string err;
+    if (!st::parse_header(p, end, data_len, entries, err))
+        return fail(err);
+    for (st::Entry &e : entries) {
+        anima_hip_weights::Tensor t;
+        t.name = std::move(e.name);
+        t.dtype = e.dtype;
+        t.shape = std::move(e.shape);
+        t.begin = e.begin;
+        t.bytes = e.bytes;
+        const size_t idx = w.tensors.size();
+        w.index[t.name] = idx;
+        w.index.emplace(strip_prefix(t.name), idx);
+        w.tensors.push_back(std::move(t));
     }
-    if (!js.at_end())
-        return fail("weights: trailing bytes after the header object");
     for (auto &t : w.tensors)
         w.short_names.push_back(strip_prefix(t.name));
     return true;

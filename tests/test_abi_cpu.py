@@ -171,3 +171,17 @@ def test_python_shape_validation():
         rt.sdpa_flash(q, np.zeros((2, 5, 9), np.float32), np.zeros((2, 5, 9), np.float32))
     with pytest.raises(ValueError):
         rt.rope(q, np.zeros((3, 4, 2, 2), np.float32))
+
+
+@pytest.mark.parametrize("entry", ["anima_hip_flash_bf16_dev", "anima_hip_flash_x3_dev"])
+@pytest.mark.parametrize("scale", [float("nan"), 0.0, -0.088, float("inf")])
+def test_bf16_and_x3_entries_refuse_a_bad_scale_before_any_device_work(entry, scale):
+    # These kernels fold the scale into exp2's argument and take the row max
+    # on raw scores, so they need a positive finite scale.  The check runs on
+    # the host before the device context is touched (no GPU needed here).
+    lib = _lib.load()
+    fn = getattr(lib, entry)
+    ok = fn(None, None, None, None, 1, 1, 1, 1, 128, None, None, None, None, ct.c_float(scale),
+            False, None)
+    assert not ok
+    assert "scale must be positive and finite" in _lib.last_error()

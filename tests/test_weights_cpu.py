@@ -47,7 +47,8 @@ def test_empty_header_and_zero_size_tensor(tmp_path):
 
 
 @pytest.mark.parametrize("case", ["truncated", "bad_json", "offsets_out", "size_mismatch",
-                                  "bad_dtype", "header_too_long", "missing_field", "trailing"])
+                                  "bad_dtype", "header_too_long", "missing_field", "trailing",
+                                  "deep_metadata", "deep_field", "shape_wraps"])
 def test_malformed_files_are_refused(tmp_path, case):
     p = tmp_path / f"{case}.safetensors"
     a = np.arange(8, dtype=np.float32)
@@ -67,7 +68,31 @@ def test_malformed_files_are_refused(tmp_path, case):
         write(p, {"a": ("F32", a)}, header_override='{"a": {"dtype": "F32", "data_offsets": [0, 32]}}')
     elif case == "trailing":
         write(p, {"a": ("F32", a)}, header_override='{"a": {"dtype": "F32", "shape": [8], "data_offsets": [0, 32]}} {}')
+    elif case == "deep_metadata":
+        # Nesting far past the parser's cap of 64 levels: refused, not a stack overflow.
+        write(p, {"a": ("F32", a)}, header_override='{"__metadata__": ' + "[" * 300000 + "}")
+    elif case == "deep_field":
+        write(p, {"a": ("F32", a)}, header_override='{"a": {"dtype": "F32", "shape": [8], "data_offsets": [0, 32], "x": '
+              + '{"k": ' * 100000 + "1" + "}" * 100000 + "}}")
+    elif case == "shape_wraps":
+        # 2^62 F32 elements: the byte count wraps to 0 in 64 bits and would
+        # match data_offsets [0, 0] without the overflow check.
+        write(p, {}, header_override='{"w": {"dtype": "F32", "shape": [4611686018427387904], "data_offsets": [0, 0]}}')
     with pytest.raises(AnimaHipError):
+        rt.Weights(p)
+
+
+def test_nesting_within_the_cap_is_accepted(tmp_path):
+    p = tmp_path / "nested.safetensors"
+    a = np.arange(8, dtype=np.float32)
+    meta = "[" * 64 + "]" * 64
+    write(p, {"a": ("F32", a)},
+          header_override='{"__metadata__": ' + meta + ', "a": {"dtype": "F32", "shape": [8], '
+                          '"data_offsets": [0, 32]}}')
+    with rt.Weights(p) as w:
+        assert w.info("a") == ("F32", (8,))
+    write(p, {"a": ("F32", a)}, header_override='{"__metadata__": ' + "[" + meta + "]" + "}")
+    with pytest.raises(AnimaHipError, match="nesting deeper than 64"):
         rt.Weights(p)
 
 
