@@ -77,21 +77,14 @@ def test_bf16_self_attention_256_and_fp64():
     assert err <= REL
 
 
-def test_bf16_self_attention_4096_sampled_heads():
-    """B=2, H=16, S=4096: full problem on the GPU, two slices vs the oracle."""
-    rng = np.random.default_rng(3003)
-    B, S, H, D = 2, 4096, 16, 128
-    q, k, v = randn(rng, B, S, H, D), randn(rng, B, S, H, D), randn(rng, B, S, H, D)
-    f = generate_rope_freqs(64, 64)
-    ones = np.ones(D, np.float32)
+def test_bf16_self_attention_4096_all_heads():
+    """B=2, H=16, S=4096: full problem on the GPU, all 32 slices vs the oracle."""
+    import fullsize
+    q, k, v, f = fullsize.self_case(4096, (64, 64), 3003)
+    ones = np.ones(128, np.float32)
     out = rt.attention(q, k, v, ones, ones, f, mode=rt.BF16)
-    assert np.isfinite(out).all()
-    for b, h in [(0, 5), (1, 11)]:
-        ref = oracle.attention_dataflow(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, h:h + 1],
-                                        v[b:b + 1, :, h:h + 1], ones, ones, f)
-        err = rel_err(out[b, :, h], ref[0, :, 0])
-        print(f"bf16 4096 tokens b={b} h={h} rel err {err:.3e}", flush=True)
-        assert err <= REL
+    fullsize.check_all_slices(out, fullsize.self_ref(4096, (64, 64), 3003), rt.BF16,
+                              "bf16 self-attention 4096 tokens")
 
 
 def test_bf16_deterministic():

@@ -175,10 +175,10 @@ def test_x3_deterministic():
     np.testing.assert_array_equal(a, rt.sdpa(q, k, v, mode=rt.F32X3))
 
 
-def test_x3_attention_core_256_and_4096_tokens_sampled_heads():
+def test_x3_attention_core_256_and_4096_tokens_all_heads():
     """The fused attention core (anima_hip_attention: RMSNorm + RoPE prologue
     writing term rows, term V^T pack, f32x3 flash) at 256 tokens and at the
-    4096-token, B=2, H=16 workload; two (batch, head) slices of the latter
+    4096-token, B=2, H=16 workload; every (batch, head) slice of the latter
     against the oracle."""
     ones = np.ones(128, np.float32)
     rng = np.random.default_rng(1001)
@@ -187,13 +187,8 @@ def test_x3_attention_core_256_and_4096_tokens_sampled_heads():
     out = rt.attention(q, k, v, ones, ones, f, mode=rt.F32X3)
     check(out, oracle.attention_dataflow(q, k, v, ones, ones, f), "attention 256 tokens")
 
-    rng = np.random.default_rng(3003)
-    B, S, H, D = 2, 4096, 16, 128
-    q, k, v = randn(rng, B, S, H, D), randn(rng, B, S, H, D), randn(rng, B, S, H, D)
-    f = generate_rope_freqs(64, 64)
+    import fullsize
+    q, k, v, f = fullsize.self_case(4096, (64, 64), 3003)
     out = rt.attention(q, k, v, ones, ones, f, mode=rt.F32X3)
-    assert np.isfinite(out).all()
-    for b, h in [(0, 3), (1, 14)]:
-        ref = oracle.attention_dataflow(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, h:h + 1],
-                                        v[b:b + 1, :, h:h + 1], ones, ones, f)
-        check(out[b, :, h], ref[0, :, 0], f"4096 tokens b={b} h={h}")
+    fullsize.check_all_slices(out, fullsize.self_ref(4096, (64, 64), 3003), rt.F32X3,
+                              "f32x3 attention core 4096 tokens")
