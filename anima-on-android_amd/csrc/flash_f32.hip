@@ -271,20 +271,24 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_f32_d128(F32Args a)
     }
 
     l += __shfl_xor(l, 32);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    // Every score of the row masked or NaN (the max never left -inf): zeros,
+    // as the reference leaves such rows (flash_attention.h:148-152, 194-201).
+    const bool dead = m == -INFINITY;
+    const float inv = dead ? 0.0f : l > 0.0f ? 1.0f / l : 0.0f;
     if (qrow < a.S_q) {
         float *op = a.o + b * a.ob + h * a.oh + qrow * a.os;
         if (a.split.n > 1) {
             const int64_t prow = (int64_t(sp) * a.split.BH + bh) * a.S_q + qrow;
             op = a.split.part + prow * kD;
             if (half == 0)
-                a.split.ml[prow] = make_float2(m, l);
+                a.split.ml[prow] = make_float2(m, dead ? 0.0f : l);
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int d0 = 4 * acc_row(r, half);
             *reinterpret_cast<f32x4 *>(op + d0) =
-                f32x4{o0[r] * inv, o1[r] * inv, o2[r] * inv, o3[r] * inv};
+                dead ? f32x4{0.f, 0.f, 0.f, 0.f}
+                     : f32x4{o0[r] * inv, o1[r] * inv, o2[r] * inv, o3[r] * inv};
         }
     }
 }
@@ -348,13 +352,14 @@ __global__ __launch_bounds__(64) void flash_f32_generic(GenArgs a)
         }
         m = m_new;
     }
+    const bool dead = m == -INFINITY;  // every score NaN: zeros, as the reference
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     float *op = a.o + b * a.ob + h * a.oh + qrow * a.os;
 #pragma unroll
     for (int i = 0; i < DPL; ++i) {
         const int d = lane + 64 * i;
         if (d < a.D)
-            op[d] = ov[i] * inv;
+            op[d] = dead ? 0.0f : ov[i] * inv;
     }
 }
 

@@ -49,9 +49,12 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(CombineArgs a)
 #pragma unroll
         for (int u = 0; u < kU; ++u)
             v[u] = s0 + u < a.sa.n ? a.sa.ml[(s0 + u) * plane + row] : make_float2(0.f, 0.f);
+        // A split with l == 0 saw no key (causal) or only masked or NaN
+        // scores; a NaN l (a NaN score among finite ones) joins and makes
+        // the row NaN, as in the reference.
 #pragma unroll
         for (int u = 0; u < kU; ++u)
-            if (v[u].y > 0.0f)
+            if (v[u].y != 0.0f)
                 mx = fmaxf(mx, v[u].x);
     }
     float lsum = 0.0f;
@@ -69,7 +72,7 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(CombineArgs a)
         }
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            if (v[u].y > 0.0f) {
+            if (v[u].y != 0.0f) {
                 const float w = v[u].y * exp2f(v[u].x - mx);
                 lsum += w;
                 acc += w * x[u];

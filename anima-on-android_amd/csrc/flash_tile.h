@@ -120,6 +120,60 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16 &s, int base)
     return r;
 }
 
+// Epilogue of the transposed bf16-MFMA kernels.  A wave holds O^T of its 32
+// query rows in four 32x32 accumulators (o_blk: d = 32 blk + acc_row(r,
+// half)), so a direct store writes 16 bytes of 32 rows 8 KiB apart per
+// instruction and fills each 128-byte line over four instructions.  Staged
+// through an LDS region of the wave instead, in two passes over d, every store
+// instruction writes four whole 256-byte half rows.
+// Rows r >= nrows are not written.  A dead row (its running max never left
+// -inf: every score was masked or NaN) is written as zeros, which is what the
+// reference's flash attention leaves there (flash_attention.h:148-152 skips
+// such rows and :194-201 divides only positive sums of a zero-filled output).
+// The caller guarantees no other wave uses `lds` (kOWaveFloats floats).
+constexpr int kOPitch = 68;  // floats per staged half row: 64 d + 4 against bank conflicts
+constexpr int kOWaveFloats = 32 * kOPitch;
+
+__device__ __forceinline__ void store_o_rows(float *lds, const f32x16 &o0, const f32x16 &o1,
+                                             const f32x16 &o2, const f32x16 &o3, float inv,
+                                             bool dead, float *row0, int64_t stride, int nrows)
+{
+    const int lane = threadIdx.x & 63, col = lane & 31, half = lane >> 5;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+            const f32x16 &ob = p == 0 ? (bb == 0 ? o0 : o1) : (bb == 0 ? o2 : o3);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                f32x4 v = f32x4{ob[4 * g] * inv, ob[4 * g + 1] * inv, ob[4 * g + 2] * inv,
+                                ob[4 * g + 3] * inv};
+                if (dead)
+                    v = f32x4{0.f, 0.f, 0.f, 0.f};
+                *reinterpret_cast<f32x4 *>(lds + col * kOPitch + 32 * bb + acc_row(4 * g, half)) =
+                    v;
+            }
+        }
+        // The rows were written by other lanes of this wave: wait for the LDS
+        // writes, and keep the compiler from moving reads above them.
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        asm volatile("" ::: "memory");
+        const int c = lane & 15;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 4 * i + (lane >> 4);
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(lds + r * kOPitch + 4 * c);
+            if (r < nrows)
+                *reinterpret_cast<f32x4 *>(row0 + r * stride + 64 * p + 4 * c) = v;
+        }
+        // This pass's reads complete before the next pass overwrites the rows.
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        asm volatile("" ::: "memory");
+    }
+}
+
 // Logical id of this workgroup, XCD-major.  The dispatcher hands workgroup i
 // to XCD i % 8, so consecutive ids land on different XCDs and every XCD ends
 // up streaming every (batch, head)'s K/V from HBM.  Renumbered so that the

@@ -63,8 +63,11 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
     constexpr int DMA = kTile / 8 / NT;  // 16-byte copies per thread per tile
     static_assert(kTile / 8 % NT == 0, "tiles must split evenly");
 
-    __shared__ __attribute__((aligned(16))) u16 Ks[2][kTile];
-    __shared__ __attribute__((aligned(16))) u16 Vs[2][kTile];
+    // K ring, then V^T ring, in one array: the epilogue reuses it whole.
+    __shared__ __attribute__((aligned(16))) u16 smem[4 * kTile];
+    u16 (*const Ks)[kTile] = reinterpret_cast<u16 (*)[kTile]>(smem);
+    u16 (*const Vs)[kTile] = reinterpret_cast<u16 (*)[kTile]>(smem + 2 * kTile);
+    static_assert(NW * kOWaveFloats * 4 <= int(sizeof(smem)), "O staging fits the rings");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -330,26 +333,21 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
     l += l2;
     l += __shfl_xor(l, 32);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    if (qrow < a.S_q) {
-        float *op = a.o + b * a.ob + h * a.oh + qrow * a.os;
-        if (a.split.n > 1) {
-            const int64_t prow = (int64_t(sp) * a.split.BH + bh) * a.S_q + qrow;
-            op = a.split.part + prow * kD;
-            if (half == 0)
-                a.split.ml[prow] = make_float2(m, l);
-        }
-#pragma unroll
-        for (int blk = 0; blk < 4; ++blk) {
-            const f32x16 &ob = blk == 0 ? o0 : blk == 1 ? o1 : blk == 2 ? o2 : o3;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d0 = 32 * blk + acc_row(4 * g, half);
-                *reinterpret_cast<f32x4 *>(op + d0) =
-                    f32x4{ob[4 * g] * inv, ob[4 * g + 1] * inv, ob[4 * g + 2] * inv,
-                          ob[4 * g + 3] * inv};
-            }
-        }
+    // Every score of the row masked or NaN: the reference leaves zeros.
+    const bool dead = m == -INFINITY;
+    const int row0 = q_tile0 + wave * 32;
+    float *op = a.o + b * a.ob + h * a.oh + row0 * a.os;
+    int64_t ostride = a.os;
+    if (a.split.n > 1) {
+        const int64_t prow0 = (int64_t(sp) * a.split.BH + bh) * a.S_q + row0;
+        op = a.split.part + prow0 * kD;
+        ostride = kD;
+        if (half == 0 && qrow < a.S_q)
+            a.split.ml[prow0 + col] = make_float2(m, dead ? 0.0f : l);
     }
+    // Every wave has passed the loop's last barrier: the rings are free.
+    store_o_rows(reinterpret_cast<float *>(smem) + wave * kOWaveFloats, o0, o1, o2, o3, inv, dead,
+                 op, ostride, a.S_q - row0);
 }
 
 // V (f32, [B,H,S,D] view, D = 128) -> packed bf16 term V^T [B,H][2D][Sp]:

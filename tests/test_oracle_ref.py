@@ -63,3 +63,23 @@ def test_layernorm_silu_bitwise_vs_reference():
     np.testing.assert_array_equal(oracle.silu(x), oracle.ref_silu(x))
     np.testing.assert_array_equal(oracle.gelu(x), oracle.ref_gelu(x))
     np.testing.assert_array_equal(oracle.softmax(x[:, :300]), oracle.ref_softmax(x[:, :300]))
+
+
+@pytest.mark.parametrize("where", ["q_row", "k_row", "v_elem"])
+def test_flash_nan_pattern_vs_reference(where):
+    # The reference's NaN behaviour, which the GPU kernels reproduce: a query
+    # row whose scores are all NaN is skipped and stays zero
+    # (flash_attention.h:148-152, 194-201); a NaN key makes every row of its
+    # head NaN; a NaN value element makes its column NaN.  The oracle matches
+    # the compiled reference bit for bit, NaN positions included.
+    rng = np.random.default_rng(17)
+    q, k, v = (rng.standard_normal((2, 600, 128)).astype(np.float32) for _ in range(3))
+    {"q_row": q, "k_row": k, "v_elem": v}[where][0, 40, 7 if where == "v_elem" else 3] = np.nan
+    out = oracle.flash_sdpa(q, k, v, 0.088)
+    np.testing.assert_array_equal(out, oracle.ref_flash_sdpa(q, k, v, 0.088))
+    if where == "q_row":
+        assert np.all(out[0, 40] == 0) and np.isfinite(np.delete(out[0], 40, axis=0)).all()
+    elif where == "k_row":
+        assert np.isnan(out[0]).all() and np.isfinite(out[1]).all()
+    else:
+        assert np.isnan(out[0, :, 7]).all() and np.isfinite(np.delete(out[0], 7, axis=1)).all()
