@@ -1,7 +1,7 @@
 // Flash attention with bf16 inputs, bf16 MFMA and f32 accumulation (gfx950).
 //
 // Same computation as anima_rt_run_sdpa_flash (anima_rt/src/anima_rt.cpp:147-156 ->
-// anima/include/cpu/flash_attention.h:55-208) with Q, K, V and the softmax
+// anima_rt/include/cpu/flash_attention.h:55-208) with Q, K, V and the softmax
 // probabilities P rounded to bf16 before the two products; scores, the
 // online max/sum and the output accumulate in f32.
 //
@@ -12,9 +12,10 @@
 //     accumulator converted to bf16 in place (8 consecutive accumulator
 //     registers = 8 keys); V^T's A operand is one 16-byte LDS read thanks to
 //     the key order of the packed V^T (vt_key_pos);
-//   * K tiles [64 keys][128 d] and V^T tiles [128 d][64 keys] are staged
-//     through LDS, double-buffered, one barrier per tile; row pitches are
-//     padded by 16 bytes so the per-lane 16-byte reads are conflict-free;
+//   * K tiles [64 keys][128 d] and V^T tiles [128 d][64 keys] reach LDS by
+//     DMA (global_load_lds) through rings of three stages, one barrier per
+//     tile; rows are unpadded and XOR-swizzled in 16-byte chunks so the
+//     per-lane 16-byte fragment reads are bank-conflict free;
 //   * software-pipelined per wave: the MFMAs computing the scores of tile
 //     j+1 are interleaved (sched_barrier) with the VALU softmax of tile j,
 //     then P.V of tile j follows, so the MFMA pipe and the VALU overlap

@@ -14,10 +14,12 @@ compiled from its own sources (oracle/_ref), called through the same methods
 as NumpyRT (scripts/phone_pipeline_nd.py:46-68); vk is that runtime's bf16
 GEMM (fp32 activations x bf16 weights, fp32 accumulation), standing in for
 the phone's Vulkan GEMM of the same arithmetic.  NumpyDiT.forward itself
-starts by resetting the Vulkan descriptor pool (numpy_dit.py:87-88), which
-this container cannot load, so `reference_forward` below runs the remaining
-statements of that method (numpy_dit.py:89-130) in order, with the model
-sizes as parameters.
+(numpy_dit.py:82-130) runs unchanged: its first statements reset the Vulkan
+descriptor pool through the phone-only module vk_ops (numpy_dit.py:87-88),
+which this script provides as a stub whose reset does nothing.
+NumpyDiT.__init__ fixes the full model's sizes (numpy_dit.py:68-79), so the
+small model's instance is assembled from the reference's own sub-module
+classes with the same attribute names and then driven through that method.
 
 Model: width 2048 (NumpyPatchEmbed fixes it), 2 blocks, 2 heads x 128, MLP
 512, text context 64 wide, 16 latent channels; latent 7 x 10 (odd height:
@@ -27,6 +29,7 @@ Run:  python tests/golden/make_dit_golden.py   (needs oracle/_ref built)
 """
 import os
 import sys
+import types
 
 import numpy as np
 
@@ -104,33 +107,18 @@ def main():
     t_embedder = nd.NumpyTimestepEmbedding(D, vk, rt)
     final_layer = nd.NumpyFinalLayer(D, vk, rt)
 
-    def reference_forward(x_np, sigma, ctx_np):
-        # numpy_dit.py:89-130, in order.
-        B, C, T_in, Hi, Wi = x_np.shape
-        orig = [B, C, T_in, Hi, Wi]
-        x_np = nd._pad_to_patch_size(x_np, 1, 2)
-        B, C, T, H_img, W_img = x_np.shape
-        padding = np.zeros((B, 1, T, H_img, W_img), dtype=np.float32)
-        x_np = np.concatenate([x_np, padding], axis=1)
-        x_bt_s_d = x_embedder.forward(x_np.astype(np.float32))
-        H, W = H_img // 2, W_img // 2
-        x = x_bt_s_d.reshape(B, T, H, W, D).astype(np.float32)
-        rope_raw = nd._generate_rope_freqs(H, W, T, hd).astype(np.float32)
-        rope_emb = rope_raw[np.newaxis, :, np.newaxis, :, :, :]
-        sigma_arr = np.atleast_1d(np.asarray(sigma, dtype=np.float32))
-        t_emb_np = nd._numpy_timesteps(sigma_arr, D)
-        t_emb, adaln_lora = t_embedder.forward(t_emb_np)
-        t_emb = rt.run_rmsnorm(t_emb, "t_embedding_norm")
-        ctx_f32 = ctx_np.astype(np.float32)
-        for blk in blocks:
-            x = blk.forward(x, t_emb, ctx_f32, rope_emb, adaln_lora)
-        x_out = final_layer.forward(x, t_emb, adaln_lora)
-        x_out = nd._rearrange_unpatchify(x_out, 2, 1, 16)
-        x_out = x_out[:, :, :orig[-3], :orig[-2], :orig[-1]]
-        return x_out.astype(np.float32)
-
-    class Model:
-        forward = staticmethod(reference_forward)
+    # The phone's Vulkan module, reached only for its pool reset.
+    vk_ops = types.ModuleType("vk_ops")
+    vk_ops._lib = types.SimpleNamespace(vk_reset_pool=lambda: None)
+    sys.modules["vk_ops"] = vk_ops
+    model = object.__new__(nd.NumpyDiT)
+    model._vk, model._rt = vk, rt
+    model.D, model.num_blocks, model.num_heads = D, CFG["blocks"], heads
+    model.head_dim, model.mlp_hidden = hd, CFG["mlp_hidden"]
+    model.ps, model.pt, model.out_ch = 2, 1, 16
+    model.x_embedder, model.t_embedder, model.final_layer = x_embedder, t_embedder, final_layer
+    model.blocks = blocks
+    reference_forward = model.forward
 
     rng = np.random.default_rng(7102)
     vec = {"weight_seed": np.array(WEIGHT_SEED)}
@@ -149,7 +137,7 @@ def main():
     sigmas = sampling.ZImageScheduler().get_sigmas(2, 1.0)
     vec["smp_noise"], vec["smp_ctx_cond"], vec["smp_ctx_uncond"] = noise, ctx_c, ctx_u
     vec["smp_sigmas"], vec["smp_cfg"] = sigmas, np.array(5.0, np.float32)
-    vec["smp_out"] = sampling.EulerSampler().sample(Model(), noise, sigmas, ctx_c, ctx_u, 5.0,
+    vec["smp_out"] = sampling.EulerSampler().sample(model, noise, sigmas, ctx_c, ctx_u, 5.0,
                                                     0).astype(np.float32)
     print("sampler done", flush=True)
     np.savez_compressed(OUT, **vec)

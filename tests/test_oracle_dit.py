@@ -146,3 +146,26 @@ def test_product_weight_names_match_reference_layout():
     for blocks, heads, hidden, ctx in ((2, 2, 512, 64), (28, 16, 8192, 1024)):
         cfg = DiTConfig.anima_2b(blocks=blocks, heads=heads, mlp_hidden=hidden, ctx_dim=ctx)
         assert weight_shapes(cfg) == dit_weights.shapes(2048, blocks, heads, 128, hidden, ctx)
+
+
+@pytest.mark.parametrize("grid", [(16, 16), (64, 64), (96, 64)])
+def test_rope_tables_match_reference_builder_bitwise(grid):
+    # Tables written by the reference's own _generate_rope_freqs
+    # (numpy_dit.py:48-60; tests/golden/make_rope_golden.py): the library's
+    # host builder (anima_hip/rope.py) and the oracle's reproduce them bit for
+    # bit at the grids of configs 1, 3 and 5, the 96x64 one rectangular.
+    import hashlib
+
+    from anima_hip.rope import generate_rope_freqs
+    g = np.load(os.path.join(HERE, "golden", "rope_ref_tables.npz"))
+    H, W = grid
+    key = f"{H}x{W}"
+    for table in (generate_rope_freqs(H, W), oracle.rope_freqs(H, W)):
+        assert table.dtype == np.float32 and table.shape == (H * W, 64, 2, 2)
+        t5 = table.reshape(H, W, 64, 2, 2)
+        np.testing.assert_array_equal(t5[:, 0], g[f"col0_{key}"])
+        np.testing.assert_array_equal(t5[0, :], g[f"row0_{key}"])
+        if f"table_{key}" in g.files:
+            np.testing.assert_array_equal(table, g[f"table_{key}"])
+        digest = hashlib.sha256(np.ascontiguousarray(table).tobytes()).hexdigest()
+        assert digest == str(g[f"sha256_{key}"])
