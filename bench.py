@@ -289,7 +289,7 @@ def cross_attention_timer(c, mode, cache, B, S_q, seed, H=16, D=128):
     return run, 4.0 * B * H * S_q * cache.tokens * D
 
 
-def other_configs(c, cpu_rate):
+def other_configs(c):
     """Configs 1, 2, 5 and the 28-block denoise step, every arithmetic mode."""
     out = {}
     for variant in VARIANTS:
@@ -330,15 +330,6 @@ def other_configs(c, cpu_rate):
         res["sampler_step_full_dit"] = sampler_step(c, mode)
         out[variant] = res
         log(f"[bench] configs {variant}: " + json.dumps(res))
-    if cpu_rate:
-        fl = {"c1": 4.0 * 16 * 256 * 256 * 128, "c2": 4.0 * 32 * 256 * 512 * 128,
-              "c3": 4.0 * 32 * 4096 * 4096 * 128,
-              "c4": 28 * 4.0 * 32 * 4096 * 128 * (4096 + 512),
-              "c5": 4.0 * 32 * 6144 * 128 * (6144 + 512)}
-        out["cpu_extrapolated_s"] = {
-            "note": "anima_rt flash attention time on one host core, extrapolated from the "
-                    "measured cpu_baseline rate (not measured per config)",
-            **{k: round(v / (cpu_rate * 1e12), 2) for k, v in fl.items()}}
     return out
 
 
@@ -567,9 +558,58 @@ def normalized_qk(c, q, k, freqs, ones):
     return out
 
 
+def cpu_model():
+    """The host CPU's model name (Linux /proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
+
+
+def cpu_per_config(fn, rate_tflops, sample):
+    """anima_rt's flash attention per configuration on one host core.
+    Configs 1 and 2 are small enough to time whole (median of 3 runs, seeded
+    N(0,1) slices of their shapes); config 3 is the headline's measured
+    sample; configs 4 and 5 are extrapolated from that sample's rate."""
+    import numpy as np
+    rng = np.random.default_rng(77)
+    out = {}
+    for key, bh, sq, sk, what in (("c1", 16, 256, 256, "self-attention B=1 H=16 256x256"),
+                                  ("c2", 32, 256, 512, "cross-attention B=2 H=16 256x512")):
+        q = rng.standard_normal((bh, sq, 128), dtype=np.float32)
+        k = rng.standard_normal((bh, sk, 128), dtype=np.float32)
+        v = rng.standard_normal((bh, sk, 128), dtype=np.float32)
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn(q, k, v, 1.0 / math.sqrt(128))
+            runs.append(time.perf_counter() - t0)
+        out[key] = {"seconds": round(sorted(runs)[1], 4), "how": "measured, median of 3",
+                    "workload": what}
+    fl = {"c3": 4.0 * 32 * 4096 * 4096 * 128,
+          "c4": 28 * 4.0 * 32 * 4096 * 128 * (4096 + 512),
+          "c5": 4.0 * 32 * 6144 * 128 * (6144 + 512)}
+    out["c3"] = {"seconds": round(fl["c3"] / (rate_tflops * 1e12), 2),
+                 "how": f"sample ({sample}), scaled to all 32 slices",
+                 "workload": "self-attention B=2 H=16 4096x4096"}
+    out["c4"] = {"seconds": round(fl["c4"] / (rate_tflops * 1e12), 1),
+                 "how": "extrapolated from the config-3 sample's rate",
+                 "workload": "28 x (self 4096x4096 + cross 4096x512), B=2 H=16"}
+    out["c5"] = {"seconds": round(fl["c5"] / (rate_tflops * 1e12), 1),
+                 "how": "extrapolated from the config-3 sample's rate",
+                 "workload": "self 6144x6144 + cross 6144x512, B=2 H=16"}
+    return out
+
+
 def cpu_baseline(qn, kn, v, B, H, S, D, heads):
     """anima_rt flash attention on `heads` (b, h) slices, one core, plus the
-    same per-head work spread over this host's cores."""
+    same per-head work spread over this host's cores, and the one-core time
+    of every configuration."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle
@@ -592,10 +632,13 @@ def cpu_baseline(qn, kn, v, B, H, S, D, heads):
     fn(np.stack(qs), np.stack(ks), np.stack(vs), scale)
     dt = time.perf_counter() - t0
     flops = 4.0 * n1 * S * S * D
+    sample = (f"{n1} of {B * H} (batch,head) slices of the 4096x4096 self-attention, "
+              f"anima_rt flash_attention, {dt:.2f} s wall")
     single = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": kind,
-              "sample": f"{n1} of {B * H} (batch,head) slices of the 4096x4096 self-attention, "
-                        f"anima_rt flash_attention, {dt:.2f} s wall",
-              "seconds": round(dt, 3), "nproc": os.cpu_count()}
+              "sample": sample, "seconds": round(dt, 3), "nproc": os.cpu_count(),
+              "cpu_model": cpu_model(), "threads": 1}
+    log("[bench] cpu baseline per config")
+    single["per_config"] = cpu_per_config(fn, single["value"], f"{n1} of {B * H} slices")
 
     threads = max(1, min(16, os.cpu_count() or 1, B * H))
     multi = None
@@ -614,7 +657,8 @@ def cpu_baseline(qn, kn, v, B, H, S, D, heads):
             t.join()
         dtm = time.perf_counter() - t0
         multi = {"value": 4.0 * threads * S * S * D / dtm / 1e12, "unit": "TFLOP/s",
-                 "cores": threads, "kind": kind,
+                 "cores": threads, "threads": threads, "cpu_model": single["cpu_model"],
+                 "kind": kind,
                  "sample": f"{threads} slices, one per thread (heads are independent)",
                  "seconds": round(dtm, 3)}
     return single, multi
@@ -697,10 +741,21 @@ def main():
     configs = None
     if not args.headline_only:
         torch.cuda.empty_cache()
-        configs = other_configs(c, cpu["value"] if cpu else None)
+        configs = other_configs(c)
 
     value = main_res["value"]
     peak = PEAK_TFLOPS[args.variant]
+    # GPU time of each configuration in the headline arithmetic next to the
+    # one-core CPU time of the same attention work.
+    speedups = None
+    if cpu and configs:
+        g = configs[args.variant]
+        gpu_s = {"c1": g["self256_B1"]["ms"], "c2": g["cross256x512_B2_cached"]["ms"],
+                 "c3": main_res["ms_per_step"], "c4": g["denoise_step_28_blocks"]["ms_per_step"],
+                 "c5": g["self6144_96x64_B2"]["ms"] + g["cross6144x512_B2"]["ms"]}
+        speedups = {k: {"cpu_s": cpu["per_config"][k]["seconds"], "gpu_ms": round(ms, 4),
+                        "speedup": round(cpu["per_config"][k]["seconds"] * 1e3 / ms, 1)}
+                    for k, ms in gpu_s.items()}
     line = {
         "metric": "attention TFLOP/s + % MFMA peak at 4096 tok B=2 H16 D128; speedup vs host CPU",
         "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -718,6 +773,7 @@ def main():
         "cpu_baseline_multicore": multi,
         "speedup_vs_cpu": None if cpu is None else round(value / cpu["value"], 1),
         "speedup_vs_cpu_multicore": None if multi is None else round(value / multi["value"], 1),
+        "speedup_per_config": speedups,
         "variants": variants,
         "dropin_c_abi": dropin,
         "configs": configs,
