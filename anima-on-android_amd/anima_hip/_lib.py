@@ -41,6 +41,8 @@ SIGNATURES = {
     "anima_hip_vt_padded_len": (ct.c_int64, [_I]),
     "anima_hip_pack_vt_dev": (_B, [_P, _P] + [_I] * 4 + [_I64P] * 2 + [_P]),
     "anima_hip_qk_prologue_dev": (_B, [_P] * 4 + [_I] * 4 + [_I64P] * 2 + [_F, _I, _P]),
+    "anima_hip_qkv_prologue_dev": (_B, [_P] * 3 + [ct.c_int64] + [_P] * 6 + [_I] * 4
+                                   + [_F, _I, _P]),
     "anima_hip_attention": (_B, [_P] * 7 + [_I] * 5 + [_F, _I]),
     "anima_hip_gemm_dev": (_B, [_P, ct.c_int64, _P, _I, ct.c_int64, _P, ct.c_int64] + [_I] * 3
                            + [_P]),

@@ -1094,6 +1094,44 @@ bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const 
     return launch_rows(p, pick_stream(stream));
 }
 
+bool anima_hip_qkv_prologue_dev(const float *q, const float *k, const float *v, int64_t ld,
+                                const float *q_norm_w, const float *k_norm_w,
+                                const float *freqs, void *qo, void *ko, uint16_t *vt, int B,
+                                int S, int H, int D, float eps, int mode, void *stream)
+{
+    if (!ready_for_device_call() || !check_dims(B, H, S, S, D))
+        return false;
+    AttnMode am;
+    if (!attn_mode_of(mode, D, "qkv_prologue_dev", am))
+        return false;
+    if (int64_t(B) * S * H == 0)
+        return true;
+    if (D != 128)
+        return fail("qkv_prologue_dev: D must be 128");
+    if (ld < 0 || (ld > 0 && ld < int64_t(H) * D))
+        return fail("qkv_prologue_dev: token row stride smaller than H*D");
+    if (!q || !k || !qo || !ko || (am != kAttnF32 && (!v || !vt)))
+        return fail("qkv_prologue_dev: null pointer");
+    PrepProblem p;
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.w[0] = q_norm_w;
+    p.w[1] = k_norm_w;
+    p.freqs = freqs;
+    p.qo = qo;
+    p.ko = ko;
+    p.vt = vt;
+    p.ld = ld > 0 ? ld : int64_t(H) * D;
+    p.B = B;
+    p.S = S;
+    p.H = H;
+    p.D = D;
+    p.eps = eps;
+    p.mode = am;
+    return launch_prep_qkv(p, pick_stream(stream));
+}
+
 bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, int64_t ldw,
                         float *c, int64_t ldc, int M, int N, int K, void *stream)
 {

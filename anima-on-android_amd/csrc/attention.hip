@@ -146,7 +146,44 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
 
     const void *kp = in.k_prep, *vp = in.v_prep;
     RowProblem pk{};
-    if (!prepared) {
+    const int64_t ld_q = in.ld_q > 0 ? in.ld_q : int64_t(H) * D;
+    const int64_t ld_kv = in.ld_kv > 0 ? in.ld_kv : int64_t(H) * D;
+    // Self-attention with q, k, v of one shape and row stride (the usual
+    // case, and the fused projection's column blocks): one launch prepares
+    // all three operands.
+    PrepProblem pp;
+    bool fused = !prepared && in.Bk == B && S_q == S_kv && ld_q == ld_kv;
+    if (fused) {
+        void *kn = cur;
+        void *vt = mode != kAttnF32 ? cur + round_up(prepared_k_bytes(B, S_kv, H, D, mode))
+                                    : nullptr;
+        pp.q = in.q;
+        pp.k = in.k;
+        pp.v = in.v;
+        pp.w[0] = in.q_norm_w;
+        pp.w[1] = in.k_norm_w;
+        pp.freqs = in.freqs;
+        pp.qo = qn;
+        pp.ko = kn;
+        pp.vt = static_cast<uint16_t *>(vt);
+        pp.ld = ld_q;
+        pp.B = B;
+        pp.S = S_q;
+        pp.H = H;
+        pp.D = D;
+        pp.eps = in.eps;
+        pp.mode = mode;
+        fused = prep_qkv_supported(pp);
+    }
+    if (fused) {
+        cur += round_up(prepared_k_bytes(B, S_kv, H, D, mode));
+        if (mode != kAttnF32)
+            cur += round_up(prepared_v_bytes(B, S_kv, H, D, mode));
+        if (!launch_prep_qkv(pp, st))
+            return false;
+        kp = pp.ko;
+        vp = mode != kAttnF32 ? static_cast<const void *>(pp.vt) : static_cast<const void *>(in.v);
+    } else if (!prepared) {
         void *kn = cur;
         cur += round_up(prepared_k_bytes(in.Bk, S_kv, H, D, mode));
         void *vt = mode != kAttnF32 ? static_cast<void *>(cur) : nullptr;
@@ -165,7 +202,7 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     // Q rows, and K rows unless prepared, in one launch.
     const RowProblem pq =
         qk_rows(in.q, in.q_norm_w, in.freqs, qn, B, S_q, H, D, in.eps, mode, in.ld_q);
-    if (!(prepared ? launch_rows(pq, st) : launch_rows_pair(pk, pq, st)))
+    if (!fused && !(prepared ? launch_rows(pq, st) : launch_rows_pair(pk, pq, st)))
         return false;
 
     const bool bcast = in.Bk == 1 && B > 1;

@@ -209,6 +209,27 @@ struct AttnInputs {
     // (dense); wider when they are column blocks of one fused projection.
     int64_t ld_q = 0, ld_kv = 0;
 };
+// A self-attention's three operands in one launch (prologue.hip): q and k
+// [B, S, H, 128] f32 with token rows ld elements apart and batch entries
+// S * ld apart, RMSNorm with w[0] / w[1] (null: weight 1) and RoPE with
+// freqs (or null), written dense to qo / ko as f32 rows (kAttnF32), bf16
+// rows (kAttnBF16) or [hi | lo] term rows (kAttnF32X3); in the last two
+// modes v is also packed into vt as the flash kernel's V^T (contiguous
+// [B][H][D or 2D][vt_padded_len(S)]).  Bit-identical to launch_rows +
+// launch_vt_pack(_terms) on the same inputs.
+struct PrepProblem {
+    const float *q = nullptr, *k = nullptr, *v = nullptr;
+    const float *w[2] = {nullptr, nullptr};
+    const float *freqs = nullptr;
+    void *qo = nullptr, *ko = nullptr;
+    uint16_t *vt = nullptr;
+    int64_t ld = 0;
+    int B = 0, S = 0, H = 0, D = 0;
+    float eps = 1e-6f;
+    AttnMode mode = kAttnF32;
+};
+bool prep_qkv_supported(const PrepProblem &p);  // D == 128, 16-byte alignment
+bool launch_prep_qkv(const PrepProblem &p, hipStream_t st);
 size_t prepared_k_bytes(int Bk, int S_kv, int H, int D, AttnMode mode);
 size_t prepared_v_bytes(int Bk, int S_kv, int H, int D, AttnMode mode);
 size_t attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D, AttnMode mode,

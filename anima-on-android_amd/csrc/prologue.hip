@@ -324,6 +324,180 @@ bool d128_eligible(const RowProblem &p)
            (!p.out_bf16 || p.lo_off % 4 == 0);
 }
 
+
+// ---- One launch for a self-attention's three operands ----
+// Q rows and K rows (RMSNorm, RoPE, written dense as f32, bf16 or bf16 term
+// rows) and, for the bf16-MFMA kernels, V packed as V^T (bf16 or hi/lo term
+// rows; the layout of vt_pack_kernel / vt_pack_terms_kernel).  The work is a
+// single grid of 64-row groups of Q, then of K, then 64-key tiles of V, so
+// the three streams share one ramp and one tail instead of three, and every
+// block keeps 32 KiB of loads in flight.  Row arithmetic is that of
+// rows_d128_block (bit-identical outputs); q, k and v are [B, S, H, 128]
+// views whose token rows are `ld` elements apart (column blocks of a fused
+// projection allowed), batch entries S * ld apart.
+constexpr int kPrepRows = 64;
+constexpr int kPrepPitch = 132;                   // floats per staged row
+constexpr int kPrepTW = 36;                       // 32-bit words per transposed V^T row
+constexpr int kPrepLds = 2 * 128 * kPrepTW;       // >= kPrepRows * kPrepPitch
+static_assert(kPrepLds >= kPrepRows * kPrepPitch, "LDS union");
+
+struct PrepArgs {
+    const float *x[2];  // q, k
+    void *out[2];       // dense rows: 128 f32, 128 bf16 or 256 bf16 (terms)
+    const float *w[2];  // RMSNorm weights or null
+    const float *freqs; // [S, 64, 2, 2] or null
+    const float *v;
+    unsigned short *vt; // [B*H][128 or 256 rows][sp]
+    int64_t ld, sp;
+    int rows;           // B*S*H (< 2^31, checked at launch)
+    int qk_units;       // 64-row groups per tensor
+    int S, H, n_vtiles;
+    float eps;
+};
+
+__device__ __forceinline__ unsigned pack_bf16x2(float a, float b)
+{
+    return unsigned(f32_to_bf16_rne(a)) | (unsigned(f32_to_bf16_rne(b)) << 16);
+}
+
+// OUT: 0 = f32 rows (no V), 1 = bf16 rows + bf16 V^T, 2 = term rows + term V^T.
+template <int OUT>
+__global__ __launch_bounds__(256) void prep_qkv_kernel(PrepArgs a)
+{
+    __shared__ __attribute__((aligned(16))) float lds[kPrepLds];
+    __shared__ float inv[kPrepRows];
+    const int t = threadIdx.x;
+    const int u = blockIdx.x;
+    if (u < 2 * a.qk_units) {
+        const int p = u >= a.qk_units ? 1 : 0;
+        const int r0 = (u - p * a.qk_units) * kPrepRows;
+        const float *x = a.x[p];
+        const int c4 = t & 31;
+        // 32-bit row arithmetic (rows < 2^31): the token index r / H and the
+        // head r % H of every row this thread loads.
+#pragma unroll
+        for (int i = 0; i < kPrepRows / 8; ++i) {
+            const int rr = (t >> 5) + 8 * i;
+            const int r = r0 + rr;
+            if (r < a.rows) {
+                const unsigned bs = unsigned(r) / unsigned(a.H);
+                const int h = r - int(bs) * a.H;
+                *reinterpret_cast<f32x4 *>(&lds[rr * kPrepPitch + 4 * c4]) =
+                    *reinterpret_cast<const f32x4 *>(x + int64_t(bs) * a.ld + h * 128 + 4 * c4);
+            }
+        }
+        __syncthreads();
+        if (t < kPrepRows) {
+            // One thread per row: the sum of squares in index order.
+            float ss = 0.0f;
+            const float *row = lds + t * kPrepPitch;
+#pragma unroll 8
+            for (int j = 0; j < 32; ++j) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(row + 4 * j);
+                ss = ss + v.x * v.x;
+                ss = ss + v.y * v.y;
+                ss = ss + v.z * v.z;
+                ss = ss + v.w * v.w;
+            }
+            inv[t] = inv_rms(ss, 128, a.eps);
+        }
+        __syncthreads();
+        const int p0 = 4 * (t & 15);
+        f32x4 wl = f32x4{1.f, 1.f, 1.f, 1.f}, wh = wl;
+        if (a.w[p]) {
+            wl = *reinterpret_cast<const f32x4 *>(a.w[p] + p0);
+            wh = *reinterpret_cast<const f32x4 *>(a.w[p] + 64 + p0);
+        }
+#pragma unroll
+        for (int i = 0; i < kPrepRows / 16; ++i) {
+            const int rr = (t >> 4) + 16 * i;
+            const int r = r0 + rr;
+            if (r >= a.rows)
+                continue;
+            const float *row = lds + rr * kPrepPitch;
+            const float fi = inv[rr];
+            f32x4 ya = *reinterpret_cast<const f32x4 *>(row + p0);
+            f32x4 yb = *reinterpret_cast<const f32x4 *>(row + 64 + p0);
+            ya = ya * fi;
+            yb = yb * fi;
+            if (a.w[p]) {
+                ya = ya * wl;
+                yb = yb * wh;
+            }
+            f32x4 lo = ya, hi = yb;
+            if (a.freqs) {
+                const int s = int((unsigned(r) / unsigned(a.H)) % unsigned(a.S));
+                const f32x4 *fq = reinterpret_cast<const f32x4 *>(a.freqs + int64_t(s) * 256 + 4 * p0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const f32x4 c = fq[e];  // [c00, c01, c10, c11] of pair p0 + e
+                    lo[e] = c.x * ya[e] + c.y * yb[e];
+                    hi[e] = c.z * ya[e] + c.w * yb[e];
+                }
+            }
+            if (OUT == 0) {
+                float *of = static_cast<float *>(a.out[p]) + int64_t(r) * 128 + p0;
+                *reinterpret_cast<f32x4 *>(of) = lo;
+                *reinterpret_cast<f32x4 *>(of + 64) = hi;
+            } else {
+                unsigned short *ob = static_cast<unsigned short *>(a.out[p]) +
+                                     int64_t(r) * (OUT == 2 ? 256 : 128) + p0;
+                store_bf16x4(ob, OUT == 2 ? 128 : 0, lo[0], lo[1], lo[2], lo[3]);
+                store_bf16x4(ob + 64, OUT == 2 ? 128 : 0, hi[0], hi[1], hi[2], hi[3]);
+            }
+        }
+        return;
+    }
+    if (OUT == 0)
+        return;
+    // V tile: 64 keys of one (batch, head), transposed through LDS into rows
+    // of V^T with keys in vt_key_pos order; adjacent key pairs share a word.
+    const unsigned vu = unsigned(u - 2 * a.qk_units);
+    const unsigned bh = vu / unsigned(a.n_vtiles);
+    const int tile = int(vu - bh * unsigned(a.n_vtiles));
+    const unsigned b = bh / unsigned(a.H);
+    const int h = int(bh - b * unsigned(a.H));
+    const int key0 = tile * 64;
+    const float *vp = a.v + int64_t(b) * a.S * a.ld + h * 128;
+    unsigned *Th = reinterpret_cast<unsigned *>(lds);
+    unsigned *Tl = Th + 128 * kPrepTW;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int f = t + 256 * i;  // (key pair, float4 column) of the tile
+        const int pr = f >> 5, c4 = f & 31;
+        const int k0 = key0 + 2 * pr, k1 = k0 + 1;
+        const f32x4 x0 = k0 < a.S
+                             ? *reinterpret_cast<const f32x4 *>(vp + int64_t(k0) * a.ld + 4 * c4)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 x1 = k1 < a.S
+                             ? *reinterpret_cast<const f32x4 *>(vp + int64_t(k1) * a.ld + 4 * c4)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+        const int wd = vt_key_pos(2 * pr) >> 1;  // word holding positions (2wd, 2wd+1)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const unsigned hw = pack_bf16x2(x0[e], x1[e]);
+            Th[(4 * c4 + e) * kPrepTW + wd] = hw;
+            if (OUT == 2) {
+                const float h0 = __uint_as_float(hw << 16), h1 = __uint_as_float(hw & 0xFFFF0000u);
+                Tl[(4 * c4 + e) * kPrepTW + wd] = pack_bf16x2(x0[e] - h0, x1[e] - h1);
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int vrows = OUT == 2 ? 256 : 128;
+    unsigned short *tp = a.vt + int64_t(bh) * vrows * a.sp + key0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int f = t + 256 * i;  // 16-byte chunk: d row, 8 keys
+        const int d = f >> 3, c = f & 7;
+        *reinterpret_cast<f32x4 *>(tp + d * a.sp + 8 * c) =
+            *reinterpret_cast<const f32x4 *>(&Th[d * kPrepTW + 4 * c]);
+        if (OUT == 2)
+            *reinterpret_cast<f32x4 *>(tp + (128 + d) * a.sp + 8 * c) =
+                *reinterpret_cast<const f32x4 *>(&Tl[d * kPrepTW + 4 * c]);
+    }
+}
+
 }  // namespace
 
 bool launch_rows_pair(const RowProblem &p1, const RowProblem &p2, hipStream_t st)
@@ -371,6 +545,59 @@ bool launch_rows(const RowProblem &p, hipStream_t st)
     const size_t shm = 4 * (nwords + (nwords & 1)) + sizeof(int64_t) * 2 * size_t(rb);
     hipLaunchKernelGGL(rows_kernel, dim3(unsigned(nblk)), dim3(256), shm, st, a);
     return hip_ok(hipGetLastError(), "rows_kernel launch");
+}
+
+
+bool prep_qkv_supported(const PrepProblem &p)
+{
+    const auto al = [](const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    return p.D == 128 && p.ld % 4 == 0 && p.ld >= int64_t(p.H) * p.D && al(p.q) && al(p.k) &&
+           al(p.qo) && al(p.ko) && (!p.w[0] || al(p.w[0])) && (!p.w[1] || al(p.w[1])) &&
+           (!p.freqs || al(p.freqs)) && (p.mode == kAttnF32 || (al(p.v) && al(p.vt)));
+}
+
+bool launch_prep_qkv(const PrepProblem &p, hipStream_t st)
+{
+    const int64_t rows = int64_t(p.B) * p.S * p.H;
+    if (rows == 0)
+        return true;
+    if (!prep_qkv_supported(p))
+        return fail("prep_qkv: D must be 128 with 16-byte aligned operands and row strides");
+    PrepArgs a;
+    a.x[0] = p.q;
+    a.x[1] = p.k;
+    a.out[0] = p.qo;
+    a.out[1] = p.ko;
+    a.w[0] = p.w[0];
+    a.w[1] = p.w[1];
+    a.freqs = p.freqs;
+    a.v = p.v;
+    a.vt = p.vt;
+    const int64_t sp = vt_padded_len(p.S);
+    const int64_t nblk = 2 * ((rows + kPrepRows - 1) / kPrepRows) +
+                         (p.mode == kAttnF32 ? 0 : int64_t(p.B) * p.H * (sp / kVtTile));
+    if (rows > INT32_MAX - kPrepRows || nblk > INT32_MAX)
+        return fail("prep_qkv: problem too large for one launch");
+    a.ld = p.ld;
+    a.rows = int(rows);
+    a.sp = sp;
+    a.qk_units = int((rows + kPrepRows - 1) / kPrepRows);
+    a.S = p.S;
+    a.H = p.H;
+    a.n_vtiles = int(sp / kVtTile);
+    a.eps = p.eps;
+    switch (p.mode) {
+    case kAttnF32:
+        hipLaunchKernelGGL(prep_qkv_kernel<0>, dim3(unsigned(nblk)), dim3(256), 0, st, a);
+        break;
+    case kAttnBF16:
+        hipLaunchKernelGGL(prep_qkv_kernel<1>, dim3(unsigned(nblk)), dim3(256), 0, st, a);
+        break;
+    default:
+        hipLaunchKernelGGL(prep_qkv_kernel<2>, dim3(unsigned(nblk)), dim3(256), 0, st, a);
+        break;
+    }
+    return hip_ok(hipGetLastError(), "prep_qkv_kernel launch");
 }
 
 }  // namespace anima_hip

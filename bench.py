@@ -7,8 +7,8 @@ at 1024x1024 output, B=2 (CFG cond+uncond), H=16, S_q=S_kv=4096 tokens
 in NumpyDiT's [B,S,H,D] layout, already resident in HBM.
 
 One step = the whole device-resident hot path over that batch:
-  prologue(q) + prologue(k)   per-head RMSNorm (w=1, eps 1e-6) + 3D RoPE
-  [bf16 / f32x3: V -> packed V^T]
+  prologue (one launch)       per-head RMSNorm (w=1, eps 1e-6) + 3D RoPE of q
+                              and k [bf16 / f32x3: and V -> packed V^T]
   flash attention             softmax(QK^T/sqrt(D)) V, output in [B,S,H,D]
 FLOPs per step = 4*B*H*S_q*S_kv*D (softmax and prologue not counted).
 
@@ -50,10 +50,11 @@ PEAK_BASIS = {"f32": "f32 dense MFMA peak (v_mfma_f32_32x32x2_f32)",
 MODE = {"f32": 0, "bf16": 1, "f32x3": 2}
 KERNEL = {"f32": "flash_f32_d128", "bf16": "flash_bf16_d128", "f32x3": "flash_x3_d128"}
 VARIANTS = ("f32x3", "f32", "bf16")
-STEP = {"f32": "qk prologue (RMSNorm+RoPE) x2 + flash attention",
-        "bf16": "qk prologue (RMSNorm+RoPE, bf16 out) x2 + V^T bf16 pack + flash attention",
-        "f32x3": "qk prologue (RMSNorm+RoPE, bf16 hi/lo term rows) x2 + V^T term pack + flash "
-                 "attention"}
+STEP = {"f32": "one-launch prologue (q, k RMSNorm+RoPE) + flash attention",
+        "bf16": "one-launch prologue (q, k RMSNorm+RoPE as bf16 rows, V^T bf16 pack) + flash "
+                "attention",
+        "f32x3": "one-launch prologue (q, k RMSNorm+RoPE as bf16 hi/lo term rows, V^T term "
+                 "pack) + flash attention"}
 PREWARM_S = 2.0  # seconds of untimed steps before the warmup steps of each headline run
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "flash_traffic.json")
 WORKLOAD = "self-attention 4096x4096, B=2 H=16 D=128 (64x64 grid, RMSNorm+3D RoPE)"
@@ -164,12 +165,6 @@ def headline(c, variant, q, k, v, freqs, ones, steps, warmup):
     bshd = _lib.strides([S * H * D, D, H * D])  # [B,S,H,D] viewed as [B,H,S,D]
     terms = _lib.strides([S * H * w * D, w * D, H * w * D])
     scale = ct.c_float(1.0 / math.sqrt(D))
-    flags = 1 | (2 if bf16 else 4 if x3 else 0)  # RMSNorm (+ bf16 output or term rows)
-
-    def prologue(x, y):
-        _lib.check(lib.anima_hip_qk_prologue_dev(x.data_ptr(), y.data_ptr(), ones.data_ptr(),
-                                                 freqs.data_ptr(), B, S, H, D, bshd, terms,
-                                                 ct.c_float(1e-6), flags, c.stp), "qk_prologue")
 
     def flash():
         if x3:
@@ -187,14 +182,12 @@ def headline(c, variant, q, k, v, freqs, ones, steps, warmup):
         _lib.check(ok, f"flash_{variant}")
 
     def step(ev=None):
-        prologue(q, qn)
-        prologue(k, kn)
-        if bf16:
-            _lib.check(lib.anima_hip_pack_vt_dev(v.data_ptr(), vt.data_ptr(), B, H, S, D, bshd,
-                                                 None, c.stp), "pack_vt")
-        elif x3:
-            _lib.check(lib.anima_hip_pack_vt_terms_dev(v.data_ptr(), vt.data_ptr(), B, H, S, D,
-                                                       bshd, None, c.stp), "pack_vt_terms")
+        # q, k rows and V^T in one launch (anima_hip_qkv_prologue_dev).
+        _lib.check(lib.anima_hip_qkv_prologue_dev(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), 0, ones.data_ptr(), ones.data_ptr(),
+            freqs.data_ptr(), qn.data_ptr(), kn.data_ptr(),
+            vt.data_ptr() if vt is not None else None, B, S, H, D, ct.c_float(1e-6),
+            MODE[variant], c.stp), "qkv_prologue")
         if ev is not None:
             ev[0].record(c.st)
         flash()

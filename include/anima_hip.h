@@ -195,6 +195,24 @@ bool anima_hip_qk_prologue_dev(const float *x, void *out, const float *w, const 
                                const int64_t *x_strides, const int64_t *out_strides,
                                float eps, int flags, void *stream);
 
+/* All three operands of a self-attention's flash call in one launch: the q
+ * and k rows of anima_hip_qk_prologue_dev (RMSNorm with q_norm_w / k_norm_w,
+ * NULL meaning weight 1, then RoPE with freqs [S, D/2, 2, 2] or NULL) and, in
+ * the bf16 and f32x3 modes, V packed as anima_hip_pack_vt_dev /
+ * anima_hip_pack_vt_terms_dev pack it.  This is NumpyAttention.forward's
+ * q/k/v preparation (anima_rt/scripts/numpy_dit.py:283-291) for the
+ * attention kernels.  q, k, v: [B, S, H, D] f32 views with token rows ld
+ * elements apart (ld = 0: H*D; wider for column blocks of one fused
+ * projection), batch entries S*ld apart; D == 128; 16-byte aligned.
+ * Outputs, dense: qo, ko as [B, S, H, D] f32 (ANIMA_HIP_F32), [B, S, H, D]
+ * bf16 (ANIMA_HIP_BF16) or [B, S, H, 2D] bf16 term rows (ANIMA_HIP_F32X3);
+ * vt as [B, H, D (bf16) or 2D (terms), anima_hip_vt_padded_len(S)] (unused
+ * and may be NULL in f32 mode).  Bit-identical to the separate entries. */
+bool anima_hip_qkv_prologue_dev(const float *q, const float *k, const float *v, int64_t ld,
+                                const float *q_norm_w, const float *k_norm_w,
+                                const float *freqs, void *qo, void *ko, uint16_t *vt, int B,
+                                int S, int H, int D, float eps, int mode, void *stream);
+
 /* C[M,N] = A[M,K] . W[N,K]^T on device memory; W is bf16 bit patterns when
  * w_bf16 != 0, else f32; leading dimensions in elements. */
 bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, int64_t ldw,
