@@ -131,13 +131,51 @@ bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, 
 uint16_t *launch_split_interleaved(const float *a, int64_t lda, int M, int K, void *scratch,
                                    size_t scratch_bytes, hipStream_t st);
 
+// Small-M bf16 GEMM (gemm_bf16.hip): C[M,N] = a0 . W^T (+ a1 . W^T) with bf16
+// activation terms a0 (a1 null for one term) [M][lda], bf16 W [N][ldw], f32
+// C [M][ldc], for M <= 1024 and K a multiple of 64 (K per term), split over K
+// into a workspace of gemm_bf16_workspace_bytes() (at most 16 MiB) and
+// reduced in split order.
+size_t gemm_bf16_workspace_bytes(int M, int N, int K);
+constexpr size_t kGemmBf16MaxWorkspace = size_t(16) << 20;
+bool gemm_bf16_supported(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
+                         const void *a0, const void *a1, const void *w, const void *c,
+                         size_t ws_bytes);
+bool launch_gemm_bf16(const uint16_t *a0, const uint16_t *a1, int64_t lda, const uint16_t *w,
+                      int64_t ldw, float *c, int64_t ldc, int M, int N, int K, void *ws,
+                      size_t ws_bytes, hipStream_t st);
+// The same product left as *parts dense [M][N] planes at `planes` (at least
+// gemm_bf16_workspace_bytes(M, N, K), and M*N*4, bytes), C their sum in
+// plane order: the consumer adds them (one plane when K is not split).
+bool launch_gemm_bf16_planes(const uint16_t *a0, const uint16_t *a1, int64_t lda,
+                             const uint16_t *w, int64_t ldw, float *planes, size_t planes_bytes,
+                             int M, int N, int K, int *parts, hipStream_t st);
+
 // The same product on A already split into bf16 terms hi (and lo, or null for
 // one term), rows of linear_terms_ld(K) elements zero-padded past K.
 int64_t linear_terms_ld(int K);
 bool linear_terms_supported(int M, int N, int K, const void *w, int64_t ldw, const float *c,
                             int64_t ldc);
+// With a workspace of gemm_bf16_workspace_bytes(M, N, K) bytes, the shapes
+// small_m_path() names run on the small-M kernel instead of the library GEMM.
+bool small_m_path(int M, int K, bool two_terms);
 bool launch_linear_terms(const uint16_t *hi, const uint16_t *lo, const uint16_t *w, int64_t ldw,
-                         float *c, int64_t ldc, int M, int N, int K, hipStream_t st);
+                         float *c, int64_t ldc, int M, int N, int K, hipStream_t st,
+                         void *ws = nullptr, size_t ws_bytes = 0);
+// C[M,N] = hi . W^T + lo . W^T on [hi | lo] rows (row stride ld_t, K
+// elements each, ld_t == linear_terms_ld(2K) on the library path) and [W | W]
+// weight rows: the small-M kernel's two-term product when it applies, else
+// one library product over the doubled rows (K' = 2K).
+bool launch_linear_pair(const uint16_t *terms, int64_t ld_t, int K, const uint16_t *w,
+                        int64_t ldw, float *c, int64_t ldc, int M, int N, hipStream_t st,
+                        void *ws = nullptr, size_t ws_bytes = 0);
+// launch_linear_terms (lo null, K per row) or launch_linear_pair (pair: [hi |
+// lo] rows of ld_t = 2K) into *parts dense [M][N] planes at `planes`
+// (planes_bytes of room), C their sum in plane order: the small-M kernel's
+// split-K partials left for the consumer, else one plane from the library.
+bool launch_linear_planes(const uint16_t *terms, int64_t ld_t, int K, bool pair,
+                          const uint16_t *w, int64_t ldw, float *planes, size_t planes_bytes,
+                          int M, int N, int *parts, hipStream_t st);
 
 // C[M,N] = hi . W^T rounded to bf16 (C bf16, ldc % 8 == 0): one product on
 // activations already rounded to bf16.
@@ -264,14 +302,16 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
 // terms (hi, and lo unless null) of the projection GEMM's input.  Row r
 // belongs to batch entry r / S, whose shift and scale are mod[b*mod_ld + :Dm]
 // and mod[b*mod_ld + Dm : 2*Dm].
-// res_y != null: first x += gate[b] * res_y (gate at res_gate + b*res_ld,
-// res_y dense [M][Dm]), written back to x (res_x must be x).  tld: term row
-// stride in elements (0: linear_terms_ld(Dm)); [hi | lo] rows in one buffer
-// use tld = 2 * linear_terms_ld(Dm) and lo = hi + linear_terms_ld(Dm).
+// res_y != null: first x += gate[b] * y (gate at res_gate + b*res_ld; y the
+// sum of res_parts dense [M][Dm] planes at res_y, in plane order), written
+// back to x (res_x must be x).  tld: term row stride in elements (0:
+// linear_terms_ld(Dm)); [hi | lo] rows in one buffer use tld = 2 *
+// linear_terms_ld(Dm) and lo = hi + linear_terms_ld(Dm).
 bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t mod_ld,
                         uint16_t *hi, uint16_t *lo, int64_t M, int S, int Dm, float eps,
                         hipStream_t st, float *res_x = nullptr, const float *res_y = nullptr,
-                        const float *res_gate = nullptr, int64_t res_ld = 0, int64_t tld = 0);
+                        const float *res_gate = nullptr, int64_t res_ld = 0, int64_t tld = 0,
+                        int res_parts = 1);
 // x += gate[b] * y for rows of S per batch entry.
 bool launch_gate_residual(float *x, const float *y, const float *mod, int64_t M, int S, int Dm,
                           hipStream_t st);

@@ -504,7 +504,7 @@ void grid_of(int T, int H, int W, int &Hp, int &Wp, int64_t &S)
 //   cross: q [M][HD] f32,    o [M][HD] f32, attention scratch, o's terms;
 //   mlp:   h [M][hidden] (f32, bf16 in bf16 mode), GELU terms [M][ld_hid].
 struct SubLayout {
-    size_t terms, a, b, attn, lin, total;
+    size_t terms, a, b, attn, lin, ws, total;
 };
 
 SubLayout sub_layout(const anima_hip_dit *d, int B, int64_t S, int kind)
@@ -526,7 +526,10 @@ SubLayout sub_layout(const anima_hip_dit *d, int B, int64_t S, int kind)
                                                                  c.head_dim, d->attn, true));
         l.lin = round_up256(M * size_t(linear_terms_ld(int(HD))) * 2 * d->reps);
     }
-    l.total = l.terms + l.a + l.b + l.attn + l.lin;
+    // Split-K partials of the small-M GEMM, right after lin (the bf16 output
+    // projection hands launch_linear both as one scratch).
+    l.ws = M <= 1024 ? kGemmBf16MaxWorkspace : 0;
+    l.total = l.terms + l.a + l.b + l.attn + l.lin + l.ws;
     return l;
 }
 
@@ -541,7 +544,9 @@ DitScratch dit_scratch(const anima_hip_dit *d, int B, int64_t S)
     const int64_t M = int64_t(B) * S;
     DitScratch s{};
     s.x = round_up256(size_t(M) * c.dim * 4);
-    s.y = s.x;
+    // The pending output projection: one [M][D] plane, or up to 16 MiB of
+    // the small-M GEMM's split-K partial planes, added by the next LayerNorm.
+    s.y = std::max(s.x, M <= 1024 ? kGemmBf16MaxWorkspace : size_t(0));
     s.patch = round_up256(size_t(M) * d->kp_in * 2) * 2;
     s.f = round_up256(size_t(M) * 4 * c.out_channels * 4);
     const SubLayout self = sub_layout(d, B, S, 0), cross = sub_layout(d, B, S, 1),
@@ -564,35 +569,58 @@ bool check_cfg(const anima_hip_dit_config &c)
     return true;
 }
 
-// x += gate * y of the pending sub-layer (when pend_y), then LayerNorm +
-// modulate into activation terms: [hi | lo] rows in f32 mode, hi rows in
-// bf16 mode (row stride ld_d either way).
+// x += gate * y of the pending sub-layer (when pend_y; y the sum of
+// pend_parts [M][D] planes), then LayerNorm + modulate into activation terms:
+// [hi | lo] rows in f32 mode, hi rows in bf16 mode (row stride ld_d either
+// way).
 bool dit_norm(const anima_hip_dit *d, float *x, const float *mod, const float *pend_y,
-              const float *pend_mod, uint16_t *terms, int64_t M, int S, hipStream_t st)
+              int pend_parts, const float *pend_mod, uint16_t *terms, int64_t M, int S,
+              hipStream_t st)
 {
     const int D = d->cfg.dim;
     uint16_t *lo = d->reps == 2 ? terms + linear_terms_ld(D) : nullptr;
     return launch_ln_modulate(x, D, mod, 3 * int64_t(D), terms, lo, M, S, D, 1e-6f, st, x, pend_y,
                               pend_y ? pend_mod + 2 * int64_t(D) : nullptr, 3 * int64_t(D),
-                              d->ld_d);
+                              d->ld_d, pend_parts);
 }
 
-// out [M][N] = a . W^T for f32 activations a [M][K]: split into terms here
-// ([hi | lo] rows with the repeated weight in f32 mode), one product.
+// out [M][N] = terms . W^T for activation terms of row stride ld_t: [hi | lo]
+// rows and [W | W] weight rows in f32 mode (a two-term product), hi rows in
+// bf16 mode.  ws: the small-M GEMM's split-K partials.
+bool dit_product(const anima_hip_dit *d, const uint16_t *terms, int64_t ld_t, const uint16_t *w,
+                 int64_t ld_w, float *out, int N, int64_t M, void *ws, size_t ws_bytes,
+                 hipStream_t st)
+{
+    if (d->reps == 2)
+        return launch_linear_pair(terms, ld_t, int(ld_t / 2), w, ld_w, out, N, int(M), N, st, ws,
+                                  ws_bytes);
+    return launch_linear_terms(terms, nullptr, w, ld_w, out, N, int(M), N, int(ld_t), st, ws,
+                               ws_bytes);
+}
+
+// The sub-layer's output projection y [M][N] = a . W^T for f32 activations a
+// [M][K], left as *parts planes at y (y_bytes of room) for the next
+// LayerNorm to add: split into terms in lin here, one product.  lin holds the
+// terms and, right after them, ws_bytes of scratch.
 bool dit_linear(const anima_hip_dit *d, const float *a, int K, const uint16_t *w, int64_t ld_w,
-                float *out, int N, int64_t M, void *lin, size_t lin_bytes, hipStream_t st)
+                float *y, size_t y_bytes, int *parts, int N, int64_t M, void *lin,
+                size_t lin_bytes, size_t ws_bytes, hipStream_t st)
 {
     if (d->reps == 2) {
         const uint16_t *t = launch_split_interleaved(a, K, int(M), K, lin, lin_bytes, st);
-        return t && launch_linear_terms(t, nullptr, w, ld_w, out, N, int(M), N, int(ld_w), st);
+        return t && launch_linear_planes(t, 2 * linear_terms_ld(K), int(linear_terms_ld(K)), true,
+                                         w, ld_w, y, y_bytes, int(M), N, parts, st);
     }
-    return launch_linear(a, K, w, ld_w, out, N, int(M), N, K, false, lin, lin_bytes, st);
+    *parts = 1;
+    return launch_linear(a, K, w, ld_w, y, N, int(M), N, K, false, lin, lin_bytes + ws_bytes, st);
 }
 
 // One sub-layer of block bw on the residual stream x (kind as sub_layout),
-// after applying the pending residual; its output projection goes to y.
+// after applying the pending residual (pend_parts planes at pend_y); its
+// output projection goes to y as *y_parts planes (y_bytes of room).
 bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, float *x,
-                  const float *mod, const float *pend_y, const float *pend_mod, float *y, int B,
+                  const float *mod, const float *pend_y, int pend_parts, const float *pend_mod,
+                  float *y, size_t y_bytes, int *y_parts, int B,
                   int64_t S, const float *freqs, void *arena, hipStream_t st)
 {
     const anima_hip_dit_config &c = d->cfg;
@@ -602,16 +630,17 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
     char *cur = static_cast<char *>(arena);
     uint16_t *terms = reinterpret_cast<uint16_t *>(cur);
     char *ra = cur + l.terms, *rb = ra + l.a, *rattn = rb + l.b, *rlin = rattn + l.attn;
-    if (!dit_norm(d, x, mod, pend_y, pend_mod, terms, M, int(S), st))
+    char *rws = rlin + l.lin;
+    if (!dit_norm(d, x, mod, pend_y, pend_parts, pend_mod, terms, M, int(S), st))
         return false;
     if (kind == 2) {  // NumpyMLP (numpy_dit.py:304-317)
         const int hid = c.mlp_hidden;
         const bool ok1 = d->bf16 ? launch_linear_terms_bf16out(terms, bw.w_fc1, d->ld_d,
                                                                reinterpret_cast<uint16_t *>(ra),
                                                                hid, int(M), hid, D, st)
-                                 : launch_linear_terms(terms, nullptr, bw.w_fc1, d->ld_d,
-                                                       reinterpret_cast<float *>(ra), hid,
-                                                       int(M), hid, int(d->ld_d), st);
+                                 : dit_product(d, terms, d->ld_d, bw.w_fc1, d->ld_d,
+                                               reinterpret_cast<float *>(ra), hid, M, rws, l.ws,
+                                               st);
         if (!ok1)
             return false;
         GeluArgs ga;
@@ -626,8 +655,9 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
         else
             hipLaunchKernelGGL(gelu_terms_kernel<false>, dim3(grid1(ga.n8)), dim3(256), 0, st, ga);
         return hip_ok(hipGetLastError(), "gelu_terms_kernel launch") &&
-               launch_linear_terms(reinterpret_cast<const uint16_t *>(rb), nullptr, bw.w_fc2,
-                                   d->ld_hid, y, D, int(M), D, int(d->ld_hid), st);
+               launch_linear_planes(reinterpret_cast<const uint16_t *>(rb), d->ld_hid,
+                                    int(d->ld_hid / d->reps), d->reps == 2, bw.w_fc2, d->ld_hid,
+                                    y, y_bytes, int(M), D, y_parts, st);
     }
     // NumpyAttention.forward (numpy_dit.py:268-297): self-attention projects
     // q, k and v in one product; cross-attention projects q and reads the
@@ -642,8 +672,7 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
     in.mode = d->attn;
     in.out = o;
     if (kind == 0) {
-        if (!launch_linear_terms(terms, nullptr, bw.w_qkv, d->ld_d, proj, 3 * HD, int(M), 3 * HD,
-                                 int(d->ld_d), st))
+        if (!dit_product(d, terms, d->ld_d, bw.w_qkv, d->ld_d, proj, 3 * HD, M, rws, l.ws, st))
             return false;
         in.q = proj;
         in.k = proj + HD;
@@ -655,8 +684,7 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
         in.Bk = B;
         in.S_kv = int(S);
     } else {
-        if (!launch_linear_terms(terms, nullptr, bw.w_cq, d->ld_d, proj, HD, int(M), HD,
-                                 int(d->ld_d), st))
+        if (!dit_product(d, terms, d->ld_d, bw.w_cq, d->ld_d, proj, HD, M, rws, l.ws, st))
             return false;
         in.q = proj;
         in.q_norm_w = bw.cx_qn;
@@ -666,7 +694,8 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
         in.S_kv = d->ctx_S;
     }
     return run_attention(in, rattn, st) &&
-           dit_linear(d, o, HD, kind == 0 ? bw.w_o : bw.w_co, d->ld_hd, y, D, M, rlin, l.lin, st);
+           dit_linear(d, o, HD, kind == 0 ? bw.w_o : bw.w_co, d->ld_hd, y, y_bytes, y_parts, D, M,
+                      rlin, l.lin, l.ws, st);
 }
 
 // The forward pass on B batch entries of the latent x ([B][C][T][H][W] with
@@ -762,13 +791,16 @@ bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, i
     // (or the final layer's) LayerNorm pass applies x += gate * yp first.
     const int64_t mod_stride = int64_t(c.max_batch) * 3 * D;  // one modulation's rows
     const float *pend_mod = nullptr;                           // modulation owning yp
+    int pend_parts = 1;                                        // planes of yp
     for (int i = 0; i < c.blocks; ++i) {
         for (int kind = 0; kind < 3; ++kind) {
             const float *mod = d->mods + (3 * i + kind) * mod_stride;
-            if (!dit_sublayer(d, d->blk[i], kind, xr, mod, pend_mod ? yp : nullptr, pend_mod, yp,
-                              B, S, freqs, arena, st))
+            int parts = 1;
+            if (!dit_sublayer(d, d->blk[i], kind, xr, mod, pend_mod ? yp : nullptr, pend_parts,
+                              pend_mod, yp, s.y, &parts, B, S, freqs, arena, st))
                 return false;
             pend_mod = mod;
+            pend_parts = parts;
         }
     }
 
@@ -779,7 +811,8 @@ bool dit_run(anima_hip_dit *d, const float *x, int64_t xb, const float *sigma, i
     const float *fmod = d->mods + int64_t(3 * c.blocks) * mod_stride;
     if (!launch_ln_modulate(xr, D, fmod, 3 * int64_t(D), thi, tlo, M, int(S), D, 1e-6f, st, xr,
                             pend_mod ? yp : nullptr,
-                            pend_mod ? pend_mod + 2 * int64_t(D) : nullptr, 3 * int64_t(D)) ||
+                            pend_mod ? pend_mod + 2 * int64_t(D) : nullptr, 3 * int64_t(D), 0,
+                            pend_parts) ||
         !launch_linear_terms(thi, tlo, d->fin_lin, D, f, 4 * c.out_channels, int(M),
                              4 * c.out_channels, D, st))
         return false;

@@ -192,9 +192,21 @@ bool linear_terms_supported(int M, int N, int K, const void *w, int64_t ldw, con
     return lt_plan(M, N, K, padded_k(K), ldw, ldc) != nullptr;
 }
 
-bool launch_linear_terms(const uint16_t *hi, const uint16_t *lo, const uint16_t *w, int64_t ldw,
-                         float *c, int64_t ldc, int M, int N, int K, hipStream_t st)
+// The small-M kernel (gemm_bf16.hip) beats the library GEMM at M <= 1024 on
+// two-term products (each W chunk staged once for both terms) and on one-term
+// products with K >= 8192 (measured at M = 512); elsewhere the library runs.
+bool small_m_path(int M, int K, bool two_terms)
 {
+    return M > 0 && M <= 1024 && K % 64 == 0 && (two_terms || K >= 8192);
+}
+
+bool launch_linear_terms(const uint16_t *hi, const uint16_t *lo, const uint16_t *w, int64_t ldw,
+                         float *c, int64_t ldc, int M, int N, int K, hipStream_t st, void *ws,
+                         size_t ws_bytes)
+{
+    if (ws && small_m_path(M, K, lo != nullptr) &&
+        gemm_bf16_supported(M, N, K, padded_k(K), ldw, ldc, hi, lo, w, c, ws_bytes))
+        return launch_gemm_bf16(hi, lo, padded_k(K), w, ldw, c, ldc, M, N, K, ws, ws_bytes, st);
     if (!linear_terms_supported(M, N, K, w, ldw, c, ldc))
         return fail("linear: no bf16 GEMM for this shape");
     if ((reinterpret_cast<uintptr_t>(hi) & 15u) != 0 || (reinterpret_cast<uintptr_t>(lo) & 15u) != 0)
@@ -204,6 +216,34 @@ bool launch_linear_terms(const uint16_t *hi, const uint16_t *lo, const uint16_t 
     if (!lt_matmul(plan, w, hi, c, 0.0f, st))
         return false;
     return !lo || lt_matmul(plan, w, lo, c, 1.0f, st);
+}
+
+bool launch_linear_pair(const uint16_t *terms, int64_t ld_t, int K, const uint16_t *w,
+                        int64_t ldw, float *c, int64_t ldc, int M, int N, hipStream_t st, void *ws,
+                        size_t ws_bytes)
+{
+    if (ws && small_m_path(M, K, true) &&
+        gemm_bf16_supported(M, N, K, ld_t, ldw, ldc, terms, terms + K, w, c, ws_bytes))
+        return launch_gemm_bf16(terms, terms + K, ld_t, w, ldw, c, ldc, M, N, K, ws, ws_bytes, st);
+    if (ld_t != padded_k(2 * K))
+        return fail("linear: [hi | lo] rows must be 2K elements long");
+    return launch_linear_terms(terms, nullptr, w, ldw, c, ldc, M, N, 2 * K, st);
+}
+
+bool launch_linear_planes(const uint16_t *terms, int64_t ld_t, int K, bool pair,
+                          const uint16_t *w, int64_t ldw, float *planes, size_t planes_bytes,
+                          int M, int N, int *parts, hipStream_t st)
+{
+    const uint16_t *lo = pair ? terms + K : nullptr;
+    const int64_t lda = pair ? ld_t : padded_k(K);
+    if ((pair || ld_t == padded_k(K)) && small_m_path(M, K, pair) &&
+        gemm_bf16_supported(M, N, K, lda, ldw, N, terms, lo, w, planes, planes_bytes) &&
+        planes_bytes >= size_t(M) * N * sizeof(float))
+        return launch_gemm_bf16_planes(terms, lo, lda, w, ldw, planes, planes_bytes, M, N, K,
+                                       parts, st);
+    *parts = 1;
+    return pair ? launch_linear_pair(terms, ld_t, K, w, ldw, planes, N, M, N, st)
+                : launch_linear_terms(terms, nullptr, w, ldw, planes, N, M, N, K, st);
 }
 
 uint16_t *launch_split_interleaved(const float *a, int64_t lda, int M, int K, void *scratch,
@@ -252,11 +292,13 @@ bool launch_linear_terms_bf16out(const uint16_t *hi, const uint16_t *w, int64_t 
     return lt_matmul(plan, w, hi, c, 0.0f, st);
 }
 
+// Shapes of the small-M kernel also hold its split-K partials, after the terms.
 size_t linear_scratch_bytes(int M, int K, bool exact)
 {
     if (M <= 0 || K <= 0)
         return 0;
-    return round_up256(size_t(M) * size_t(padded_k(K)) * 2) * (exact ? 2 : 1);
+    return round_up256(size_t(M) * size_t(padded_k(K)) * 2) * (exact ? 2 : 1) +
+           (small_m_path(M, K, exact) ? kGemmBf16MaxWorkspace : 0);
 }
 
 bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *c,
@@ -300,6 +342,17 @@ bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, 
     hipLaunchKernelGGL(split_kernel, dim3(unsigned(nblk)), dim3(256), 0, st, s);
     if (!hip_ok(hipGetLastError(), "split_kernel launch"))
         return false;
+    // Small M: both terms in one product of the small-M kernel, its partials
+    // after the terms in the scratch.
+    const size_t terms = round_up256(size_t(M) * kp * 2) * (exact ? 2 : 1);
+    if (small_m_path(M, K, exact)) {
+        void *ws = static_cast<char *>(scratch) + terms;
+        const size_t wsb = scratch_bytes - terms;
+        const uint16_t *hi = reinterpret_cast<const uint16_t *>(s.hi);
+        const uint16_t *lo = reinterpret_cast<const uint16_t *>(s.lo);
+        if (gemm_bf16_supported(M, N, K, kp, ldw, ldc, hi, lo, w, c, wsb))
+            return launch_gemm_bf16(hi, lo, kp, w, ldw, c, ldc, M, N, K, ws, wsb, st);
+    }
     std::lock_guard<std::mutex> g(g_lt_mu);
     if (!lt_matmul(plan, w, s.hi, c, 0.0f, st))
         return false;

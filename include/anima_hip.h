@@ -228,8 +228,12 @@ bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, 
  *                        error <= 2^-16 |a|), f32 accumulation;
  *   mode ANIMA_HIP_BF16: a is rounded to bf16 (<= 2^-8 |a|).
  * scratch: anima_hip_linear_scratch_bytes(M, K, mode) bytes of device memory,
- * 16-byte aligned; nothing is allocated.  Shapes without a library solution
- * (e.g. ldw not a multiple of 8) run the exact f32-MFMA kernel instead. */
+ * 16-byte aligned; nothing is allocated.  At M <= 1024 with K a multiple of 64
+ * (f32 modes, or bf16 mode with K >= 8192) the size includes 16 MiB for the
+ * split-K partials of the hand-written small-M GEMM, which then runs instead
+ * of the library GEMM; the partials are added in a fixed order, so results
+ * are deterministic.  Shapes without a library solution (e.g. ldw not a
+ * multiple of 8) run the exact f32-MFMA kernel instead. */
 size_t anima_hip_linear_scratch_bytes(int M, int K, int mode);
 bool anima_hip_linear_dev(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *c,
                           int64_t ldc, int M, int N, int K, int mode, void *scratch,

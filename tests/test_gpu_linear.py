@@ -77,6 +77,33 @@ def test_linear_modes(M, N, K, lda):
         assert e32 * 20 < e16
 
 
+# Shapes of the small-M kernel (M <= 1024, K a multiple of 64; split over K
+# with a deterministic reduction): the 256x256 image's fc2 (K = 8192, the
+# f32 mode's two terms doubling it), q/k/v and output projections at M = 512,
+# and ragged M and N (tails clamped).  Rows are sampled for the oracle.
+SMALL_M = [(512, 2048, 8192), (512, 6144, 2048), (512, 2048, 2048), (77, 300, 512),
+           (1000, 2052, 4096), (8, 128, 64), (512, 2048, 16384), (256, 384, 576),
+           (640, 1024, 1536)]
+
+
+@pytest.mark.parametrize("M,N,K", SMALL_M)
+def test_small_m_kernel_vs_oracle(M, N, K):
+    a, w = _data(M * 7 + N + K, M, N, K)
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M).integers(0, M, 14)]))
+    ref = oracle.gemm_bf16(np.ascontiguousarray(a[rows]), w)
+    print(f"small-M linear M={M} N={N} K={K}", flush=True)
+    e = {}
+    for mode, tol in ((rt.F32, REL_F32), (rt.BF16, REL_BF16)):
+        out = run_linear(a, w, mode)
+        assert np.isfinite(out).all()
+        e[mode] = rel_err(out[rows], ref)
+        print(f"  mode {mode}: rel err {e[mode]:.2e} on {len(rows)} rows", flush=True)
+        assert e[mode] <= tol
+        # Deterministic: the split partials are added in a fixed order.
+        np.testing.assert_array_equal(run_linear(a, w, mode), out)
+    assert e[rt.F32] * 20 < e[rt.BF16]
+
+
 def test_linear_projection_8192x2048x2048_sampled_rows():
     """The per-block projection at 4096 tokens, B=2: [8192, 2048] x [2048, 2048]^T;
     64 rows (first, last and random) are checked against the oracle."""
