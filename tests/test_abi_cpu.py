@@ -185,3 +185,20 @@ def test_bf16_and_x3_entries_refuse_a_bad_scale_before_any_device_work(entry, sc
             False, None)
     assert not ok
     assert "scale must be positive and finite" in _lib.last_error()
+
+
+def test_linear_scratch_holds_the_small_m_partials_only_where_that_kernel_runs():
+    # anima_hip_linear_scratch_bytes: the bf16 terms (two for the f32 modes),
+    # plus 16 MiB of split-K partials where the hand-written small-M GEMM
+    # replaces the library: M <= 1024, K a multiple of 64, and two terms or
+    # K >= 8192 (pure host arithmetic, no GPU).
+    lib = _lib.load()
+    part = 16 << 20
+    terms = lambda M, K, n: -(-(M * (-(-K // 8) * 8) * 2) // 256) * 256 * n  # noqa: E731
+    for M, K, mode, extra in [(512, 2048, rt.F32, True), (512, 2048, rt.F32X3, True),
+                              (512, 2048, rt.BF16, False), (512, 8192, rt.BF16, True),
+                              (1024, 4096, rt.F32, True), (1025, 4096, rt.F32, False),
+                              (512, 2056, rt.F32, False), (77, 64, rt.F32, True)]:
+        n = 1 if mode == rt.BF16 else 2
+        want = terms(M, K, n) + (part if extra else 0)
+        assert lib.anima_hip_linear_scratch_bytes(M, K, mode) == want, (M, K, mode)
