@@ -60,6 +60,8 @@ SIGNATURES = {
     "anima_hip_attention_scratch_bytes": (ct.c_size_t, [_I] * 7),
     "anima_hip_attention_dev": (_B, [_P] * 8 + [ct.c_size_t] + [_I] * 6 + [_F, _I, _P]),
     "anima_hip_attention_static_dev": (_B, [_P] * 7 + [_I] * 6 + [_F, _I, _P]),
+    "anima_hip_attention_terms_dev": (_B, [_P] * 7 + [ct.c_int64] * 2 + [_P, ct.c_size_t]
+                                      + [_I] * 6 + [_F, _I, _P]),
     "anima_hip_dit_default_config": (None, [_P]),
     "anima_hip_dit_create": (_P, [_P, _P, _P, ct.POINTER(_I), _I64P, _I, _I]),
     "anima_hip_dit_destroy": (None, [_P]),

@@ -1170,22 +1170,27 @@ size_t anima_hip_attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H
     return attention_scratch_bytes(B, S_q, Bk, S_kv, H, D, size_mode(mode), false);
 }
 
-bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
-                             const float *q_norm_w, const float *k_norm_w, const float *freqs,
-                             float *out, void *scratch, size_t scratch_bytes, int B, int S_q,
-                             int Bk, int S_kv, int H, int D, float eps, int mode, void *stream)
+namespace {
+// anima_hip_attention_dev and its term-output form: O goes to out (f32) or,
+// when out_t is set, to bf16 term rows (AttnInputs::out_t).
+bool attention_dev_call(const char *name, const float *q, const float *k, const float *v,
+                        const float *q_norm_w, const float *k_norm_w, const float *freqs,
+                        float *out, uint16_t *out_t, int64_t ld_t, int64_t lo_t, void *scratch,
+                        size_t scratch_bytes, int B, int S_q, int Bk, int S_kv, int H, int D,
+                        float eps, int mode, void *stream)
 {
     if (!ready_for_device_call() || !check_dims(B, H, S_q, S_kv, D))
         return false;
     AttnMode am;
-    if (!attn_mode_of(mode, D, "attention_dev", am))
+    if (!attn_mode_of(mode, D, name, am))
         return false;
     if (int64_t(B) * S_q * H * D == 0)
         return true;
-    if (!q || !out || !scratch || (S_kv > 0 && (!k || !v)))
-        return fail("attention_dev: null pointer");
+    const std::string who(name);
+    if (!q || !(out || out_t) || !scratch || (S_kv > 0 && (!k || !v)))
+        return fail(who + ": null pointer");
     if (scratch_bytes < attention_scratch_bytes(B, S_q, Bk, S_kv, H, D, am, false))
-        return fail("attention_dev: scratch smaller than anima_hip_attention_scratch_bytes()");
+        return fail(who + ": scratch smaller than anima_hip_attention_scratch_bytes()");
     AttnInputs in;
     in.q = q;
     in.q_norm_w = q_norm_w;
@@ -1194,6 +1199,9 @@ bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
     in.v = v;
     in.k_norm_w = k_norm_w;
     in.out = out;
+    in.out_t = out_t;
+    in.ld_t = ld_t;
+    in.lo_t = lo_t;
     in.B = B;
     in.Bk = Bk;
     in.S_q = S_q;
@@ -1203,6 +1211,39 @@ bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
     in.eps = eps;
     in.mode = am;
     return run_attention(in, scratch, pick_stream(stream));
+}
+}  // namespace
+
+bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
+                             const float *q_norm_w, const float *k_norm_w, const float *freqs,
+                             float *out, void *scratch, size_t scratch_bytes, int B, int S_q,
+                             int Bk, int S_kv, int H, int D, float eps, int mode, void *stream)
+{
+    return attention_dev_call("attention_dev", q, k, v, q_norm_w, k_norm_w, freqs, out, nullptr,
+                              0, 0, scratch, scratch_bytes, B, S_q, Bk, S_kv, H, D, eps, mode,
+                              stream);
+}
+
+bool anima_hip_attention_terms_dev(const float *q, const float *k, const float *v,
+                                   const float *q_norm_w, const float *k_norm_w,
+                                   const float *freqs, uint16_t *out_terms, int64_t ld_terms,
+                                   int64_t lo_offset, void *scratch, size_t scratch_bytes, int B,
+                                   int S_q, int Bk, int S_kv, int H, int D, float eps, int mode,
+                                   void *stream)
+{
+    if (D != 128)
+        return fail("attention_terms_dev: the term output needs D == 128");
+    const int64_t HD = int64_t(H) * D;
+    if (ld_terms < HD || lo_offset < 0 || (lo_offset > 0 && (lo_offset < HD ||
+                                                             lo_offset + HD > ld_terms)))
+        return fail("attention_terms_dev: a row of ld_terms elements must hold the hi block "
+                    "[0, H*D) and, when lo_offset > 0, the lo block [lo_offset, lo_offset + H*D)");
+    if (ld_terms % 8 || lo_offset % 8 || (reinterpret_cast<uintptr_t>(out_terms) & 15u))
+        return fail("attention_terms_dev: out_terms must be 16-byte aligned, ld_terms and "
+                    "lo_offset multiples of 8");
+    return attention_dev_call("attention_terms_dev", q, k, v, q_norm_w, k_norm_w, freqs, nullptr,
+                              out_terms, ld_terms, lo_offset, scratch, scratch_bytes, B, S_q, Bk,
+                              S_kv, H, D, eps, mode, stream);
 }
 
 bool anima_hip_attention(const float *q, const float *k, const float *v, const float *q_norm_w,

@@ -225,6 +225,15 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     p.D = D;
     p.scale = float(1.0 / std::sqrt(double(D)));
     p.causal = false;
+    if (in.out_t) {
+        p.o = nullptr;
+        p.os = Strides{0, 0, 0};
+        p.ot.t = in.out_t;
+        p.ot.tb = int64_t(S_q) * in.ld_t;
+        p.ot.th = D;
+        p.ot.ts = in.ld_t;
+        p.ot.lo = in.lo_t;
+    }
     switch (mode) {
     case kAttnBF16:
         return launch_flash_bf16(p, st, part, part_bytes);

@@ -379,6 +379,23 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
     in.D = D;
     in.eps = p.eps;
     in.mode = p.mode;
+    // With D == 128 the attention writes O straight into output_proj's bf16
+    // terms, where launch_linear would split it: hi rows of
+    // linear_terms_ld(HD) at lin and, in the f32 modes, the lo rows after
+    // them (lo_t = the hi block's size).  Other head dims, or a shape the
+    // library GEMM does not take (launch_linear's exact f32 fallback needs
+    // O itself): f32 O at o.
+    const bool terms_out = D == 128 && linear_terms_supported(int(M), Dm, HD, p.wo, HD, y, Dm);
+    const int64_t kp = linear_terms_ld(HD);
+    const size_t hi_bytes = round_up256(size_t(M) * size_t(kp) * 2);
+    uint16_t *ohi = static_cast<uint16_t *>(lin);
+    uint16_t *olo = bf16 ? nullptr : ohi + hi_bytes / 2;
+    if (terms_out) {
+        in.out = nullptr;
+        in.out_t = ohi;
+        in.ld_t = kp;
+        in.lo_t = bf16 ? 0 : int64_t(hi_bytes / 2);
+    }
     if (!run_attention(in, attn, st))
         return false;
 
@@ -389,11 +406,18 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
     // not take with a per-channel scale: the projection into y, then a
     // residual pass.
     if (bf16 && linear_residual_supported(S, Dm, HD, p.wo, HD, p.x, Dm))
-        return launch_linear_residual(o, HD, p.wo, HD, p.x, Dm, p.mod + 2 * int64_t(Dm),
-                                      3 * int64_t(Dm), B, S, Dm, HD, lin, s.lin, st);
-    if (!launch_linear(o, HD, p.wo, HD, y, Dm, int(M), Dm, HD, !bf16, lin, s.lin, st))
-        return false;
-    return launch_gate_residual(p.x, y, p.mod, M, S, Dm, st);
+        return terms_out
+                   ? launch_linear_residual_terms(ohi, p.wo, HD, p.x, Dm, p.mod + 2 * int64_t(Dm),
+                                                  3 * int64_t(Dm), B, S, Dm, HD, st)
+                   : launch_linear_residual(o, HD, p.wo, HD, p.x, Dm, p.mod + 2 * int64_t(Dm),
+                                            3 * int64_t(Dm), B, S, Dm, HD, lin, s.lin, st);
+    const size_t terms_bytes = hi_bytes * (bf16 ? 1 : 2);
+    const bool ok =
+        terms_out ? launch_linear_terms(ohi, olo, p.wo, HD, y, Dm, int(M), Dm, HD, st,
+                                        static_cast<char *>(lin) + terms_bytes,
+                                        s.lin - terms_bytes)
+                  : launch_linear(o, HD, p.wo, HD, y, Dm, int(M), Dm, HD, !bf16, lin, s.lin, st);
+    return ok && launch_gate_residual(p.x, y, p.mod, M, S, Dm, st);
 }
 
 }  // namespace anima_hip

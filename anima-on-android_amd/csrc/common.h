@@ -24,15 +24,28 @@ struct Strides {
     int64_t b, h, s;
 };
 
+// O of the D == 128 flash kernels written as the bf16 terms a bf16-MFMA
+// projection of O reads, instead of f32: hi = bf16(O) (round to nearest even)
+// at t + b*tb + h*th + q*ts + d and, when lo > 0, bf16(O - hi) lo elements
+// after it.  These are the values split_kernel (linear.hip) writes from the
+// f32 O, so the projection needs no split pass.  t == nullptr: f32 O.
+// Offsets and strides are multiples of 8 elements and t is 16-byte aligned.
+struct TermOut {
+    uint16_t *t = nullptr;
+    int64_t tb = 0, th = 0, ts = 0, lo = 0;
+};
+
 // Everything the attention kernels need; pointers are device pointers.
 struct FlashProblem {
     const void *q, *k, *v;  // f32 or bf16 (see kernel)
-    float *o;
+    float *o;               // unused when ot.t is set
     Strides qs, ks, vs, os;
     int B, H, S_q, S_kv, D;
     float scale;       // softmax scale applied to q.k
     bool causal;       // mask key j > query i (top-left aligned, like anima_rt)
+    TermOut ot;        // bf16 term output in place of o
 };
+bool term_out_ok(const TermOut &t);  // alignment of a set term output
 
 // Launch shape of the D == 128 flash kernels.  A grid of B*H*ceil(S_q/256)
 // workgroups of 8 waves fills the GPU when it has at least one workgroup per
@@ -48,7 +61,17 @@ struct FlashPlan {
     int tiles = 1 << 30;  // key tiles per split
     size_t bytes = 0;     // scratch for the partials (0 when unsplit)
 };
-FlashPlan flash_plan(int64_t BH, int S_q, int S_kv, int D);
+// tile_us > 0: the kernel's time per 64-key tile in a 4-wave workgroup (us);
+// the key range is then split only where the tiles a workgroup no longer
+// walks are worth more than a split grid's fixed cost (kSplitCostUs: every
+// split loads its query tile and writes f32 partials that the combine pass
+// reads back).  tile_us == 0 always splits a small grid: the scratch size
+// every mode's plan fits in.
+FlashPlan flash_plan(int64_t BH, int S_q, int S_kv, int D, float tile_us = 0.0f);
+// Measured on MI355X at 32 heads x 256 queries (unsplit 4-wave grids over
+// 4 and 8 key tiles; split grids against them, combine included).
+constexpr float kSplitCostUs = 13.0f;
+constexpr float kTileUsF32 = 9.1f, kTileUsBF16 = 1.3f, kTileUsX3 = 2.5f;
 
 // What a split workgroup writes (device view).  Partials are laid out
 // [splits][BH][S_q][128] f32 and (max, sum) pairs [splits][BH][S_q] float2,
@@ -240,6 +263,10 @@ struct AttnInputs {
     const void *k_prep = nullptr;     // prepared K/V (context cache), or null
     const void *v_prep = nullptr;
     float *out = nullptr;             // [B, S_q, H, D] f32
+    // Or O as bf16 projection terms (D == 128): token rows ld_t elements
+    // apart, hi at column h*D + d, lo (when lo_t > 0) lo_t elements after it.
+    uint16_t *out_t = nullptr;
+    int64_t ld_t = 0, lo_t = 0;
     int B = 0, Bk = 0, S_q = 0, S_kv = 0, H = 0, D = 0;
     float eps = 1e-6f;
     AttnMode mode = kAttnF32;

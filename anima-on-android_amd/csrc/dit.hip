@@ -615,6 +615,27 @@ bool dit_linear(const anima_hip_dit *d, const float *a, int K, const uint16_t *w
     return launch_linear(a, K, w, ld_w, y, N, int(M), N, K, false, lin, lin_bytes + ws_bytes, st);
 }
 
+// The output projection of an attention sub-layer whose kernels wrote O as
+// the projection's bf16 terms at t (attention_term_rows' layout), left as
+// *parts planes at y like dit_linear's.
+struct TermRows {
+    int64_t ld, lo;  // row length and lo offset (0: hi only) in bf16 elements
+};
+TermRows attention_term_rows(const anima_hip_dit *d, int K)
+{
+    const int64_t kp = linear_terms_ld(K);
+    return d->reps == 2 ? TermRows{2 * kp, kp} : TermRows{kp, 0};
+}
+
+bool dit_project_terms(const anima_hip_dit *d, const uint16_t *t, int K, const uint16_t *w,
+                       int64_t ld_w, float *y, size_t y_bytes, int *parts, int N, int64_t M,
+                       hipStream_t st)
+{
+    const TermRows tr = attention_term_rows(d, K);
+    return launch_linear_planes(t, tr.ld, d->reps == 2 ? int(tr.lo) : K, d->reps == 2, w, ld_w,
+                                y, y_bytes, int(M), N, parts, st);
+}
+
 // One sub-layer of block bw on the residual stream x (kind as sub_layout),
 // after applying the pending residual (pend_parts planes at pend_y); its
 // output projection goes to y as *y_parts planes (y_bytes of room).
@@ -693,9 +714,20 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
         in.Bk = d->ctx_B;
         in.S_kv = d->ctx_S;
     }
+    const uint16_t *wo = kind == 0 ? bw.w_o : bw.w_co;
+    if (c.head_dim != 128)  // the generic f32 kernel writes f32 O only
+        return run_attention(in, rattn, st) &&
+               dit_linear(d, o, HD, wo, d->ld_hd, y, y_bytes, y_parts, D, M, rlin, l.lin, l.ws,
+                          st);
+    // O straight into output_proj's bf16 terms: no split pass.
+    const TermRows tr = attention_term_rows(d, HD);
+    uint16_t *ot = reinterpret_cast<uint16_t *>(rlin);
+    in.out = nullptr;
+    in.out_t = ot;
+    in.ld_t = tr.ld;
+    in.lo_t = tr.lo;
     return run_attention(in, rattn, st) &&
-           dit_linear(d, o, HD, kind == 0 ? bw.w_o : bw.w_co, d->ld_hd, y, y_bytes, y_parts, D, M,
-                      rlin, l.lin, l.ws, st);
+           dit_project_terms(d, ot, HD, wo, d->ld_hd, y, y_bytes, y_parts, D, M, st);
 }
 
 // The forward pass on B batch entries of the latent x ([B][C][T][H][W] with

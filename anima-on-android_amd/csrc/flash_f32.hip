@@ -24,6 +24,7 @@
 // lane reads K and Q as contiguous float4s; the permutation is applied to Q
 // and K alike, so the dot products are unchanged.
 #include "common.h"
+#include "flash_tile.h"
 
 #include <cmath>
 
@@ -49,6 +50,7 @@ struct F32Args {
     float c;     // scale * log2(e)
     int causal;
     FlashSplitArgs split;  // n == 1: write O; n > 1: write this split's partial
+    TermOut ot;            // n == 1 and ot.t set: O as bf16 terms
 };
 
 __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c)
@@ -277,18 +279,21 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_f32_d128(F32Args a)
     const float inv = dead ? 0.0f : l > 0.0f ? 1.0f / l : 0.0f;
     if (qrow < a.S_q) {
         float *op = a.o + b * a.ob + h * a.oh + qrow * a.os;
+        uint16_t *tp = a.ot.t ? a.ot.t + b * a.ot.tb + h * a.ot.th + qrow * a.ot.ts : nullptr;
         if (a.split.n > 1) {
             const int64_t prow = (int64_t(sp) * a.split.BH + bh) * a.S_q + qrow;
             op = a.split.part + prow * kD;
+            tp = nullptr;
             if (half == 0)
                 a.split.ml[prow] = make_float2(m, dead ? 0.0f : l);
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int d0 = 4 * acc_row(r, half);
-            *reinterpret_cast<f32x4 *>(op + d0) =
-                dead ? f32x4{0.f, 0.f, 0.f, 0.f}
-                     : f32x4{o0[r] * inv, o1[r] * inv, o2[r] * inv, o3[r] * inv};
+            flash_tile::store_out4(dead ? f32x4{0.f, 0.f, 0.f, 0.f}
+                                        : f32x4{o0[r] * inv, o1[r] * inv, o2[r] * inv,
+                                                o3[r] * inv},
+                                   op, tp, a.ot.lo, d0);
         }
     }
 }
@@ -410,10 +415,14 @@ bool launch_flash_f32(const FlashProblem &p, hipStream_t st, void *part, size_t 
     const int64_t BH = int64_t(p.B) * p.H;
     if (BH == 0 || p.S_q == 0)
         return true;
+    if (p.ot.t && !(flash_f32_fast_path(p) && term_out_ok(p.ot)))
+        return fail("flash_f32: term output needs D == 128, 16-byte aligned operands and an "
+                    "16-byte aligned output with strides of 8 elements");
     if (flash_f32_fast_path(p)) {
         F32Args a;
         fill_common(a, p);
-        const FlashPlan pl = flash_plan(BH, p.S_q, p.S_kv, p.D);
+        a.ot = p.ot;
+        const FlashPlan pl = flash_plan(BH, p.S_q, p.S_kv, p.D, kTileUsF32);
         a.split = flash_split_args(pl, BH, p.S_q, part, part_bytes);
         if (!(pl.waves == 4 ? launch_d128<4>(a, BH, st) : launch_d128<8>(a, BH, st)))
             return false;

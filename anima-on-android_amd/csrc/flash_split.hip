@@ -8,6 +8,7 @@
 // split s holding O_s = sum_j p_j v_j / l_s, p_j = 2^(x_j - m_s), l_s = sum_j p_j,
 //   O = sum_s l_s 2^(m_s - M) O_s / sum_s l_s 2^(m_s - M),  M = max_s m_s.
 #include "common.h"
+#include "flash_tile.h"
 
 #include <cmath>
 
@@ -28,6 +29,7 @@ struct CombineArgs {
     int64_t ob, oh, os;
     int H, S_q;
     FlashSplitArgs sa;
+    TermOut ot;     // set: O as bf16 terms instead of f32 at o
     int64_t total;  // BH * S_q * 32 float4 columns
 };
 
@@ -83,12 +85,20 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(CombineArgs a)
     const int64_t bh = row / a.S_q;
     const int q = int(row - bh * a.S_q);
     const int b = int(bh / a.H), h = int(bh - int64_t(b) * a.H);
-    *reinterpret_cast<f32x4 *>(a.o + b * a.ob + h * a.oh + q * a.os + 4 * c4) = acc * inv;
+    flash_tile::store_out4(acc * inv, a.o + b * a.ob + h * a.oh + q * a.os,
+                           a.ot.t ? a.ot.t + b * a.ot.tb + h * a.ot.th + q * a.ot.ts : nullptr,
+                           a.ot.lo, 4 * c4);
 }
 
 }  // namespace
 
-FlashPlan flash_plan(int64_t BH, int S_q, int S_kv, int D)
+bool term_out_ok(const TermOut &t)
+{
+    return (reinterpret_cast<uintptr_t>(t.t) & 15u) == 0 && t.tb % 8 == 0 && t.th % 8 == 0 &&
+           t.ts % 8 == 0 && t.lo % 8 == 0 && t.lo >= 0;
+}
+
+FlashPlan flash_plan(int64_t BH, int S_q, int S_kv, int D, float tile_us)
 {
     FlashPlan pl;
     if (D != kD || BH <= 0 || S_q <= 0 || BH * ceil_div(S_q, 256) >= kTargetBlocks)
@@ -101,7 +111,7 @@ FlashPlan flash_plan(int64_t BH, int S_q, int S_kv, int D)
         return pl;
     const int64_t tiles = ceil_div(ntiles, std::min(want, ntiles));
     const int64_t splits = ceil_div(ntiles, tiles);
-    if (splits < 2)
+    if (splits < 2 || (tile_us > 0.0f && double(ntiles - tiles) * tile_us < kSplitCostUs))
         return pl;
     pl.splits = int(splits);
     pl.tiles = int(tiles);
@@ -137,6 +147,7 @@ bool launch_flash_combine(const FlashProblem &p, const FlashSplitArgs &sa, hipSt
     a.H = p.H;
     a.S_q = p.S_q;
     a.sa = sa;
+    a.ot = p.ot;
     a.total = sa.BH * p.S_q * (kD / 4);
     const int64_t nblk = ceil_div(a.total, 256);
     if (nblk > INT32_MAX)

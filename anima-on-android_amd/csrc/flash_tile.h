@@ -120,6 +120,36 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16 &s, int base)
     return r;
 }
 
+// hi = bf16(v) and lo = bf16(v - hi), both rounded to nearest even, as two
+// bf16 pairs each: split_kernel's arithmetic (linear.hip), so a term output
+// equals the split of the f32 output bit for bit.  v - hi is exact in f32.
+__device__ __forceinline__ void split_terms4(const f32x4 &v, uint2 &hi, uint2 &lo)
+{
+    const bf16x2 h0 = __builtin_convertvector(f32x2{v.x, v.y}, bf16x2);
+    const bf16x2 h1 = __builtin_convertvector(f32x2{v.z, v.w}, bf16x2);
+    const bf16x2 l0 =
+        __builtin_convertvector(f32x2{v.x - float(h0[0]), v.y - float(h0[1])}, bf16x2);
+    const bf16x2 l1 =
+        __builtin_convertvector(f32x2{v.z - float(h1[0]), v.w - float(h1[1])}, bf16x2);
+    hi = uint2{__builtin_bit_cast(unsigned, h0), __builtin_bit_cast(unsigned, h1)};
+    lo = uint2{__builtin_bit_cast(unsigned, l0), __builtin_bit_cast(unsigned, l1)};
+}
+
+// Four f32 values of an output row at d (a multiple of 4): as f32 at o + d,
+// or, when t is set, as bf16 terms at t + d (and t + lo + d when lo > 0).
+__device__ __forceinline__ void store_out4(const f32x4 &v, float *o, u16 *t, int64_t lo, int d)
+{
+    if (t) {
+        uint2 h, l;
+        split_terms4(v, h, l);
+        *reinterpret_cast<uint2 *>(t + d) = h;
+        if (lo > 0)
+            *reinterpret_cast<uint2 *>(t + lo + d) = l;
+    } else {
+        *reinterpret_cast<f32x4 *>(o + d) = v;
+    }
+}
+
 // Epilogue of the transposed bf16-MFMA kernels.  A wave holds O^T of its 32
 // query rows in four 32x32 accumulators (o_blk: d = 32 blk + acc_row(r,
 // half)), so a direct store writes 16 bytes of 32 rows 8 KiB apart per
@@ -130,13 +160,16 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16 &s, int base)
 // -inf: every score was masked or NaN) is written as zeros, which is what the
 // reference's flash attention leaves there (flash_attention.h:148-152 skips
 // such rows and :194-201 divides only positive sums of a zero-filled output).
+// With trow0 set, the rows go out as bf16 terms (split_terms4) at trow0 +
+// r * tstride instead of f32 at row0 + r * stride, in 16-byte stores.
 // The caller guarantees no other wave uses `lds` (kOWaveFloats floats).
 constexpr int kOPitch = 68;  // floats per staged half row: 64 d + 4 against bank conflicts
 constexpr int kOWaveFloats = 32 * kOPitch;
 
 __device__ __forceinline__ void store_o_rows(float *lds, const f32x16 &o0, const f32x16 &o1,
                                              const f32x16 &o2, const f32x16 &o3, float inv,
-                                             bool dead, float *row0, int64_t stride, int nrows)
+                                             bool dead, float *row0, int64_t stride, int nrows,
+                                             u16 *trow0, int64_t tstride, int64_t tlo)
 {
     const int lane = threadIdx.x & 63, col = lane & 31, half = lane >> 5;
 #pragma unroll
@@ -159,13 +192,33 @@ __device__ __forceinline__ void store_o_rows(float *lds, const f32x16 &o0, const
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         asm volatile("" ::: "memory");
-        const int c = lane & 15;
+        if (trow0) {
+            // Terms: 8 values per lane, so each term goes out as one 16-byte
+            // store and an instruction writes 8 whole 128-byte half rows.
+            const int c = lane & 7;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = 4 * i + (lane >> 4);
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(lds + r * kOPitch + 4 * c);
-            if (r < nrows)
-                *reinterpret_cast<f32x4 *>(row0 + r * stride + 64 * p + 4 * c) = v;
+            for (int i = 0; i < 4; ++i) {
+                const int r = 8 * i + (lane >> 3);
+                const float *src = lds + r * kOPitch + 8 * c;
+                uint2 h0, l0, h1, l1;
+                split_terms4(*reinterpret_cast<const f32x4 *>(src), h0, l0);
+                split_terms4(*reinterpret_cast<const f32x4 *>(src + 4), h1, l1);
+                u16 *dst = trow0 + r * tstride + 64 * p + 8 * c;
+                if (r < nrows) {
+                    *reinterpret_cast<uint4 *>(dst) = uint4{h0.x, h0.y, h1.x, h1.y};
+                    if (tlo > 0)
+                        *reinterpret_cast<uint4 *>(dst + tlo) = uint4{l0.x, l0.y, l1.x, l1.y};
+                }
+            }
+        } else {
+            const int c = lane & 15;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int r = 4 * i + (lane >> 4);
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(lds + r * kOPitch + 4 * c);
+                if (r < nrows)
+                    *reinterpret_cast<f32x4 *>(row0 + r * stride + 64 * p + 4 * c) = v;
+            }
         }
         // This pass's reads complete before the next pass overwrites the rows.
         asm volatile("" ::: "memory");

@@ -53,6 +53,7 @@ struct X3Args {
     int causal;
     int dma32;  // K/V^T tile rows fit 32-bit byte offsets from the tile start
     FlashSplitArgs split;  // n == 1: write O; n > 1: write this split's partial
+    TermOut ot;            // n == 1 and ot.t set: O as bf16 terms
 };
 
 template <int NW>
@@ -338,7 +339,9 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
     const int row0 = q_tile0 + wave * 32;
     float *op = a.o + b * a.ob + h * a.oh + row0 * a.os;
     int64_t ostride = a.os;
+    u16 *tp = a.ot.t ? a.ot.t + b * a.ot.tb + h * a.ot.th + row0 * a.ot.ts : nullptr;
     if (a.split.n > 1) {
+        tp = nullptr;
         const int64_t prow0 = (int64_t(sp) * a.split.BH + bh) * a.S_q + row0;
         op = a.split.part + prow0 * kD;
         ostride = kD;
@@ -347,7 +350,7 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
     }
     // Every wave has passed the loop's last barrier: the rings are free.
     store_o_rows(reinterpret_cast<float *>(smem) + wave * kOWaveFloats, o0, o1, o2, o3, inv, dead,
-                 op, ostride, a.S_q - row0);
+                 op, ostride, a.S_q - row0, tp, a.ot.ts, a.ot.lo);
 }
 
 // V (f32, [B,H,S,D] view, D = 128) -> packed bf16 term V^T [B,H][2D][Sp]:
@@ -453,6 +456,8 @@ bool launch_flash_x3(const FlashProblem &p, hipStream_t st, void *part, size_t p
     if (!aligned(p.q, 16) || !aligned(p.k, 16) || !aligned(p.v, 16) || !aligned(p.o, 16) ||
         !s8(p.qs) || !s8(p.ks) || !s8(p.vs) || p.os.b % 4 || p.os.h % 4 || p.os.s % 4)
         return fail("flash_x3: operands must be 16-byte aligned with 16-byte row strides");
+    if (p.ot.t && !term_out_ok(p.ot))
+        return fail("flash_x3: term output must be 16-byte aligned with strides of 8 elements");
     X3Args a;
     a.q = static_cast<const u16 *>(p.q);
     a.k = static_cast<const u16 *>(p.k);
@@ -462,6 +467,7 @@ bool launch_flash_x3(const FlashProblem &p, hipStream_t st, void *part, size_t p
     a.kb = p.ks.b; a.kh = p.ks.h; a.ks = p.ks.s;
     a.vb = p.vs.b; a.vh = p.vs.h; a.vd = sp;
     a.ob = p.os.b; a.oh = p.os.h; a.os = p.os.s;
+    a.ot = p.ot;
     a.H = p.H;
     a.S_q = p.S_q;
     a.S_kv = p.S_kv;
@@ -471,7 +477,7 @@ bool launch_flash_x3(const FlashProblem &p, hipStream_t st, void *part, size_t p
     // r*ks, V^T rows r < 256 at r*Sp, plus one row of 512 bytes.
     a.dma32 = (int64_t(kBN) * p.ks.s * 2 + 512 < (int64_t(1) << 31)) &&
               (int64_t(2 * kD) * sp * 2 + 512 < (int64_t(1) << 31));
-    const FlashPlan pl = flash_plan(BH, p.S_q, p.S_kv, p.D);
+    const FlashPlan pl = flash_plan(BH, p.S_q, p.S_kv, p.D, kTileUsX3);
     a.split = flash_split_args(pl, BH, p.S_q, part, part_bytes);
     if (!(pl.waves == 4 ? launch_d128<4>(a, BH, st) : launch_d128<8>(a, BH, st)))
         return false;

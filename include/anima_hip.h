@@ -253,6 +253,24 @@ bool anima_hip_attention_dev(const float *q, const float *k, const float *v,
                              float *out, void *scratch, size_t scratch_bytes, int B, int S_q,
                              int Bk, int S_kv, int H, int D, float eps, int mode, void *stream);
 
+/* anima_hip_attention_dev with O written as the bf16 terms of the input of a
+ * bf16-MFMA projection of O instead of f32 (no counterpart in the
+ * reference: NumpyAttention.forward hands O to output_proj as f32,
+ * anima_rt/scripts/numpy_dit.py:294-296, and this form saves the pass that
+ * splits it).  Token row t = b*S_q + s of out_terms is ld_terms bf16
+ * elements long: hi = bf16(O) (round to nearest even) at column h*D + d and,
+ * when lo_offset > 0, lo = bf16(O - hi) at lo_offset + h*D + d -- the terms
+ * anima_hip_linear_dev forms from an f32 A (one term in ANIMA_HIP_BF16 mode,
+ * two otherwise), bit for bit.  D must be 128; out_terms 16-byte aligned;
+ * ld_terms and lo_offset multiples of 8, lo_offset >= H*D and
+ * lo_offset + H*D <= ld_terms.  Same scratch as anima_hip_attention_dev. */
+bool anima_hip_attention_terms_dev(const float *q, const float *k, const float *v,
+                                   const float *q_norm_w, const float *k_norm_w,
+                                   const float *freqs, uint16_t *out_terms, int64_t ld_terms,
+                                   int64_t lo_offset, void *scratch, size_t scratch_bytes, int B,
+                                   int S_q, int Bk, int S_kv, int H, int D, float eps, int mode,
+                                   void *stream);
+
 /* anima_hip_attention_dev without scratch and without any allocation.  No
  * counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops that forbid

@@ -38,7 +38,7 @@ def _case(where, bh, s, d, seed):
 
 @pytest.mark.parametrize("where", ["q_row", "k_row", "v_elem"])
 @pytest.mark.parametrize("bh,s,d,modes", [
-    (2, 600, 128, (rt.F32, rt.F32X3, rt.BF16)),    # split-KV partials + combine
+    (2, 1000, 128, (rt.F32, rt.F32X3, rt.BF16)),   # split-KV partials + combine
     (256, 300, 128, (rt.F32, rt.F32X3, rt.BF16)),  # 8-wave grid, ragged tail
     (3, 130, 80, (rt.F32,)),                      # generic kernel (D != 128)
 ])

@@ -85,9 +85,10 @@ def _static(dev, B, S_q, Bk, S_kv, mode):
 @pytest.mark.parametrize("mode", [rt.F32, rt.F32X3, rt.BF16])
 def test_static_scratch_matches_caller_scratch(mode):
     # Call 1: self-attention, B=2, 1024 tokens (32 x 32 RoPE grid), 8-wave
-    # grid.  Call 2: one batch entry of 256 query tokens against 512 keys
-    # (no RoPE), which splits the key range through scratch partials.
-    calls = [(2, 1024, 2, 1024, (32, 32)), (1, 256, 1, 512, None)]
+    # grid.  Call 2: one batch entry of 256 query tokens against 1024 keys
+    # (no RoPE), which splits the key range through scratch partials in
+    # every mode (8 splits of 2 key tiles).
+    calls = [(2, 1024, 2, 1024, (32, 32)), (1, 256, 1, 1024, None)]
     for i, (B, S_q, Bk, S_kv, grid) in enumerate(calls):
         q, k, v, qw, kw, freqs = _case(7000 + 10 * i + mode, B, S_q, Bk, S_kv, grid)
         dev = _Dev(q, k, v, qw, kw, freqs)
