@@ -118,34 +118,38 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
     //       at c ^ (r & 15);
     //   V^T [256 rows][64 keys] (hi d-rows 0..127, lo 128..255): chunk c of
     //       row r at c ^ ((r >> 1) & 7).
-    // Copy slot f = 64w + lane of window w = wave*DMA + i fills physical
-    // chunk f of the tile; this lane's sources as byte offsets from the tile's
-    // first row (dma32) or row/chunk indices for the clamped path.
-    unsigned koff_b[DMA], voff_b[DMA];
-    int krow[DMA], kchk[DMA];
+    // Copy i of wave w fills physical chunks f = i*NT + 64w + lane of the
+    // tile: K row f >> 5 = i*NT/32 + 2w + half, chunk col ^ (row & 15); V^T
+    // row f >> 3 = i*NT/8 + 8w + lane/8.  With NT a multiple of 256 the V^T
+    // swizzle term does not depend on i and the K term only on i's parity, so
+    // a lane's source offset is one register (two for K) plus a uniform step
+    // per copy (247 -> 231 VGPRs at NW = 8).
+    const int krl = 2 * wave + half;  // K row of copy 0
+    unsigned koff_b[2];
 #pragma unroll
-    for (int i = 0; i < DMA; ++i) {
-        const int f = (wave * DMA + i) * 64 + lane;
-        const int r = f >> 5, c = (f & 31) ^ (r & 15);
-        krow[i] = r;
-        kchk[i] = c;
-        koff_b[i] = unsigned(r * a.ks + 8 * c) * 2u;
-        const int rv = f >> 3, cv = (f & 7) ^ ((rv >> 1) & 7);
-        voff_b[i] = unsigned(rv * a.vd + 8 * cv) * 2u;
+    for (int i = 0; i < 2; ++i) {
+        const int c = col ^ ((i * (NT / 32) + krl) & 15);
+        koff_b[i] = unsigned(krl * a.ks + 8 * c) * 2u;
     }
+    const int vrl = 8 * wave + (lane >> 3);  // V^T row of copy 0
+    const int vcl = (lane & 7) ^ ((vrl >> 1) & 7);
+    const unsigned voff_b = unsigned(vrl * a.vd + 8 * vcl) * 2u;
+    static_assert(NT % 256 == 0, "copy offsets assume whole 256-thread groups");
     auto dma_k = [&](int t, int stage) {
         const int key0 = (j0 + t) * kBN;
         if (a.dma32 && key0 + kBN <= a.S_kv) {
             const u16 *base = kp + int64_t(key0) * a.ks;
 #pragma unroll
             for (int i = 0; i < DMA; ++i)
-                dma16s(base, koff_b[i], &Ks[stage][(wave * DMA + i) * 512]);
+                dma16s(base + int64_t(i * (NT / 32)) * a.ks, koff_b[i & 1],
+                       &Ks[stage][(i * NT + 64 * wave) * 8]);
         } else {
             // Keys past S_kv copy row S_kv - 1; their scores are masked.
 #pragma unroll
             for (int i = 0; i < DMA; ++i) {
-                const int key = min(key0 + krow[i], a.S_kv - 1);
-                dma16(kp + key * a.ks + 8 * kchk[i], &Ks[stage][(wave * DMA + i) * 512]);
+                const int r = i * (NT / 32) + krl;
+                const int key = min(key0 + r, a.S_kv - 1);
+                dma16(kp + key * a.ks + 8 * (col ^ (r & 15)), &Ks[stage][(i * NT + 64 * wave) * 8]);
             }
         }
     };
@@ -156,14 +160,13 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
             const u16 *base = vp + key0;
 #pragma unroll
             for (int i = 0; i < DMA; ++i)
-                dma16s(base, voff_b[i], &Vs[stage][(wave * DMA + i) * 512]);
+                dma16s(base + int64_t(i * (NT / 8)) * a.vd, voff_b,
+                       &Vs[stage][(i * NT + 64 * wave) * 8]);
         } else {
 #pragma unroll
-            for (int i = 0; i < DMA; ++i) {
-                const int f = (wave * DMA + i) * 64 + lane;
-                const int r = f >> 3, c = (f & 7) ^ ((r >> 1) & 7);
-                dma16(vp + r * a.vd + key0 + 8 * c, &Vs[stage][(wave * DMA + i) * 512]);
-            }
+            for (int i = 0; i < DMA; ++i)
+                dma16(vp + (i * (NT / 8) + vrl) * a.vd + key0 + 8 * vcl,
+                      &Vs[stage][(i * NT + 64 * wave) * 8]);
         }
     };
     // Fragments: K key row col + 32*kb, term chunk 16*term + 8*half + t;
