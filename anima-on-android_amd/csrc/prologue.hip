@@ -340,6 +340,16 @@ constexpr int kPrepPitch = 132;                   // floats per staged row
 constexpr int kPrepTW = 36;                       // 32-bit words per transposed V^T row
 constexpr int kPrepLds = 2 * 128 * kPrepTW;       // >= kPrepRows * kPrepPitch
 static_assert(kPrepLds >= kPrepRows * kPrepPitch, "LDS union");
+// RoPE table rows ([64 pairs][4] f32, 1 KiB per token) staged once per row
+// group when its rows span at most this many tokens (H >= 16): read from L2
+// per row instead, every table row would be fetched once per head.
+constexpr int kPrepTabTokens = 4;
+constexpr int kPrepTabFloats = kPrepTabTokens * 256;
+// The LDS array: rows + table for Q/K groups, the two transposed V^T halves
+// for V tiles (37 KiB: four blocks per CU).
+constexpr int kPrepLdsAll = kPrepRows * kPrepPitch + kPrepTabFloats > kPrepLds
+                                ? kPrepRows * kPrepPitch + kPrepTabFloats
+                                : kPrepLds;
 
 struct PrepArgs {
     const float *x[2];  // q, k
@@ -364,7 +374,7 @@ __device__ __forceinline__ unsigned pack_bf16x2(float a, float b)
 template <int OUT>
 __global__ __launch_bounds__(256) void prep_qkv_kernel(PrepArgs a)
 {
-    __shared__ __attribute__((aligned(16))) float lds[kPrepLds];
+    __shared__ __attribute__((aligned(16))) float lds[kPrepLdsAll];
     __shared__ float inv[kPrepRows];
     const int t = threadIdx.x;
     const int u = blockIdx.x;
@@ -385,6 +395,22 @@ __global__ __launch_bounds__(256) void prep_qkv_kernel(PrepArgs a)
                 *reinterpret_cast<f32x4 *>(&lds[rr * kPrepPitch + 4 * c4]) =
                     *reinterpret_cast<const f32x4 *>(x + int64_t(bs) * a.ld + h * 128 + 4 * c4);
             }
+        }
+        // The RoPE table rows of the group's tokens bs0 .. bs1 (batch * S +
+        // token), staged after the rows when there are at most
+        // kPrepTabTokens of them: one 16-byte chunk (the 2x2 matrix of pair
+        // c) per thread, stored at (c % 4) * 16 + c / 4 so that the 16
+        // threads of a row, which read pairs 4i + e (i = 0..15) for one e at
+        // a time, hit 16 consecutive chunks.
+        const unsigned bs0 = unsigned(r0) / unsigned(a.H);
+        const unsigned bs1 = unsigned(min(r0 + kPrepRows, a.rows) - 1) / unsigned(a.H);
+        const bool tab_lds = a.freqs && bs1 - bs0 < unsigned(kPrepTabTokens);
+        float *tab = lds + kPrepRows * kPrepPitch;
+        if (tab_lds && bs0 + unsigned(t >> 6) <= bs1) {
+            const int c = t & 63;
+            *reinterpret_cast<f32x4 *>(&tab[(t >> 6) * 256 + 4 * ((c & 3) * 16 + (c >> 2))]) =
+                *reinterpret_cast<const f32x4 *>(
+                    a.freqs + int64_t((bs0 + unsigned(t >> 6)) % unsigned(a.S)) * 256 + 4 * c);
         }
         __syncthreads();
         if (t < kPrepRows) {
@@ -426,11 +452,15 @@ __global__ __launch_bounds__(256) void prep_qkv_kernel(PrepArgs a)
             }
             f32x4 lo = ya, hi = yb;
             if (a.freqs) {
-                const int s = int((unsigned(r) / unsigned(a.H)) % unsigned(a.S));
-                const f32x4 *fq = reinterpret_cast<const f32x4 *>(a.freqs + int64_t(s) * 256 + 4 * p0);
+                const unsigned bs = unsigned(r) / unsigned(a.H);
+                const f32x4 *fq = reinterpret_cast<const f32x4 *>(
+                    a.freqs + int64_t(bs % unsigned(a.S)) * 256 + 4 * p0);
+                const f32x4 *fl =
+                    reinterpret_cast<const f32x4 *>(tab + (bs - bs0) * 256 + 4 * (t & 15));
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const f32x4 c = fq[e];  // [c00, c01, c10, c11] of pair p0 + e
+                    // [c00, c01, c10, c11] of pair p0 + e
+                    const f32x4 c = tab_lds ? fl[16 * e] : fq[e];
                     lo[e] = c.x * ya[e] + c.y * yb[e];
                     hi[e] = c.z * ya[e] + c.w * yb[e];
                 }
