@@ -329,27 +329,32 @@ bool d128_eligible(const RowProblem &p)
 // Q rows and K rows (RMSNorm, RoPE, written dense as f32, bf16 or bf16 term
 // rows) and, for the bf16-MFMA kernels, V packed as V^T (bf16 or hi/lo term
 // rows; the layout of vt_pack_kernel / vt_pack_terms_kernel).  The work is a
-// single grid of 64-row groups of Q, then of K, then 64-key tiles of V, so
-// the three streams share one ramp and one tail instead of three, and every
-// block keeps 32 KiB of loads in flight.  Row arithmetic is that of
+// single grid of 32-row groups of Q, then of K, then 32-key halves of V^T
+// tiles, so the three streams share one ramp and one tail instead of three,
+// and every block keeps 16 KiB of loads in flight.  Row arithmetic is that of
 // rows_d128_block (bit-identical outputs); q, k and v are [B, S, H, 128]
 // views whose token rows are `ld` elements apart (column blocks of a fused
 // projection allowed), batch entries S * ld apart.
-constexpr int kPrepRows = 64;
+constexpr int kPrepRows = 32;
 constexpr int kPrepPitch = 132;                   // floats per staged row
-constexpr int kPrepTW = 36;                       // 32-bit words per transposed V^T row
+// Row groups of 32 and V^T blocks of 32 keys (half a 64-key tile) keep the
+// block at 20 KiB of LDS, eight blocks per CU: against 64-row groups and
+// whole tiles (37 KiB, four blocks) 62.5 against 69.9 us (bf16) and 88.3
+// against 89.7 us (f32x3) for 4096 tokens, B=2, H=16.
+constexpr int kPrepVKeys = 32;                    // keys per V^T block (half a 64-key tile)
+constexpr int kPrepTW = kPrepVKeys / 2 + 4;        // 32-bit words per transposed V^T row
 constexpr int kPrepLds = 2 * 128 * kPrepTW;       // >= kPrepRows * kPrepPitch
 static_assert(kPrepLds >= kPrepRows * kPrepPitch, "LDS union");
 // RoPE table rows ([64 pairs][4] f32, 1 KiB per token) staged once per row
 // group when its rows span at most this many tokens (H >= 16): read from L2
-// per row instead, every table row would be fetched once per head.
-constexpr int kPrepTabTokens = 4;
+// per row instead, every table row would be fetched once per head
+// (one-launch prologue 93 -> 89 us f32x3, 73 -> 70 us bf16 at 64-row groups).
+constexpr int kPrepTabTokens = 2;
 constexpr int kPrepTabFloats = kPrepTabTokens * 256;
-// The LDS array: rows + table for Q/K groups, the two transposed V^T halves
-// for V tiles (37 KiB: four blocks per CU).
-constexpr int kPrepLdsAll = kPrepRows * kPrepPitch + kPrepTabFloats > kPrepLds
-                                ? kPrepRows * kPrepPitch + kPrepTabFloats
-                                : kPrepLds;
+// The LDS array: rows, table and 1/rms for Q/K groups, the two transposed
+// V^T term blocks for V (20 KiB: eight blocks per CU).
+constexpr int kPrepQKFloats = kPrepRows * kPrepPitch + kPrepTabFloats + kPrepRows;
+constexpr int kPrepLdsAll = kPrepQKFloats > kPrepLds ? kPrepQKFloats : kPrepLds;
 
 struct PrepArgs {
     const float *x[2];  // q, k
@@ -360,7 +365,7 @@ struct PrepArgs {
     unsigned short *vt; // [B*H][128 or 256 rows][sp]
     int64_t ld, sp;
     int rows;           // B*S*H (< 2^31, checked at launch)
-    int qk_units;       // 64-row groups per tensor
+    int qk_units;       // row groups per tensor
     int S, H, n_vtiles;
     float eps;
 };
@@ -375,7 +380,7 @@ template <int OUT>
 __global__ __launch_bounds__(256) void prep_qkv_kernel(PrepArgs a)
 {
     __shared__ __attribute__((aligned(16))) float lds[kPrepLdsAll];
-    __shared__ float inv[kPrepRows];
+    float *const inv = lds + kPrepRows * kPrepPitch + kPrepTabFloats;  // Q/K groups
     const int t = threadIdx.x;
     const int u = blockIdx.x;
     if (u < 2 * a.qk_units) {
@@ -406,7 +411,7 @@ __global__ __launch_bounds__(256) void prep_qkv_kernel(PrepArgs a)
         const unsigned bs1 = unsigned(min(r0 + kPrepRows, a.rows) - 1) / unsigned(a.H);
         const bool tab_lds = a.freqs && bs1 - bs0 < unsigned(kPrepTabTokens);
         float *tab = lds + kPrepRows * kPrepPitch;
-        if (tab_lds && bs0 + unsigned(t >> 6) <= bs1) {
+        if (tab_lds && (t >> 6) < kPrepTabTokens && bs0 + unsigned(t >> 6) <= bs1) {
             const int c = t & 63;
             *reinterpret_cast<f32x4 *>(&tab[(t >> 6) * 256 + 4 * ((c & 3) * 16 + (c >> 2))]) =
                 *reinterpret_cast<const f32x4 *>(
@@ -480,19 +485,19 @@ __global__ __launch_bounds__(256) void prep_qkv_kernel(PrepArgs a)
     }
     if (OUT == 0)
         return;
-    // V tile: 64 keys of one (batch, head), transposed through LDS into rows
+    // V block: kPrepVKeys keys of one (batch, head), transposed through LDS into rows
     // of V^T with keys in vt_key_pos order; adjacent key pairs share a word.
     const unsigned vu = unsigned(u - 2 * a.qk_units);
     const unsigned bh = vu / unsigned(a.n_vtiles);
     const int tile = int(vu - bh * unsigned(a.n_vtiles));
     const unsigned b = bh / unsigned(a.H);
     const int h = int(bh - b * unsigned(a.H));
-    const int key0 = tile * 64;
+    const int key0 = tile * kPrepVKeys;
     const float *vp = a.v + int64_t(b) * a.S * a.ld + h * 128;
     unsigned *Th = reinterpret_cast<unsigned *>(lds);
     unsigned *Tl = Th + 128 * kPrepTW;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kPrepVKeys / 16; ++i) {
         const int f = t + 256 * i;  // (key pair, float4 column) of the tile
         const int pr = f >> 5, c4 = f & 31;
         const int k0 = key0 + 2 * pr, k1 = k0 + 1;
@@ -517,9 +522,9 @@ __global__ __launch_bounds__(256) void prep_qkv_kernel(PrepArgs a)
     constexpr int vrows = OUT == 2 ? 256 : 128;
     unsigned short *tp = a.vt + int64_t(bh) * vrows * a.sp + key0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kPrepVKeys / 16; ++i) {
         const int f = t + 256 * i;  // 16-byte chunk: d row, 8 keys
-        const int d = f >> 3, c = f & 7;
+        const int d = f / (kPrepVKeys / 8), c = f % (kPrepVKeys / 8);
         *reinterpret_cast<f32x4 *>(tp + d * a.sp + 8 * c) =
             *reinterpret_cast<const f32x4 *>(&Th[d * kPrepTW + 4 * c]);
         if (OUT == 2)
@@ -605,7 +610,7 @@ bool launch_prep_qkv(const PrepProblem &p, hipStream_t st)
     a.vt = p.vt;
     const int64_t sp = vt_padded_len(p.S);
     const int64_t nblk = 2 * ((rows + kPrepRows - 1) / kPrepRows) +
-                         (p.mode == kAttnF32 ? 0 : int64_t(p.B) * p.H * (sp / kVtTile));
+                         (p.mode == kAttnF32 ? 0 : int64_t(p.B) * p.H * (sp / kPrepVKeys));
     if (rows > INT32_MAX - kPrepRows || nblk > INT32_MAX)
         return fail("prep_qkv: problem too large for one launch");
     a.ld = p.ld;
@@ -614,7 +619,7 @@ bool launch_prep_qkv(const PrepProblem &p, hipStream_t st)
     a.qk_units = int((rows + kPrepRows - 1) / kPrepRows);
     a.S = p.S;
     a.H = p.H;
-    a.n_vtiles = int(sp / kVtTile);
+    a.n_vtiles = int(sp / kPrepVKeys);
     a.eps = p.eps;
     switch (p.mode) {
     case kAttnF32:
