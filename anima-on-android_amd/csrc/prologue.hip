@@ -329,8 +329,8 @@ bool d128_eligible(const RowProblem &p)
 // Q rows and K rows (RMSNorm, RoPE, written dense as f32, bf16 or bf16 term
 // rows) and, for the bf16-MFMA kernels, V packed as V^T (bf16 or hi/lo term
 // rows; the layout of vt_pack_kernel / vt_pack_terms_kernel).  The work is a
-// single grid of 32-row groups of Q, then of K, then 32-key halves of V^T
-// tiles, so the three streams share one ramp and one tail instead of three,
+// single grid of 32-key halves of V^T tiles, then 32-row groups of K, then
+// of Q, so the three streams share one ramp and one tail instead of three,
 // and every block keeps 16 KiB of loads in flight.  Row arithmetic is that of
 // rows_d128_block (bit-identical outputs); q, k and v are [B, S, H, 128]
 // views whose token rows are `ld` elements apart (column blocks of a fused
@@ -367,6 +367,7 @@ struct PrepArgs {
     int rows;           // B*S*H (< 2^31, checked at launch)
     int qk_units;       // row groups per tensor
     int S, H, n_vtiles;
+    int v_units;        // V^T blocks (0 in f32 mode); they come first in the grid
     float eps;
 };
 
@@ -382,10 +383,14 @@ __global__ __launch_bounds__(256) void prep_qkv_kernel(PrepArgs a)
     __shared__ __attribute__((aligned(16))) float lds[kPrepLdsAll];
     float *const inv = lds + kPrepRows * kPrepPitch + kPrepTabFloats;  // Q/K groups
     const int t = threadIdx.x;
-    const int u = blockIdx.x;
-    if (u < 2 * a.qk_units) {
-        const int p = u >= a.qk_units ? 1 : 0;
-        const int r0 = (u - p * a.qk_units) * kPrepRows;
+    // Grid order: V^T blocks, then K row groups, then Q row groups, so the
+    // rows the attention kernel reads first (Q) are the last written (and the
+    // launch itself runs faster: 88.8 -> 81.3 us f32x3, 62.7 -> 60.3 us bf16
+    // at 4096 tokens, B=2, H=16; the step 0.85 % and 0.6 % faster).
+    const int u = int(blockIdx.x) - a.v_units;
+    if (u >= 0) {
+        const int p = u < a.qk_units ? 1 : 0;
+        const int r0 = (p ? u : u - a.qk_units) * kPrepRows;
         const float *x = a.x[p];
         const int c4 = t & 31;
         // 32-bit row arithmetic (rows < 2^31): the token index r / H and the
@@ -487,7 +492,7 @@ __global__ __launch_bounds__(256) void prep_qkv_kernel(PrepArgs a)
         return;
     // V block: kPrepVKeys keys of one (batch, head), transposed through LDS into rows
     // of V^T with keys in vt_key_pos order; adjacent key pairs share a word.
-    const unsigned vu = unsigned(u - 2 * a.qk_units);
+    const unsigned vu = blockIdx.x;
     const unsigned bh = vu / unsigned(a.n_vtiles);
     const int tile = int(vu - bh * unsigned(a.n_vtiles));
     const unsigned b = bh / unsigned(a.H);
@@ -620,6 +625,7 @@ bool launch_prep_qkv(const PrepProblem &p, hipStream_t st)
     a.S = p.S;
     a.H = p.H;
     a.n_vtiles = int(sp / kPrepVKeys);
+    a.v_units = p.mode == kAttnF32 ? 0 : int(int64_t(p.B) * p.H * (sp / kPrepVKeys));
     a.eps = p.eps;
     switch (p.mode) {
     case kAttnF32:
