@@ -30,6 +30,10 @@ CASES = [  # B, S, H, grid (None: no RoPE), fused projection layout, norm weight
     (2, 77, 3, (7, 11), True, True),
     (1, 1000, 16, None, True, True),
     (3, 64, 2, (8, 8), False, True),
+    # RoPE table rows staged in LDS per 32-row group (H >= 16): a last group
+    # holding one token (1 * 77 * 16 rows), and one token per group (H = 32).
+    (1, 77, 16, (7, 11), True, True),
+    (2, 64, 32, (8, 8), False, True),
 ]
 
 
