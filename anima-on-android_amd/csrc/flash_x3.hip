@@ -198,9 +198,10 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
         // Tile j+1 into the other stage, read by every wave in iteration j-1
         // (before the barrier that ended it).  A copy instruction holds its
         // wave at issue for about a hundred cycles, so the two waves of a
-        // SIMD (w and w + 4) do not issue theirs together: waves 0-3 right
-        // after the barrier, waves 4-7 after their score MFMAs (1.4 % faster
-        // at 4096 tokens than all waves at the top of the tile).
+        // SIMD (w and w + 4, waves being placed round-robin on the four
+        // SIMDs) do not issue theirs together: waves 0-3 right after the
+        // barrier, waves 4-7 after their score MFMAs (1.0-1.4 % faster at
+        // 4096 tokens than all waves at the top of the tile).
         const bool late_copies = (wave >> 2) & 1;
         const bool copy_next = j + 1 < ntiles;
         if (copy_next && !late_copies) {
