@@ -13,6 +13,7 @@
 #include <condition_variable>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -87,7 +88,10 @@ struct CallTimer {
 
 // Host memcpy split over the caller and a few parked worker threads.  One
 // thread copies pageable memory into pinned memory at ~30 GB/s on an MI355X
-// host, four at ~73 GB/s, above the ~57 GB/s of the host link's DMA.
+// host, four at ~73 GB/s, above the ~57 GB/s of the host link's DMA.  A
+// grouped call (run_groups) feeds both directions' copies through the pool,
+// and a fresh output array takes its page faults in the copy-out: six
+// threads ran such calls 3-17 % faster than four, eight no faster than six.
 class CopyPool {
   public:
     static CopyPool &get()
@@ -127,7 +131,7 @@ class CopyPool {
     CopyPool() : pid_(getpid())
     {
         const unsigned hw = std::thread::hardware_concurrency();
-        const int n = int(std::min(4u, std::max(1u, hw / 2)));
+        const int n = int(std::min(6u, std::max(1u, hw / 2)));
         for (int i = 1; i < n; ++i)
             workers_.emplace_back([this, i] { worker(i); });
         for (std::thread &t : workers_)
@@ -294,10 +298,13 @@ struct Runtime {
     hipStream_t stream = nullptr;
     DevBuf q, k, v, o, w0, w1, fr, q2, k2, v2, scratch;
     CallTimer timer;
-    Staging staging;
-    // Second stream and events of the host SDPA's two-group pipeline.
-    hipStream_t cstream = nullptr;
-    hipEvent_t up_ev[2] = {nullptr, nullptr}, done_ev[2] = {nullptr, nullptr};
+    Staging staging;   // uploads, and the single-stream calls' downloads
+    Staging dstaging;  // downloads of a grouped call (run_groups)
+    // Compute and download streams and the per-group events of a grouped
+    // host-pointer call.
+    static constexpr int kMaxGroups = 4;
+    hipStream_t cstream = nullptr, dstream = nullptr;
+    hipEvent_t up_ev[kMaxGroups] = {}, done_ev[kMaxGroups] = {};
 };
 
 Runtime &rt()
@@ -326,23 +333,23 @@ bool ensure_ready(Runtime &r)
     return true;
 }
 
-// The compute stream (default priority, like every stream here) and the
-// events of the host SDPA pipeline, created at its first use.
+// The compute and download streams (default priority, like every stream
+// here) and the events of a grouped host-pointer call, created at first use.
 bool ensure_pipeline(Runtime &r)
 {
-    if (r.cstream)
-        return true;
-    if (!hip_ok(hipStreamCreateWithFlags(&r.cstream, hipStreamNonBlocking), "hipStreamCreate"))
-        return false;
-    for (hipEvent_t *e : {&r.up_ev[0], &r.up_ev[1], &r.done_ev[0], &r.done_ev[1]})
-        if (!hip_ok(hipEventCreateWithFlags(e, hipEventDisableTiming), "hipEventCreate"))
+    for (hipStream_t *s : {&r.cstream, &r.dstream})
+        if (!*s && !hip_ok(hipStreamCreateWithFlags(s, hipStreamNonBlocking), "hipStreamCreate"))
             return false;
+    for (int g = 0; g < Runtime::kMaxGroups; ++g)
+        for (hipEvent_t *e : {&r.up_ev[g], &r.done_ev[g]})
+            if (!*e && !hip_ok(hipEventCreateWithFlags(e, hipEventDisableTiming), "hipEventCreate"))
+                return false;
     return true;
 }
 
-// Drains both runtime streams when a host-pointer call returns early after
-// enqueuing work, so that no kernel of a failed call still reads or writes
-// the shared workspace when the next call uploads into it.
+// Drains the runtime streams when a host-pointer call returns early after
+// enqueuing work, so that no kernel or copy of a failed call still reads or
+// writes the shared workspace or staging when the next call uses them.
 struct DrainOnError {
     Runtime &r;
     bool done = false;
@@ -350,9 +357,9 @@ struct DrainOnError {
     {
         if (done || !r.stream)
             return;
-        (void)hipStreamSynchronize(r.stream);
-        if (r.cstream)
-            (void)hipStreamSynchronize(r.cstream);
+        for (hipStream_t s : {r.stream, r.cstream, r.dstream})
+            if (s)
+                (void)hipStreamSynchronize(s);
     }
 };
 
@@ -464,6 +471,192 @@ bool finish_call(Runtime &r)
     return true;
 }
 
+// One host <-> device copy of a grouped host-pointer call.
+struct Piece {
+    char *dst;
+    const char *src;
+    size_t n;
+};
+typedef std::vector<Piece> Pieces[Runtime::kMaxGroups];
+
+// A host-pointer call as G groups (1 <= G <= kMaxGroups): group g's uploads
+// on the runtime stream, its kernels (launch(g, stream)) on the compute
+// stream once they have landed, its downloads on the download stream once
+// the kernels end.  Pieces of kMinStaged bytes or more move in chunks through
+// pinned slots, one ring per direction.  The calling thread copies a landed
+// download chunk out whenever one is ready and stages the next upload chunk
+// otherwise, so the later groups' uploads and the earlier groups' downloads
+// use the host link's two directions at the same time.  With G == 1 all of it
+// runs on the runtime stream.  Returns once every download has reached host
+// memory; the call's timing marks are those of finish_call (end of the last
+// upload to the start of the last group's downloads, first upload to last
+// download).
+bool run_groups(Runtime &r, int G, const Pieces &up, const Pieces &down,
+                const std::function<bool(int, hipStream_t)> &launch)
+{
+    if (G < 1 || G > Runtime::kMaxGroups)
+        return fail("internal: group count out of range");
+    const hipStream_t st = r.stream;
+    if (G > 1 && !ensure_pipeline(r))
+        return false;
+    const hipStream_t cs = G > 1 ? r.cstream : st, ds = G > 1 ? r.dstream : st;
+    Staging &us = r.staging, &dsg = r.dstaging;
+    const bool staged = us.ensure() && dsg.ensure();
+
+    struct Chunk {
+        int g;
+        char *dst;
+        const char *src;
+        size_t n;
+        bool staged;
+    };
+    std::vector<Chunk> uc, dc;
+    for (int g = 0; g < G; ++g) {
+        for (int dir = 0; dir < 2; ++dir)
+            for (const Piece &p : (dir ? down : up)[g]) {
+                std::vector<Chunk> &out = dir ? dc : uc;
+                if (p.n == 0)
+                    continue;
+                if (!staged || p.n < Staging::kMinStaged) {
+                    out.push_back({g, p.dst, p.src, p.n, false});
+                    continue;
+                }
+                for (size_t off = 0; off < p.n; off += Staging::kChunk)
+                    out.push_back(
+                        {g, p.dst + off, p.src + off, std::min(Staging::kChunk, p.n - off), true});
+            }
+    }
+
+    CallTimer &t = r.timer;
+    auto rec = [&](int i, hipStream_t s) {
+        return !t.ev[i] || hip_ok(hipEventRecord(t.ev[i], s), "hipEventRecord");
+    };
+    size_t ui = 0;  // next upload chunk
+    int uslot = 0;  // pinned upload slot of the next staged upload chunk
+    int launched = 0;
+    auto launch_group = [&](int g) {
+        if (G > 1 && !(hip_ok(hipEventRecord(r.up_ev[g], st), "hipEventRecord") &&
+                       hip_ok(hipStreamWaitEvent(cs, r.up_ev[g], 0), "hipStreamWaitEvent")))
+            return false;
+        if (!launch(g, cs))
+            return false;
+        return G == 1 || (hip_ok(hipEventRecord(r.done_ev[g], cs), "hipEventRecord") &&
+                          hip_ok(hipStreamWaitEvent(ds, r.done_ev[g], 0), "hipStreamWaitEvent"));
+    };
+    // Launches every group whose uploads have all been issued (uc is ordered
+    // by group).
+    auto launch_ready = [&] {
+        while (launched < G && (ui == uc.size() || uc[ui].g > launched))
+            if (!launch_group(launched++))
+                return false;
+        return true;
+    };
+    auto upload_one = [&] {
+        const Chunk &c = uc[ui];
+        if (ui == 0 && !t.up) {  // the call's first upload
+            if (!rec(0, st))
+                return false;
+            t.up = true;
+        }
+        if (c.staged) {
+            const int s = uslot;
+            uslot = (uslot + 1) % Staging::kSlots;
+            if (!us.drain(s))
+                return false;
+            CopyPool::get().copy(us.slot[s], c.src, c.n);
+            if (!us.issue(s, c.dst, us.slot[s], c.n, hipMemcpyHostToDevice, st))
+                return false;
+        } else if (!hip_ok(hipMemcpyAsync(c.dst, c.src, c.n, hipMemcpyHostToDevice, st),
+                           "H2D copy")) {
+            return false;
+        }
+        ++ui;
+        return ui < uc.size() || rec(1, st);
+    };
+
+    // Downloads: chunks [dd, di) are enqueued; the staged ones among them sit
+    // in slots dslot[], oldest first.
+    size_t di = 0, dd = 0;
+    int dnext = 0;  // pinned download slot of the next staged download chunk
+    std::vector<int> dslot;
+    size_t dslot_head = 0;
+    const size_t last_group_first =
+        std::find_if(dc.begin(), dc.end(), [&](const Chunk &c) { return c.g == G - 1; }) -
+        dc.begin();
+    auto enqueue_downloads = [&] {
+        while (di < dc.size() && dc[di].g < launched &&
+               (!dc[di].staged || dslot.size() - dslot_head < size_t(Staging::kSlots))) {
+            const Chunk &c = dc[di];
+            if (di == last_group_first) {
+                if (!rec(2, ds))
+                    return false;
+                t.down = true;
+            }
+            if (c.staged) {
+                const int s = dnext;
+                dnext = (dnext + 1) % Staging::kSlots;
+                if (!dsg.drain(s) ||
+                    !dsg.issue(s, dsg.slot[s], c.src, c.n, hipMemcpyDeviceToHost, ds))
+                    return false;
+                dslot.push_back(s);
+            } else if (!hip_ok(hipMemcpyAsync(c.dst, c.src, c.n, hipMemcpyDeviceToHost, ds),
+                               "D2H copy")) {
+                return false;
+            }
+            ++di;
+            if (di == dc.size() && !rec(3, ds))
+                return false;
+        }
+        return true;
+    };
+    // Oldest enqueued staged download: landed (or, with wait, once it lands)
+    // -> copied out of its slot.  Unstaged chunks before it need no copy-out.
+    auto finish_download = [&](bool wait, bool &did) {
+        did = false;
+        while (dd < di && !dc[dd].staged)
+            ++dd;
+        if (dd == di)
+            return true;
+        const int s = dslot[dslot_head];
+        if (!wait) {
+            const hipError_t q = hipEventQuery(dsg.done[s]);
+            if (q == hipErrorNotReady)
+                return true;
+            if (!hip_ok(q, "staging query"))
+                return false;
+        }
+        if (!dsg.drain(s))
+            return false;
+        CopyPool::get().copy(dc[dd].dst, dsg.slot[s], dc[dd].n);
+        ++dslot_head;
+        ++dd;
+        did = true;
+        return true;
+    };
+
+    if (!launch_ready())
+        return false;
+    while (launched < G || ui < uc.size() || dd < dc.size()) {
+        if (!enqueue_downloads())
+            return false;
+        bool did = false;
+        if (!finish_download(false, did))
+            return false;
+        if (did)
+            continue;
+        if (ui < uc.size()) {
+            if (!upload_one() || !launch_ready())
+                return false;
+            continue;
+        }
+        // Every group is launched and every download that fits is enqueued:
+        // wait for the oldest staged one (unstaged ones land with the stream).
+        if (!launch_ready() || !enqueue_downloads() || !finish_download(true, did))
+            return false;
+    }
+    return sync(ds);
+}
+
 // Kernels of the host-pointer SDPA for heads [h0, h0 + nh) of the uploaded
 // [BH, S, D] f32 workspace arrays, on stream st: the f32 flash kernel, or the
 // bf16 / f32x3 operand passes (Q and K rows, packed V^T) and their kernel.
@@ -529,18 +722,23 @@ bool sdpa_heads(Runtime &r, int64_t h0, int nh, int S_q, int S_kv, int D, float 
               : launch_flash_bf16(p, st, r.scratch.p, part_bytes);
 }
 
-// Head groups of a host-pointer SDPA.  Two when the copies are large and
-// half the heads still fill the GPU (flash_plan keeps 8-wave workgroups and
-// no key split): the second half's upload then overlaps the first half's
-// kernels on the runtime's compute stream, and the first half's output comes
-// back while the second half computes.
+// Head groups of a host-pointer SDPA: the most groups (4 or 2) that still
+// fill the GPU each (flash_plan keeps 8-wave workgroups and no key split)
+// when the copies are large, else one.  Group g+1 uploads while group g
+// computes, and group g's output comes back while later groups upload.
 int sdpa_groups(int BH, int S_q, int S_kv, int D)
 {
     const int64_t bytes = int64_t(BH) * (2 * int64_t(S_q) + 2 * int64_t(S_kv)) * D * 4;
-    if (BH < 2 || BH % 2 != 0 || bytes < (int64_t(64) << 20))
+    if (bytes < (int64_t(64) << 20))
         return 1;
-    const FlashPlan half = flash_plan(BH / 2, S_q, S_kv, D);
-    return half.waves == 8 && half.splits == 1 ? 2 : 1;
+    for (int G = Runtime::kMaxGroups; G > 1; G /= 2) {
+        if (BH % G != 0)
+            continue;
+        const FlashPlan part = flash_plan(BH / G, S_q, S_kv, D);
+        if (part.waves == 8 && part.splits == 1)
+            return G;
+    }
+    return 1;
 }
 
 // Shared body of the host-pointer SDPA entries ([BH, S, D] f32 host arrays).
@@ -558,7 +756,6 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
     if ((bf16 || x3) && D != 128)
         return fail(std::string("sdpa: the ") + (bf16 ? "bf16" : "f32x3") + " mode needs D == 128");
     Runtime &r = rt();
-    const hipStream_t st = r.stream;
     begin_call(r);
     const int G = sdpa_groups(BH, S_q, S_kv, D), nh = BH / G;
     if (!r.q.reserve(f32_bytes(nq), "workspace Q") || !r.o.reserve(f32_bytes(nq), "workspace O") ||
@@ -572,30 +769,24 @@ bool host_sdpa(const float *Q, const float *K, const float *V, float *out, int B
             !r.v2.reserve(size_t(BH) * w * D * vt_padded_len(S_kv) * 2, "workspace v^T"))
             return false;
     }
-    if (G > 1 && !ensure_pipeline(r))
-        return false;
-    const hipStream_t cs = G > 1 ? r.cstream : st;
     DrainOnError drain{r};
     const int64_t gq = int64_t(nh) * S_q * D, gk = int64_t(nh) * S_kv * D;  // elements per group
+    const auto dev = [](DevBuf &b, int64_t off) { return static_cast<char *>(b.p) + f32_bytes(off); };
+    const auto host = [](const float *p, int64_t off) {
+        return reinterpret_cast<const char *>(p) + f32_bytes(off);
+    };
+    Pieces up, down;
     for (int g = 0; g < G; ++g) {
-        if (!h2d(static_cast<float *>(r.q.p) + g * gq, Q + g * gq, f32_bytes(gq), st) ||
-            !h2d(static_cast<float *>(r.k.p) + g * gk, K + g * gk, f32_bytes(gk), st) ||
-            !h2d(static_cast<float *>(r.v.p) + g * gk, V + g * gk, f32_bytes(gk), st))
-            return false;
-        if (G > 1 && !(hip_ok(hipEventRecord(r.up_ev[g], st), "hipEventRecord") &&
-                       hip_ok(hipStreamWaitEvent(cs, r.up_ev[g], 0), "hipStreamWaitEvent")))
-            return false;
-        if (!sdpa_heads(r, int64_t(g) * nh, nh, S_q, S_kv, D, scale, causal, mode, cs))
-            return false;
-        if (G > 1 && !hip_ok(hipEventRecord(r.done_ev[g], cs), "hipEventRecord"))
-            return false;
+        up[g] = {{dev(r.q, g * gq), host(Q, g * gq), f32_bytes(gq)},
+                 {dev(r.k, g * gk), host(K, g * gk), f32_bytes(gk)},
+                 {dev(r.v, g * gk), host(V, g * gk), f32_bytes(gk)}};
+        down[g] = {{reinterpret_cast<char *>(out) + f32_bytes(g * gq), dev(r.o, g * gq),
+                    f32_bytes(gq)}};
     }
-    for (int g = 0; g < G; ++g) {
-        if (G > 1 && !hip_ok(hipStreamWaitEvent(st, r.done_ev[g], 0), "hipStreamWaitEvent"))
-            return false;
-        if (!d2h(out + g * gq, static_cast<float *>(r.o.p) + g * gq, f32_bytes(gq), st))
-            return false;
-    }
+    if (!run_groups(r, G, up, down, [&](int g, hipStream_t s) {
+            return sdpa_heads(r, int64_t(g) * nh, nh, S_q, S_kv, D, scale, causal, mode, s);
+        }))
+        return false;
     drain.done = true;
     return finish_call(r);
 }
@@ -702,21 +893,27 @@ void anima_rt_destroy(void)
     std::lock_guard<std::recursive_mutex> g(r.mu);
     if (!r.ready)
         return;
-    (void)hipStreamSynchronize(r.stream);
+    for (hipStream_t s : {r.stream, r.cstream, r.dstream})
+        if (s)
+            (void)hipStreamSynchronize(s);
     for (DevBuf *b : {&r.q, &r.k, &r.v, &r.o, &r.w0, &r.w1, &r.fr, &r.q2, &r.k2, &r.v2, &r.scratch})
         b->release();
     r.staging.release();
-    if (r.cstream)
-        (void)hipStreamSynchronize(r.cstream);
-    for (hipEvent_t *e : {&r.timer.ev[0], &r.timer.ev[1], &r.timer.ev[2], &r.timer.ev[3],
-                          &r.up_ev[0], &r.up_ev[1], &r.done_ev[0], &r.done_ev[1]}) {
+    r.dstaging.release();
+    std::vector<hipEvent_t *> evs = {&r.timer.ev[0], &r.timer.ev[1], &r.timer.ev[2], &r.timer.ev[3]};
+    for (int g = 0; g < Runtime::kMaxGroups; ++g) {
+        evs.push_back(&r.up_ev[g]);
+        evs.push_back(&r.done_ev[g]);
+    }
+    for (hipEvent_t *e : evs) {
         if (*e)
             (void)hipEventDestroy(*e);
         *e = nullptr;
     }
-    if (r.cstream) {
-        (void)hipStreamDestroy(r.cstream);
-        r.cstream = nullptr;
+    for (hipStream_t *s : {&r.cstream, &r.dstream}) {
+        if (*s)
+            (void)hipStreamDestroy(*s);
+        *s = nullptr;
     }
     (void)hipStreamDestroy(r.stream);
     r.stream = nullptr;
@@ -1266,24 +1463,21 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
         return fail("anima_hip_attention: null pointer");
     const hipStream_t st = r.stream;
     begin_call(r);
-    // Two batch groups, like the SDPA's head groups, when the copies are
-    // large and half the batch still fills the GPU: the second half's upload
-    // overlaps the first half's kernels.
+    // Batch groups, like the SDPA's head groups (sdpa_groups), when the
+    // copies are large and each group still fills the GPU.
     const int64_t bytes = 2 * f32_bytes(nq) + 2 * f32_bytes(nk);
-    const FlashPlan half = flash_plan(int64_t(B / 2) * H, S_q, S_kv, D);
-    const int G = B % 2 == 0 && bytes >= (int64_t(64) << 20) && half.waves == 8 &&
-                          half.splits == 1
-                      ? 2
-                      : 1;
+    int G = 1;
+    for (int c = Runtime::kMaxGroups; c > 1 && G == 1 && bytes >= (int64_t(64) << 20); c /= 2) {
+        const FlashPlan part = flash_plan(int64_t(B / c) * H, S_q, S_kv, D);
+        if (B % c == 0 && part.waves == 8 && part.splits == 1)
+            G = c;
+    }
     const int Bg = B / G;
     const size_t scratch = attention_scratch_bytes(Bg, S_q, Bg, S_kv, H, D, am, false);
     if (!r.q.reserve(f32_bytes(nq), "workspace q") || !r.k.reserve(f32_bytes(nk), "workspace k") ||
         !r.v.reserve(f32_bytes(nk), "workspace v") || !r.o.reserve(f32_bytes(nq), "workspace o") ||
         !r.scratch.reserve(scratch, "workspace scratch"))
         return false;
-    if (G > 1 && !ensure_pipeline(r))
-        return false;
-    const hipStream_t cs = G > 1 ? r.cstream : st;
     DrainOnError drain{r};
     AttnInputs in;
     if (!upload_optional(r.w0, q_norm_w, D, "workspace q_norm", st, in.q_norm_w) ||
@@ -1299,30 +1493,24 @@ bool anima_hip_attention(const float *q, const float *k, const float *v, const f
     in.eps = eps;
     in.mode = am;
     const int64_t gq = nq / G, gk = nk / G;  // elements per group
+    float *const qd = static_cast<float *>(r.q.p), *const kd = static_cast<float *>(r.k.p);
+    float *const vd = static_cast<float *>(r.v.p), *const od = static_cast<float *>(r.o.p);
+    const auto bytes_of = [](const float *p) { return reinterpret_cast<const char *>(p); };
+    Pieces up, down;
     for (int g = 0; g < G; ++g) {
-        float *qd = static_cast<float *>(r.q.p) + g * gq, *kd = static_cast<float *>(r.k.p) + g * gk;
-        float *vd = static_cast<float *>(r.v.p) + g * gk;
-        if (!h2d(qd, q + g * gq, f32_bytes(gq), st) || !h2d(kd, k + g * gk, f32_bytes(gk), st) ||
-            !h2d(vd, v + g * gk, f32_bytes(gk), st))
-            return false;
-        if (G > 1 && !(hip_ok(hipEventRecord(r.up_ev[g], st), "hipEventRecord") &&
-                       hip_ok(hipStreamWaitEvent(cs, r.up_ev[g], 0), "hipStreamWaitEvent")))
-            return false;
-        in.q = qd;
-        in.k = kd;
-        in.v = vd;
-        in.out = static_cast<float *>(r.o.p) + g * gq;
-        if (!run_attention(in, r.scratch.p, cs))
-            return false;
-        if (G > 1 && !hip_ok(hipEventRecord(r.done_ev[g], cs), "hipEventRecord"))
-            return false;
+        up[g] = {{reinterpret_cast<char *>(qd + g * gq), bytes_of(q + g * gq), f32_bytes(gq)},
+                 {reinterpret_cast<char *>(kd + g * gk), bytes_of(k + g * gk), f32_bytes(gk)},
+                 {reinterpret_cast<char *>(vd + g * gk), bytes_of(v + g * gk), f32_bytes(gk)}};
+        down[g] = {{reinterpret_cast<char *>(out + g * gq), bytes_of(od + g * gq), f32_bytes(gq)}};
     }
-    for (int g = 0; g < G; ++g) {
-        if (G > 1 && !hip_ok(hipStreamWaitEvent(st, r.done_ev[g], 0), "hipStreamWaitEvent"))
-            return false;
-        if (!d2h(out + g * gq, static_cast<float *>(r.o.p) + g * gq, f32_bytes(gq), st))
-            return false;
-    }
+    if (!run_groups(r, G, up, down, [&](int g, hipStream_t s) {
+            in.q = qd + g * gq;
+            in.k = kd + g * gk;
+            in.v = vd + g * gk;
+            in.out = od + g * gq;
+            return run_attention(in, r.scratch.p, s);
+        }))
+        return false;
     drain.done = true;
     return finish_call(r);
 }

@@ -511,9 +511,9 @@ def dropin_call(c, host, B, H, S, D, iters=3):
     anima_rt_run_sdpa_flash, on host numpy [B*H, S, D] buffers: host wall
     time, and from the library's timing hook (anima_hip_last_call_ms) the
     device time of the whole call (PCIe copies included) and the part of it
-    in which kernels ran with no copy beside them.  Large calls run as two
-    head groups, the second group's upload overlapping the first group's
-    kernels, so kernels and copies overlap."""
+    in which kernels ran with no copy beside them.  Large calls run as head
+    groups: later groups' uploads overlap earlier groups' kernels and
+    downloads."""
     import numpy as np
     from anima_hip import rt
     q, k, v = (np.ascontiguousarray(x.transpose(0, 2, 1, 3)).reshape(B * H, S, D) for x in host)

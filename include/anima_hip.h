@@ -470,12 +470,12 @@ bool anima_hip_dit_euler_dev(anima_hip_dit *dit, float *latent, const float *sig
 
 /* Timing hook: device time of the last completed host-pointer call (the
  * anima_rt_run_* drop-ins, anima_hip_sdpa, anima_hip_attention,
- * anima_hip_cross_attention), from HIP events on the library's stream:
- * kernel_ms between the end of its uploads and the start of its downloads
- * (for a large SDPA call run as two overlapped head groups, the kernel time
- * that no copy hid), total_ms from the first upload to the end of the last
- * download (PCIe included).  Either pointer may be NULL.  False before any
- * such call. */
+ * anima_hip_cross_attention), from HIP events on the library's streams:
+ * kernel_ms between the end of its uploads and the start of its last
+ * group's downloads (for a large call run as overlapped head or batch
+ * groups, the kernel time that no copy hid), total_ms from the first upload
+ * to the end of the last download (PCIe included).  Either pointer may be
+ * NULL.  False before any such call. */
 bool anima_hip_last_call_ms(float *kernel_ms, float *total_ms);
 
 /* ---- Device memory for hosts without another HIP binding ---- */
