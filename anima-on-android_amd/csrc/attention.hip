@@ -199,10 +199,25 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     void *part = cur;
     const size_t part_bytes = flash_plan(int64_t(B) * H, S_q, S_kv, D).bytes;
 
+    // Cross-attention (K/V prepared, no RoPE) in f32x3 on a grid of at least
+    // one 8-wave workgroup per CU: the flash kernel prepares its own query
+    // rows from the raw projection (RawQ), one pass over HBM fewer.  The
+    // kernel reads the same bytes for a raw f32 row as for a [hi | lo] term
+    // row (4096 x 512, B = 2: 119.9 -> 108.9 us).  Smaller grids keep the row
+    // pass (256 x 512: 28.0 against 28.9 us on the raw path, whose copies go
+    // out ahead of Q), and split grids would repeat it per split.
+    // Self-attention keeps it too, where the RoPE table's reads at each
+    // workgroup's start cost more than the pass.
+    const auto a16 = [](const void *x) { return (reinterpret_cast<uintptr_t>(x) & 15u) == 0; };
+    const FlashPlan x3_plan = flash_plan(int64_t(B) * H, S_q, S_kv, D, kTileUsX3);
+    const bool raw_q = prepared && !in.freqs && mode == kAttnF32X3 && a16(in.q) &&
+                       ld_q % 4 == 0 && (!in.q_norm_w || a16(in.q_norm_w)) &&
+                       x3_plan.waves == 8 && x3_plan.splits == 1;
+
     // Q rows, and K rows unless prepared, in one launch.
     const RowProblem pq =
         qk_rows(in.q, in.q_norm_w, in.freqs, qn, B, S_q, H, D, in.eps, mode, in.ld_q);
-    if (!fused && !(prepared ? launch_rows(pq, st) : launch_rows_pair(pk, pq, st)))
+    if (!fused && !raw_q && !(prepared ? launch_rows(pq, st) : launch_rows_pair(pk, pq, st)))
         return false;
 
     const bool bcast = in.Bk == 1 && B > 1;
@@ -225,6 +240,13 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     p.D = D;
     p.scale = float(1.0 / std::sqrt(double(D)));
     p.causal = false;
+    if (raw_q) {
+        p.q = nullptr;
+        p.rq.x = in.q;
+        p.rq.s = bshd(S_q, H, D, false, in.ld_q);
+        p.rq.w = in.q_norm_w;
+        p.rq.eps = in.eps;
+    }
     if (in.out_t) {
         p.o = nullptr;
         p.os = Strides{0, 0, 0};

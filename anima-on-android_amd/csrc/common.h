@@ -35,6 +35,19 @@ struct TermOut {
     int64_t tb = 0, th = 0, ts = 0, lo = 0;
 };
 
+// Query rows handed to a flash kernel unprepared: f32 x, [B, S_q, H, 128]
+// rows through strides s, 16-byte aligned.  The kernel applies the per-head
+// RMSNorm (optional weight w), the rotate-half RoPE of table freqs
+// ([S_q, 64, 2, 2], optional) and its own operand conversion, bit-identical to
+// the row prologue followed by the kernel.  x == nullptr: q is prepared.
+struct RawQ {
+    const float *x = nullptr;
+    Strides s{0, 0, 0};
+    const float *w = nullptr;
+    const float *freqs = nullptr;
+    float eps = 1e-6f;
+};
+
 // Everything the attention kernels need; pointers are device pointers.
 struct FlashProblem {
     const void *q, *k, *v;  // f32 or bf16 (see kernel)
@@ -44,6 +57,7 @@ struct FlashProblem {
     float scale;       // softmax scale applied to q.k
     bool causal;       // mask key j > query i (top-left aligned, like anima_rt)
     TermOut ot;        // bf16 term output in place of o
+    RawQ rq;           // f32x3 kernel only: q given as raw projection rows
 };
 bool term_out_ok(const TermOut &t);  // alignment of a set term output
 

@@ -32,6 +32,7 @@
 //     is about 2.4x its VALU work, and the second wave of each SIMD fills the
 //     remaining issue gaps.
 #include "flash_tile.h"
+#include "rowmath.h"
 
 #include <cmath>
 
@@ -54,7 +55,92 @@ struct X3Args {
     int dma32;  // K/V^T tile rows fit 32-bit byte offsets from the tile start
     FlashSplitArgs split;  // n == 1: write O; n > 1: write this split's partial
     TermOut ot;            // n == 1 and ot.t set: O as bf16 terms
+    // Raw query rows (RawQ) in place of q's term rows when qx is set.
+    const float *qx, *qw, *qf;
+    int64_t rqb, rqh, rqs;
+    float eps;
 };
+
+// Both halves of a query row at once: lo = v of lane l % 32, hi = v of lane
+// 32 + l % 32 (one v_permlane32_swap).
+__device__ __forceinline__ void row_halves(float v, float &lo, float &hi)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+}
+
+// The Q terms of one query row prepared from its raw f32 projection row, as
+// the row prologue (prologue.hip) computes them for anima_rt's rmsnorm and
+// rope kernels (anima_rt/include/cpu/rmsnorm_kernel.h:11-31,
+// rope_kernel.h:65-97): y = x * inv_rms(sum x^2) [* w], then, with a table,
+// for pair p
+//     out[p] = c00 y[p] + c01 y[p+64],  out[p+64] = c10 y[p] + c11 y[p+64]
+// (two products and one add, no contraction), split into hi = bf16(out) and
+// lo = bf16(out - hi).  Lane half h owns d = 64h .. 64h+63 (the Q fragment
+// layout).  The sum of squares keeps the reference's index order across the
+// two halves: half 0 adds d < 64 from zero, half 1 continues from half 0's
+// partial.  Every lane takes part in the exchanges; lanes whose row is not
+// `valid` (past S_q) read nothing and end with zero terms.
+__device__ __forceinline__ void q_terms_from_raw(const float *xrow, const float *w,
+                                                 const float *fq, float eps, bool valid,
+                                                 int half, bf16x8 (&qh)[8], bf16x8 (&ql)[8])
+{
+#pragma clang fp contract(off)
+    f32x4 x[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        x[j] = valid ? *reinterpret_cast<const f32x4 *>(xrow + 64 * half + 4 * j)
+                     : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            ss = ss + x[j][e] * x[j][e];
+    float ss0, unused;
+    row_halves(ss, ss0, unused);
+    float ss1 = ss0;  // half 1: half 0's partial, then its own squares in order
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            ss1 = ss1 + x[j][e] * x[j][e];
+    float total;
+    row_halves(ss1, unused, total);
+    const float inv = inv_rms(total, kD, eps);
+    const f32x4 *wv = w ? reinterpret_cast<const f32x4 *>(w + 64 * half) : nullptr;
+    const float *fh = fq ? fq + 2 * half : nullptr;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        unsigned hw[4], lw[4];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+            unsigned short hb[2], lb[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int i = 8 * t + 2 * e2 + u;
+                float y = x[i >> 2][i & 3] * inv;
+                if (wv)
+                    y = y * wv[i >> 2][i & 3];
+                float out = y;
+                if (fh) {
+                    float ya, yb;
+                    row_halves(y, ya, yb);
+                    const float2 c = *reinterpret_cast<const float2 *>(fh + 4 * i);
+                    out = c.x * ya + c.y * yb;
+                }
+                hb[u] = f32_to_bf16_rne(out);
+                lb[u] = bf16_lo_term(out, hb[u]);
+            }
+            hw[e2] = valid ? unsigned(hb[0]) | (unsigned(hb[1]) << 16) : 0u;
+            lw[e2] = valid ? unsigned(lb[0]) | (unsigned(lb[1]) << 16) : 0u;
+        }
+        qh[t] = __builtin_bit_cast(bf16x8, uint4{hw[0], hw[1], hw[2], hw[3]});
+        ql[t] = __builtin_bit_cast(bf16x8, uint4{lw[0], lw[1], lw[2], lw[3]});
+    }
+}
 
 template <int NW>
 __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
@@ -88,23 +174,6 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
     const u16 *qp = a.q + b * a.qb + h * a.qh;
     const u16 *kp = a.k + b * a.kb + h * a.kh;
     const u16 *vp = a.vt + b * a.vb + h * a.vh;
-
-    // Q terms: hi Q[qrow][64*half + 8t .. +7], lo 128 elements further.
-    bf16x8 qh[8], ql[8];
-    if (qrow < a.S_q) {
-        const bf16x8 *src = reinterpret_cast<const bf16x8 *>(qp + qrow * a.qs + 64 * half);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            qh[t] = src[t];
-            ql[t] = src[kD / 8 + t];
-        }
-    } else {
-#pragma unroll
-        for (int t = 0; t < 8; ++t)
-            qh[t] = ql[t] = bf16x8{};
-    }
-    // Retire the Q loads before the loop, whose vmcnt waits count only copies.
-    __builtin_amdgcn_s_waitcnt(kVmcnt0);
 
     int kv_end = a.S_kv;
     if (a.causal)
@@ -186,9 +255,38 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_x3_d128(X3Args a)
     float l = 0.0f, l2 = 0.0f;  // row sums of the hi and lo P terms
     const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
 
+    // Q terms: hi Q[qrow][64*half + 8t .. +7], lo 128 elements further.
+    bf16x8 qh[8], ql[8];
+    if (!a.qx) {
+        if (qrow < a.S_q) {
+            const bf16x8 *src = reinterpret_cast<const bf16x8 *>(qp + qrow * a.qs + 64 * half);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                qh[t] = src[t];
+                ql[t] = src[kD / 8 + t];
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                qh[t] = ql[t] = bf16x8{};
+        }
+        // Retire the Q loads before the loop, whose vmcnt waits count only
+        // copies.
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    }
     if (ntiles > 0) {
         dma_k(0, 0);
         dma_v(0, 0);
+    }
+    // Raw query rows are prepared while the first tile's copies are in
+    // flight (issued first, so the two latencies overlap).  Prepared rows
+    // load first: copies first cost a small 4-wave grid (256 x 512 keys,
+    // B = 2, H = 16) 3 %.
+    if (a.qx) {
+        const int r = min(qrow, a.S_q - 1);
+        q_terms_from_raw(a.qx + b * a.rqb + h * a.rqh + int64_t(r) * a.rqs, a.qw,
+                         a.qf ? a.qf + int64_t(r) * 4 * kD / 2 : nullptr, a.eps, qrow < a.S_q,
+                         half, qh, ql);
     }
     wait_vmcnt<0>();
     ring_barrier();
@@ -460,7 +558,8 @@ bool launch_flash_x3(const FlashProblem &p, hipStream_t st, void *part, size_t p
                 return false;
         return true;
     };
-    if (!rows_fit(p.qs) || !rows_fit(p.ks))
+    const bool raw_q = p.rq.x != nullptr;  // q's term rows unused
+    if ((!raw_q && !rows_fit(p.qs)) || !rows_fit(p.ks))
         return fail("flash_x3: q/k strides must leave 2*D = 256 elements per row (hi | lo terms)");
     // Each (batch, head) of the term V^T holds 2*D rows of Sp keys.
     for (const int64_t v : {p.vs.b, p.vs.h})
@@ -468,9 +567,15 @@ bool launch_flash_x3(const FlashProblem &p, hipStream_t st, void *part, size_t p
             return fail("flash_x3: V^T batch/head strides must leave 2*D rows of the padded key "
                         "count per head");
     const auto s8 = [](const Strides &x) { return x.b % 8 == 0 && x.h % 8 == 0 && x.s % 8 == 0; };
-    if (!aligned(p.q, 16) || !aligned(p.k, 16) || !aligned(p.v, 16) || !aligned(p.o, 16) ||
-        !s8(p.qs) || !s8(p.ks) || !s8(p.vs) || p.os.b % 4 || p.os.h % 4 || p.os.s % 4)
+    if ((!raw_q && (!aligned(p.q, 16) || !s8(p.qs))) || !aligned(p.k, 16) || !aligned(p.v, 16) ||
+        !aligned(p.o, 16) || !s8(p.ks) || !s8(p.vs) || p.os.b % 4 || p.os.h % 4 || p.os.s % 4)
         return fail("flash_x3: operands must be 16-byte aligned with 16-byte row strides");
+    if (raw_q) {
+        const Strides &x = p.rq.s;
+        if (!aligned(p.rq.x, 16) || x.b % 4 || x.h % 4 || x.s % 4 ||
+            (p.rq.w && !aligned(p.rq.w, 16)) || (p.rq.freqs && !aligned(p.rq.freqs, 16)))
+            return fail("flash_x3: raw query rows must be 16-byte aligned with 16-byte strides");
+    }
     if (p.ot.t && !term_out_ok(p.ot))
         return fail("flash_x3: term output must be 16-byte aligned with strides of 8 elements");
     X3Args a;
@@ -492,6 +597,11 @@ bool launch_flash_x3(const FlashProblem &p, hipStream_t st, void *part, size_t p
     // r*ks, V^T rows r < 256 at r*Sp, plus one row of 512 bytes.
     a.dma32 = (int64_t(kBN) * p.ks.s * 2 + 512 < (int64_t(1) << 31)) &&
               (int64_t(2 * kD) * sp * 2 + 512 < (int64_t(1) << 31));
+    a.qx = p.rq.x;
+    a.qw = p.rq.w;
+    a.qf = p.rq.freqs;
+    a.rqb = p.rq.s.b; a.rqh = p.rq.s.h; a.rqs = p.rq.s.s;
+    a.eps = p.rq.eps;
     const FlashPlan pl = flash_plan(BH, p.S_q, p.S_kv, p.D, kTileUsX3);
     a.split = flash_split_args(pl, BH, p.S_q, part, part_bytes);
     if (!(pl.waves == 4 ? launch_d128<4>(a, BH, st) : launch_d128<8>(a, BH, st)))

@@ -22,6 +22,7 @@
 // sqrt are rounded correctly by evaluating them in f64 and rounding once.
 // Rows are staged through LDS so global loads and stores stay coalesced.
 #include "common.h"
+#include "rowmath.h"
 
 #pragma clang fp contract(off)
 
@@ -40,19 +41,6 @@ struct RowArgs {
     float eps;
     int norm, out_bf16;
 };
-
-__device__ __forceinline__ unsigned short f32_to_bf16_rne(float f)
-{
-    unsigned int u = __float_as_uint(f);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (unsigned short)(u >> 16);
-}
-
-// Second bf16 term of f: bf16(f - hi), hi = bf16(f) (f - hi is exact in f32).
-__device__ __forceinline__ unsigned short bf16_lo_term(float f, unsigned short hi)
-{
-    return f32_to_bf16_rne(f - __uint_as_float(unsigned(hi) << 16));
-}
 
 // Four consecutive outputs as bf16 hi terms at ob and, when lo_off != 0, lo
 // terms at ob + lo_off.
@@ -107,15 +95,6 @@ __device__ __forceinline__ float out_elem(const RowArgs &a, const float *row, fl
     const float yb = norm_elem(a, row, inv, p + half);
     const float *fq = a.freqs + int64_t(s) * a.D * 2 + 4 * p + (lower ? 0 : 2);
     return fq[0] * ya + fq[1] * yb;
-}
-
-__device__ __forceinline__ float inv_rms(float ss, int D, float eps)
-{
-    // f32 divide and sqrt, each correctly rounded: evaluated in f64 and
-    // rounded once (exact for f32 operands).
-    const float ms = (float)((double)ss / (double)D);
-    const float root = (float)sqrt((double)(ms + eps));
-    return (float)(1.0 / (double)root);
 }
 
 // Any D: rows staged in LDS with an odd pitch, per-row offsets computed once.

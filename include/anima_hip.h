@@ -17,7 +17,7 @@
  *     anima_hip_ctx_kv_create) copy to the GPU, run, copy back and return
  *     when the output is complete.  They are serialised by a library mutex.
  *     Copies of 4 MiB and more pass through pinned staging buffers, with
- *     the host memcpy split over the caller and up to 3 library threads.
+ *     the host memcpy split over the caller and up to 5 library threads.
  *   - "_dev" entry points take device pointers and a hipStream_t (passed as
  *     void*; NULL = HIP's default stream) and are asynchronous: they only
  *     enqueue work on that stream.
@@ -172,6 +172,21 @@ bool anima_hip_flash_x3_dev(const uint16_t *q, const uint16_t *k, const uint16_t
                             const int64_t *q_strides, const int64_t *k_strides,
                             const int64_t *vt_strides, const int64_t *o_strides,
                             float scale, bool is_causal, void *stream);
+
+/* anima_hip_flash_x3_dev with q given as raw f32 projection rows ([B,S_q,H,D]
+ * through q_strides, NULL = contiguous; 16-byte aligned rows): the kernel
+ * applies the per-head RMSNorm (q_norm_w may be NULL), the RoPE of freqs
+ * ([S_q, D/2, 2, 2] or NULL) and the hi/lo term split itself, bit-identical to
+ * anima_hip_qk_prologue_dev (flags 1 | 4) followed by anima_hip_flash_x3_dev.
+ * NumpyAttention.forward's q path (anima_rt/scripts/numpy_dit.py:285-291)
+ * and its attention in one launch; the cross-attention entries use it on
+ * unsplit grids. */
+bool anima_hip_flash_x3_rawq_dev(const float *q, const float *q_norm_w, const float *freqs,
+                                 float eps, const uint16_t *k, const uint16_t *vt, float *o,
+                                 int B, int H, int S_q, int S_kv, int D,
+                                 const int64_t *q_strides, const int64_t *k_strides,
+                                 const int64_t *vt_strides, const int64_t *o_strides,
+                                 float scale, bool is_causal, void *stream);
 
 /* Pack f32 V into the term V^T layout of anima_hip_flash_x3_dev: per (batch,
  * head) the [D][anima_hip_vt_padded_len(S_kv)] hi matrix of

@@ -1,0 +1,132 @@
+"""The f32x3 flash kernel given raw query rows (anima_hip_flash_x3_rawq_dev:
+RMSNorm, RoPE and the hi/lo term split of q inside the kernel) against the
+two-pass form it replaces (anima_hip_qk_prologue_dev with flags 1 | 4, then
+anima_hip_flash_x3_dev), bit for bit: dense and fused-projection layouts,
+with and without norm weights and RoPE, ragged query and key tiles, causal
+masking, cross-attention shapes, the 4-wave grid of small problems, and
+NaN / infinity in the raw rows.  The prologue is itself pinned bit for bit to
+the reference's RMSNorm and RoPE (tests/test_gpu_flash.py), and the composed
+attention to the oracle (tests/test_gpu_x3.py), so equality here carries both.
+
+Also: the k/v-only form of anima_hip_qkv_prologue_dev (q = qo = NULL) against
+the full one, and anima_hip_attention_dev in f32x3 mode, which now takes the
+raw-q kernel on unsplit grids, against prologue + flash_x3_dev."""
+import ctypes as ct
+import math
+
+import numpy as np
+import pytest
+
+from anima_hip import _lib, rt
+from anima_hip.rope import generate_rope_freqs
+from devmem import DevBuf
+
+pytestmark = pytest.mark.gpu
+D = 128
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    rt.init()
+
+
+def _ptr(b):
+    return b.addr if b is not None else None
+
+
+def _bits(x):
+    return np.ascontiguousarray(x).view(np.uint32)
+
+
+CASES = [  # B, S_q, S_kv, H, grid (None: no RoPE), fused projection layout, weights, causal
+    (2, 4096, 4096, 16, (64, 64), False, True, False),
+    (2, 77, 77, 3, (7, 11), True, True, False),
+    (1, 1000, 1000, 16, None, False, False, False),
+    (3, 64, 64, 2, (8, 8), False, True, True),
+    (2, 300, 512, 16, None, False, True, False),
+    (1, 520, 100, 4, None, True, False, True),
+]
+
+
+@pytest.mark.parametrize("B,S_q,S_kv,H,grid,fused,weights,causal", CASES)
+def test_rawq_matches_prologue_then_flash(B, S_q, S_kv, H, grid, fused, weights, causal):
+    lib = _lib.load()
+    rng = np.random.default_rng(B * 7919 + S_q * 31 + S_kv + H)
+    print(f"rawq case B={B} S_q={S_q} S_kv={S_kv} H={H} grid={grid} fused={fused} "
+          f"weights={weights} causal={causal}", flush=True)
+    ld = 3 * H * D if fused else H * D
+    qraw = rng.standard_normal((B, S_q, ld), dtype=np.float32)
+    qraw[0, S_q // 3, :D] *= 40.0  # one large row: a wide range inside the sum of squares
+    qb = DevBuf.of(qraw)
+    k = DevBuf.of(rng.standard_normal((B, S_kv, H, D), dtype=np.float32))
+    v = DevBuf.of(rng.standard_normal((B, S_kv, H, D), dtype=np.float32))
+    wq = DevBuf.of(rng.uniform(0.5, 1.5, D).astype(np.float32)) if weights else None
+    wk = DevBuf.of(rng.uniform(0.5, 1.5, D).astype(np.float32)) if weights else None
+    fr = DevBuf.of(generate_rope_freqs(*grid)) if grid else None
+    eps = ct.c_float(1e-6)
+    scale = ct.c_float(1.0 / math.sqrt(D))
+    sp = lib.anima_hip_vt_padded_len(S_kv)
+    row = 2 * D
+    qx_s = _lib.strides([S_q * ld, D, ld])
+    q_terms = DevBuf(B * S_q * H * row * 2)
+    k_terms = DevBuf(B * S_kv * H * row * 2)
+    vt = DevBuf(B * H * row * sp * 2)
+    qts = _lib.strides([S_q * H * row, row, H * row])
+    kts = _lib.strides([S_kv * H * row, row, H * row])
+    kvs = _lib.strides([S_kv * H * D, D, H * D])
+    os_ = _lib.strides([S_q * H * D, D, H * D])
+    _lib.check(lib.anima_hip_qk_prologue_dev(qb.addr, q_terms.addr, _ptr(wq), _ptr(fr), B, S_q,
+                                             H, D, qx_s, qts, eps, 1 | 4, None), "q prologue")
+    _lib.check(lib.anima_hip_qk_prologue_dev(k.addr, k_terms.addr, _ptr(wk),
+                                             _ptr(fr) if S_q == S_kv else None, B, S_kv, H, D,
+                                             kvs, kts, eps, 1 | 4, None), "k prologue")
+    _lib.check(lib.anima_hip_pack_vt_terms_dev(v.addr, vt.addr, B, H, S_kv, D, kvs, None, None),
+               "pack_vt_terms_dev")
+    o_ref, o_raw = DevBuf(B * S_q * H * D * 4), DevBuf(B * S_q * H * D * 4)
+    _lib.check(lib.anima_hip_flash_x3_dev(q_terms.addr, k_terms.addr, vt.addr, o_ref.addr, B, H,
+                                          S_q, S_kv, D, qts, kts, None, os_, scale, causal,
+                                          None), "flash_x3_dev")
+    _lib.check(lib.anima_hip_flash_x3_rawq_dev(qb.addr, _ptr(wq), _ptr(fr), eps, k_terms.addr,
+                                               vt.addr, o_raw.addr, B, H, S_q, S_kv, D, qx_s,
+                                               kts, None, os_, scale, causal, None),
+               "flash_x3_rawq_dev")
+    ref = o_ref.get((B, S_q, H, D))
+    out = o_raw.get((B, S_q, H, D))
+    assert np.isfinite(out).all()
+    assert np.array_equal(_bits(out), _bits(ref))
+
+
+def test_rawq_nan_and_inf_rows_match():
+    """A NaN and an infinity in two raw rows: the kernel's preparation
+    propagates them exactly as the row prologue does."""
+    lib = _lib.load()
+    rng = np.random.default_rng(404)
+    B, S, H = 1, 256, 4
+    qraw = rng.standard_normal((B, S, H, D), dtype=np.float32)
+    qraw[0, 5, 1, 70] = np.nan
+    qraw[0, 9, 2, 3] = np.inf
+    qb = DevBuf.of(qraw)
+    kv = rng.standard_normal((2, B, S, H, D), dtype=np.float32)
+    fr = DevBuf.of(generate_rope_freqs(16, 16))
+    eps = ct.c_float(1e-6)
+    scale = ct.c_float(1.0 / math.sqrt(D))
+    sp = lib.anima_hip_vt_padded_len(S)
+    xs = _lib.strides([S * H * D, D, H * D])
+    ts = _lib.strides([S * H * 2 * D, 2 * D, H * 2 * D])
+    qt, kt = DevBuf(B * S * H * 2 * D * 2), DevBuf(B * S * H * 2 * D * 2)
+    k, v = DevBuf.of(kv[0]), DevBuf.of(kv[1])
+    vt = DevBuf(B * H * 2 * D * sp * 2)
+    for x, o in ((qb, qt), (k, kt)):
+        _lib.check(lib.anima_hip_qk_prologue_dev(x.addr, o.addr, None, fr.addr, B, S, H, D, xs,
+                                                 ts, eps, 1 | 4, None), "prologue")
+    _lib.check(lib.anima_hip_pack_vt_terms_dev(v.addr, vt.addr, B, H, S, D, xs, None, None),
+               "pack")
+    o_ref, o_raw = DevBuf(B * S * H * D * 4), DevBuf(B * S * H * D * 4)
+    _lib.check(lib.anima_hip_flash_x3_dev(qt.addr, kt.addr, vt.addr, o_ref.addr, B, H, S, S, D,
+                                          ts, ts, None, xs, scale, False, None), "flash")
+    _lib.check(lib.anima_hip_flash_x3_rawq_dev(qb.addr, None, fr.addr, eps, kt.addr, vt.addr,
+                                               o_raw.addr, B, H, S, S, D, xs, ts, None, xs,
+                                               scale, False, None), "flash rawq")
+    ref, out = o_ref.get((B, S, H, D)), o_raw.get((B, S, H, D))
+    assert np.isfinite(ref[0, 6]).all()
+    assert np.array_equal(_bits(out), _bits(ref))
