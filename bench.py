@@ -532,7 +532,8 @@ def dropin_call(c, host, B, H, S, D, iters=3):
             "device_call_ms": round(tot[i], 3), "kernel_only_ms": round(kern[i], 3),
             "pcie_bytes": moved, "bytes_per_call_time_GBps": round(moved / (tot[i] * 1e-3) / 1e9, 1),
             "note": "best of %d calls; kernel_only_ms is the time between the last upload and the "
-                    "first download, i.e. the kernels not hidden behind copies" % iters}
+                    "start of the last head group's downloads, i.e. the kernels not hidden behind "
+                    "copies" % iters}
 
 
 def normalized_qk(c, q, k, freqs, ones):
