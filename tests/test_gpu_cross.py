@@ -145,3 +145,34 @@ def test_rectangular_96x64_grid_6144_tokens_all_heads(mode):
         cache.close()
     fullsize.check_all_slices(out, fullsize.cross_ref(6144, 5007, 5006), mode,
                               "cross-attention 6144x512 (cached context)")
+
+
+@pytest.mark.parametrize("mode", [rt.F32X3, rt.F32])
+def test_broadcast_context_4096_tokens_equals_repeated_context(mode):
+    """One context (Bc = 1) serving both CFG entries at 4096 query tokens, the
+    grid on which f32x3 prepares its raw query rows inside the flash kernel,
+    with a norm weight on q: equal bit for bit to the same context repeated
+    (Bc = 2), and two slices within the f32 tolerance of the oracle."""
+    import fullsize
+    ctx, wk, wv = fullsize.context_case(6006, Bc=1)
+    rng = np.random.default_rng(6007)
+    qw = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    kw = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    q = fullsize.cross_q(4096, 6008)
+    outs = []
+    for c in (ctx, np.concatenate([ctx, ctx])):
+        cache = rt.ContextKV(c, wk, wv, kw, heads=16, head_dim=128, mode=mode)
+        try:
+            print(f"cross 4096x512 Bc={c.shape[0]} mode={mode}", flush=True)
+            outs.append(cache.attend(q, qw))
+        finally:
+            cache.close()
+    np.testing.assert_array_equal(outs[0], outs[1])
+    k = oracle.gemm_bf16(ctx[0], wk).reshape(1, 512, 16, 128)
+    v = oracle.gemm_bf16(ctx[0], wv).reshape(1, 512, 16, 128)
+    for b, h in ((0, 2), (1, 13)):
+        ref = oracle.attention_dataflow(q[b:b + 1, :, h:h + 1], k[:, :, h:h + 1],
+                                        v[:, :, h:h + 1], qw, kw, None)[0, :, 0]
+        err = float(np.abs(outs[0][b, :, h] - ref).max())
+        print(f"cross 4096x512 broadcast mode={mode} b={b} h={h}: max-abs {err:.3e}", flush=True)
+        assert err <= 1e-4
