@@ -112,3 +112,26 @@ def test_attention_two_batch_groups_equal_the_single_batch_calls(mode):
             assert err <= 2e-2 * float(np.abs(ref).max())
         else:
             assert err <= 1e-4
+
+
+def test_attention_four_batch_groups_equal_the_single_batch_calls():
+    """anima_hip_attention at B=4, 4096 tokens, H=16 (RMSNorm + 3D RoPE) runs
+    as four batch groups; each must equal a B=1 call bit for bit (f32x3)."""
+    from anima_hip.rope import generate_rope_freqs
+    B, S, H, D = 4, 4096, 16, 128
+    mode = rt.F32X3
+    rng = np.random.default_rng(256)
+    q, k, v = (rng.standard_normal((B, S, H, D), dtype=np.float32) for _ in range(3))
+    wq = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    wk = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    f = generate_rope_freqs(64, 64)
+    print(f"pipeline attention case B={B} S={S} mode={mode}", flush=True)
+    full = rt.attention(q, k, v, wq, wk, f, mode=mode)
+    for b in range(B):
+        one = rt.attention(q[b:b + 1], k[b:b + 1], v[b:b + 1], wq, wk, f, mode=mode)
+        np.testing.assert_array_equal(full[b:b + 1], one)
+    ref = oracle.attention_dataflow(q[3:4, :, 9:10], k[3:4, :, 9:10], v[3:4, :, 9:10], wq, wk,
+                                    f)[0, :, 0]
+    err = float(np.abs(full[3, :, 9] - ref).max())
+    print(f"pipeline attention four groups b=3 h=9: max-abs {err:.3e}", flush=True)
+    assert err <= 1e-4
