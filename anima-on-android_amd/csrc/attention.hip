@@ -208,11 +208,15 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     // out ahead of Q), and split grids would repeat it per split.
     // Self-attention keeps it too, where the RoPE table's reads at each
     // workgroup's start cost more than the pass.
+    // The f32 kernel, which reads Q as f32 rows anyway, does the same (RMSNorm
+    // only: its rows carry no terms; 4096 x 512: 307.5 -> 286.5 us).
     const auto a16 = [](const void *x) { return (reinterpret_cast<uintptr_t>(x) & 15u) == 0; };
-    const FlashPlan x3_plan = flash_plan(int64_t(B) * H, S_q, S_kv, D, kTileUsX3);
-    const bool raw_q = prepared && !in.freqs && mode == kAttnF32X3 && a16(in.q) &&
-                       ld_q % 4 == 0 && (!in.q_norm_w || a16(in.q_norm_w)) &&
-                       x3_plan.waves == 8 && x3_plan.splits == 1;
+    const FlashPlan raw_plan = flash_plan(int64_t(B) * H, S_q, S_kv, D,
+                                          mode == kAttnF32X3 ? kTileUsX3 : kTileUsF32);
+    const bool raw_q = prepared && !in.freqs && (mode == kAttnF32X3 || mode == kAttnF32) &&
+                       D == 128 && a16(in.q) && ld_q % 4 == 0 &&
+                       (!in.q_norm_w || a16(in.q_norm_w)) && raw_plan.waves == 8 &&
+                       raw_plan.splits == 1;
 
     // Q rows, and K rows unless prepared, in one launch.
     const RowProblem pq =

@@ -25,6 +25,7 @@
 // and K alike, so the dot products are unchanged.
 #include "common.h"
 #include "flash_tile.h"
+#include "rowmath.h"
 
 #include <cmath>
 
@@ -51,7 +52,48 @@ struct F32Args {
     int causal;
     FlashSplitArgs split;  // n == 1: write O; n > 1: write this split's partial
     TermOut ot;            // n == 1 and ot.t set: O as bf16 terms
+    // q holds raw projection rows (RawQ, no RoPE): the kernel applies the
+    // per-head RMSNorm (weight qw, optional) itself.
+    int raw_q;
+    const float *qw;
+    float eps;
 };
+
+// RMSNorm of one query row held as the f32 kernel's Q fragment (lane half h
+// owns d = 64h .. 64h+63), as the row prologue (prologue.hip) computes it for
+// anima_rt's rmsnorm_kernel (anima_rt/include/cpu/rmsnorm_kernel.h:11-31):
+// y = x * inv_rms(sum x^2) [* w], no contraction.  The sum of squares keeps
+// the reference's index order across the halves: half 0 adds d < 64 from
+// zero, half 1 continues from half 0's partial (one v_permlane32_swap each
+// way).  Every lane takes part; a zero row stays zero.
+__device__ __forceinline__ void rms_norm_fragment(float (&x)[64], const float *w, float eps,
+                                                  int half)
+{
+#pragma clang fp contract(off)
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i)
+        ss = ss + x[i] * x[i];
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false,
+                                                    false);
+    float ss1 = __uint_as_float(a[0]);  // half 0's partial
+#pragma unroll
+    for (int i = 0; i < 64; ++i)
+        ss1 = ss1 + x[i] * x[i];
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss1), __float_as_uint(ss1),
+                                                    false, false);
+    const float inv = inv_rms(__uint_as_float(b[1]), kD, eps);  // half 1's total
+    const f32x4 *wv = w ? reinterpret_cast<const f32x4 *>(w + 64 * half) : nullptr;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const f32x4 wj = wv ? wv[j] : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float y = x[4 * j + e] * inv;
+            x[4 * j + e] = wv ? y * wj[e] : y;
+        }
+    }
+}
 
 __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c)
 {
@@ -121,6 +163,8 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_f32_d128(F32Args a)
         for (int i = 0; i < 64; ++i)
             qf[i] = 0.0f;
     }
+    if (a.raw_q)
+        rms_norm_fragment(qf, a.qw, a.eps, half);
     // Retire the Q loads here.  Otherwise the compiler still counts them as
     // outstanding inside the tile loop and waits for vmcnt(0) before the
     // first MFMAs, which also waits for the next tile's prefetch.
@@ -415,13 +459,27 @@ bool launch_flash_f32(const FlashProblem &p, hipStream_t st, void *part, size_t 
     const int64_t BH = int64_t(p.B) * p.H;
     if (BH == 0 || p.S_q == 0)
         return true;
-    if (p.ot.t && !(flash_f32_fast_path(p) && term_out_ok(p.ot)))
+    // Raw query rows (RMSNorm, no RoPE) are read like prepared f32 rows, by
+    // the D == 128 kernel only.
+    const bool raw_q = p.rq.x != nullptr;
+    FlashProblem f = p;
+    if (raw_q) {
+        f.q = p.rq.x;
+        f.qs = p.rq.s;
+        if (p.rq.freqs || !flash_f32_fast_path(f) || (p.rq.w && !aligned16(p.rq.w)))
+            return fail("flash_f32: raw query rows need D == 128, 16-byte aligned rows and "
+                        "strides, and no RoPE table");
+    }
+    if (f.ot.t && !(flash_f32_fast_path(f) && term_out_ok(f.ot)))
         return fail("flash_f32: term output needs D == 128, 16-byte aligned operands and an "
                     "16-byte aligned output with strides of 8 elements");
-    if (flash_f32_fast_path(p)) {
+    if (flash_f32_fast_path(f)) {
         F32Args a;
-        fill_common(a, p);
-        a.ot = p.ot;
+        fill_common(a, f);
+        a.ot = f.ot;
+        a.raw_q = raw_q ? 1 : 0;
+        a.qw = p.rq.w;
+        a.eps = p.rq.eps;
         const FlashPlan pl = flash_plan(BH, p.S_q, p.S_kv, p.D, kTileUsF32);
         a.split = flash_split_args(pl, BH, p.S_q, part, part_bytes);
         if (!(pl.waves == 4 ? launch_d128<4>(a, BH, st) : launch_d128<8>(a, BH, st)))

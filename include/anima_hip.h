@@ -173,6 +173,20 @@ bool anima_hip_flash_x3_dev(const uint16_t *q, const uint16_t *k, const uint16_t
                             const int64_t *vt_strides, const int64_t *o_strides,
                             float scale, bool is_causal, void *stream);
 
+/* anima_hip_flash_f32_dev with q given as raw f32 projection rows ([B,S_q,H,D]
+ * through q_strides, NULL = contiguous; D == 128, 16-byte aligned rows): the
+ * kernel applies the per-head RMSNorm (q_norm_w may be NULL) itself,
+ * bit-identical to anima_hip_qk_prologue_dev (flags 1) followed by
+ * anima_hip_flash_f32_dev.  No RoPE.  NumpyAttention.forward's cross-attention
+ * q path (anima_rt/scripts/numpy_dit.py:285-286) and its attention in one
+ * launch; the cross-attention entries use it on unsplit 8-wave grids. */
+bool anima_hip_flash_f32_rawq_dev(const float *q, const float *q_norm_w, float eps,
+                                  const float *k, const float *v, float *o, int B, int H,
+                                  int S_q, int S_kv, int D, const int64_t *q_strides,
+                                  const int64_t *k_strides, const int64_t *v_strides,
+                                  const int64_t *o_strides, float scale, bool is_causal,
+                                  void *stream);
+
 /* anima_hip_flash_x3_dev with q given as raw f32 projection rows ([B,S_q,H,D]
  * through q_strides, NULL = contiguous; 16-byte aligned rows): the kernel
  * applies the per-head RMSNorm (q_norm_w may be NULL), the RoPE of freqs

@@ -1,16 +1,20 @@
-"""The f32x3 flash kernel given raw query rows (anima_hip_flash_x3_rawq_dev:
-RMSNorm, RoPE and the hi/lo term split of q inside the kernel) against the
-two-pass form it replaces (anima_hip_qk_prologue_dev with flags 1 | 4, then
-anima_hip_flash_x3_dev), bit for bit: dense and fused-projection layouts,
-with and without norm weights and RoPE, ragged query and key tiles, causal
-masking, cross-attention shapes, the 4-wave grid of small problems, and
-NaN / infinity in the raw rows.  The prologue is itself pinned bit for bit to
-the reference's RMSNorm and RoPE (tests/test_gpu_flash.py), and the composed
-attention to the oracle (tests/test_gpu_x3.py), so equality here carries both.
+"""The flash kernels given raw query rows against the two-pass form they
+replace, bit for bit:
 
-Also: the k/v-only form of anima_hip_qkv_prologue_dev (q = qo = NULL) against
-the full one, and anima_hip_attention_dev in f32x3 mode, which now takes the
-raw-q kernel on unsplit grids, against prologue + flash_x3_dev."""
+- f32x3, anima_hip_flash_x3_rawq_dev (RMSNorm, RoPE and the hi/lo term split
+  of q inside the kernel) against anima_hip_qk_prologue_dev (flags 1 | 4) +
+  anima_hip_flash_x3_dev: dense and fused-projection layouts, with and
+  without norm weights and RoPE, ragged query and key tiles, causal masking,
+  cross-attention shapes, the 4-wave grid of small problems, NaN / infinity;
+- f32, anima_hip_flash_f32_rawq_dev (RMSNorm inside the kernel) against
+  anima_hip_qk_prologue_dev (flags 1) + anima_hip_flash_f32_dev, with NaN and
+  infinity rows.
+
+The prologue is itself pinned bit for bit to the reference's RMSNorm and RoPE
+(tests/test_gpu_flash.py), and the composed attention to the oracle
+(tests/test_gpu_x3.py, test_gpu_flash.py), so equality here carries both.  The
+cross-attention entries take these kernels on unsplit 8-wave grids;
+tests/test_gpu_cross.py holds them to the oracle at configs 2, 4 and 5."""
 import ctypes as ct
 import math
 
@@ -129,4 +133,51 @@ def test_rawq_nan_and_inf_rows_match():
                                                scale, False, None), "flash rawq")
     ref, out = o_ref.get((B, S, H, D)), o_raw.get((B, S, H, D))
     assert np.isfinite(ref[0, 6]).all()
+    assert np.array_equal(_bits(out), _bits(ref))
+
+
+F32_CASES = [  # B, S_q, S_kv, H, fused projection layout, weights, causal
+    (2, 4096, 512, 16, False, True, False),
+    (2, 77, 77, 3, True, True, False),
+    (1, 1000, 1000, 16, False, False, True),
+    (2, 256, 512, 16, True, False, False),
+]
+
+
+@pytest.mark.parametrize("B,S_q,S_kv,H,fused,weights,causal", F32_CASES)
+def test_f32_rawq_matches_prologue_then_flash(B, S_q, S_kv, H, fused, weights, causal):
+    """anima_hip_flash_f32_rawq_dev (q RMSNorm inside the f32 kernel) against
+    anima_hip_qk_prologue_dev (flags 1, f32 rows) + anima_hip_flash_f32_dev,
+    bit for bit; one row carries a NaN and one an infinity."""
+    lib = _lib.load()
+    rng = np.random.default_rng(B * 104729 + S_q * 17 + S_kv + H)
+    print(f"f32 rawq case B={B} S_q={S_q} S_kv={S_kv} H={H} fused={fused} weights={weights} "
+          f"causal={causal}", flush=True)
+    ld = 3 * H * D if fused else H * D
+    qraw = rng.standard_normal((B, S_q, ld), dtype=np.float32)
+    qraw[0, S_q // 3, :D] *= 40.0
+    qraw[B - 1, S_q // 2, 5] = np.nan
+    qraw[0, S_q - 1, D + 7 if H > 1 else 7] = np.inf
+    qb = DevBuf.of(qraw)
+    k = DevBuf.of(rng.standard_normal((B, S_kv, H, D), dtype=np.float32))
+    v = DevBuf.of(rng.standard_normal((B, S_kv, H, D), dtype=np.float32))
+    wq = DevBuf.of(rng.uniform(0.5, 1.5, D).astype(np.float32)) if weights else None
+    eps = ct.c_float(1e-6)
+    scale = ct.c_float(1.0 / math.sqrt(D))
+    qx_s = _lib.strides([S_q * ld, D, ld])
+    qs = _lib.strides([S_q * H * D, D, H * D])
+    kvs = _lib.strides([S_kv * H * D, D, H * D])
+    qn = DevBuf(B * S_q * H * D * 4)
+    _lib.check(lib.anima_hip_qk_prologue_dev(qb.addr, qn.addr, _ptr(wq), None, B, S_q, H, D,
+                                             qx_s, qs, eps, 1, None), "q prologue")
+    o_ref, o_raw = DevBuf(B * S_q * H * D * 4), DevBuf(B * S_q * H * D * 4)
+    _lib.check(lib.anima_hip_flash_f32_dev(qn.addr, k.addr, v.addr, o_ref.addr, B, H, S_q, S_kv,
+                                           D, qs, kvs, kvs, qs, scale, causal, None),
+               "flash_f32_dev")
+    _lib.check(lib.anima_hip_flash_f32_rawq_dev(qb.addr, _ptr(wq), eps, k.addr, v.addr,
+                                                o_raw.addr, B, H, S_q, S_kv, D, qx_s, kvs, kvs,
+                                                qs, scale, causal, None), "flash_f32_rawq_dev")
+    ref = o_ref.get((B, S_q, H, D))
+    out = o_raw.get((B, S_q, H, D))
+    assert np.isfinite(ref[0, 1]).all()
     assert np.array_equal(_bits(out), _bits(ref))
