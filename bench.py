@@ -85,6 +85,9 @@ def parse():
     ap.add_argument("--sampler-step", action="store_true",
                     help="only the whole-DiT Euler/CFG sampler step at 1024x1024, both modes; "
                          "prints one JSON line of its own")
+    ap.add_argument("--cross-step", action="store_true",
+                    help="only the cached-context cross-attention at 4096 x 512 (B=2, H=16), "
+                         "every mode; prints one JSON line of its own")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 256 MiB device copy (calibrates "
                          "FETCH_SIZE/WRITE_SIZE) then 2 steps of each variant; prints no JSON")
@@ -678,6 +681,18 @@ def main():
     lib = _lib.load()
     _lib.check(lib.anima_rt_init(), "anima_rt_init")
     c = Ctx(torch, lib, _lib)
+
+    if args.cross_step:
+        res = {}
+        for v in ("bf16", "f32x3", "f32"):
+            cache = context_cache(c, MODE[v], 2, 4000)
+            run, fl = cross_attention_timer(c, MODE[v], cache, 2, 4096, 77)
+            ms = c.time(run, 50, 3, prewarm_s=1.0)
+            cache.close()
+            res[v] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 2)}
+        print(json.dumps({"config": "cross_attention_4096x512_B2_cached", "results": res}),
+              flush=True)
+        return
 
     if args.sampler_step:
         n = args.sampler_latent
