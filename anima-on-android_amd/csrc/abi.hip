@@ -1812,20 +1812,63 @@ bool anima_hip_cross_attention(const float *q, const float *q_norm_w, const anim
         return true;
     if (!q || !out)
         return fail("cross_attention: null pointer");
+    if (kv->Bc != 1 && kv->Bc != B)
+        return fail("cross_attention: context batch must be 1 (broadcast) or equal to the query "
+                    "batch");
     const hipStream_t st = r.stream;
     begin_call(r);
-    const size_t scratch = attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D,
-                                                   AttnMode(kv->mode), true);
+    const AttnMode am = AttnMode(kv->mode);
+    // Batch groups, like the SDPA's head groups (sdpa_groups), when the
+    // copies are large and each group still fills the GPU: group g reads the
+    // cache's batch entries of its own queries (or the one shared entry).
+    int G = 1;
+    for (int c = Runtime::kMaxGroups; c > 1 && G == 1 && 2 * f32_bytes(nq) >= (size_t(64) << 20);
+         c /= 2) {
+        const FlashPlan part = flash_plan(int64_t(B / c) * kv->H, S_q, kv->S_kv, kv->D);
+        if (B % c == 0 && part.waves == 8 && part.splits == 1)
+            G = c;
+    }
+    const int Bg = B / G, Bkg = kv->Bc == 1 ? 1 : Bg;
+    const size_t scratch =
+        attention_scratch_bytes(Bg, S_q, Bkg, kv->S_kv, kv->H, kv->D, am, true);
     const float *qw = nullptr;
     if (!r.q.reserve(f32_bytes(nq), "workspace q") || !r.o.reserve(f32_bytes(nq), "workspace o") ||
-        !r.scratch.reserve(scratch, "workspace scratch") || !h2d(r.q.p, q, f32_bytes(nq), st) ||
-        !upload_optional(r.w0, q_norm_w, kv->D, "workspace q_norm", st, qw))
+        !r.scratch.reserve(scratch, "workspace scratch"))
         return false;
-    if (!anima_hip_cross_attention_dev(static_cast<const float *>(r.q.p), qw, kv,
-                                       static_cast<float *>(r.o.p), r.scratch.p, scratch, B, S_q,
-                                       eps, st) ||
-        !d2h(out, r.o.p, f32_bytes(nq), st))
+    DrainOnError drain{r};
+    if (!upload_optional(r.w0, q_norm_w, kv->D, "workspace q_norm", st, qw))
         return false;
+    const int64_t gq = nq / G;  // elements per group
+    float *const qd = static_cast<float *>(r.q.p), *const od = static_cast<float *>(r.o.p);
+    Pieces up, down;
+    for (int g = 0; g < G; ++g) {
+        up[g] = {{reinterpret_cast<char *>(qd + g * gq),
+                  reinterpret_cast<const char *>(q + g * gq), f32_bytes(gq)}};
+        down[g] = {{reinterpret_cast<char *>(out + g * gq),
+                    reinterpret_cast<const char *>(od + g * gq), f32_bytes(gq)}};
+    }
+    const size_t kb1 = prepared_k_bytes(1, kv->S_kv, kv->H, kv->D, am);
+    const size_t vb1 = prepared_v_bytes(1, kv->S_kv, kv->H, kv->D, am);
+    if (!run_groups(r, G, up, down, [&](int g, hipStream_t s) {
+            const size_t b0 = kv->Bc == 1 ? 0 : size_t(g) * Bg;
+            AttnInputs in;
+            in.q = qd + g * gq;
+            in.q_norm_w = qw;
+            in.k_prep = static_cast<const char *>(kv->k) + b0 * kb1;
+            in.v_prep = static_cast<const char *>(kv->v) + b0 * vb1;
+            in.out = od + g * gq;
+            in.B = Bg;
+            in.Bk = Bkg;
+            in.S_q = S_q;
+            in.S_kv = kv->S_kv;
+            in.H = kv->H;
+            in.D = kv->D;
+            in.eps = eps;
+            in.mode = am;
+            return run_attention(in, r.scratch.p, s);
+        }))
+        return false;
+    drain.done = true;
     return finish_call(r);
 }
 

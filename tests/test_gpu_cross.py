@@ -176,3 +176,29 @@ def test_broadcast_context_4096_tokens_equals_repeated_context(mode):
         err = float(np.abs(outs[0][b, :, h] - ref).max())
         print(f"cross 4096x512 broadcast mode={mode} b={b} h={h}: max-abs {err:.3e}", flush=True)
         assert err <= 1e-4
+
+
+@pytest.mark.parametrize("mode", [rt.F32X3, rt.BF16, rt.F32])
+def test_host_call_batch_groups_equal_per_batch_calls(mode):
+    """anima_hip_cross_attention (host pointers) at B = 2, 4096 query tokens
+    runs as two batch groups, each reading its own entry of a Bc = 2 context
+    cache while the other group's copies run; equal bit for bit to B = 1 calls
+    on caches of each context entry alone."""
+    import fullsize
+    ctx, wk, wv = fullsize.context_case(7007)
+    rng = np.random.default_rng(7008)
+    qw = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    kw = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    q = fullsize.cross_q(4096, 7009)
+    print(f"cross host groups mode={mode}", flush=True)
+    cache = rt.ContextKV(ctx, wk, wv, kw, heads=16, head_dim=128, mode=mode)
+    try:
+        full = cache.attend(q, qw)
+    finally:
+        cache.close()
+    for b in range(2):
+        one = rt.ContextKV(ctx[b:b + 1], wk, wv, kw, heads=16, head_dim=128, mode=mode)
+        try:
+            np.testing.assert_array_equal(full[b:b + 1], one.attend(q[b:b + 1], qw))
+        finally:
+            one.close()
