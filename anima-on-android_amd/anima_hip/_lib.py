@@ -84,6 +84,8 @@ SIGNATURES = {
     "anima_hip_cross_attention": (_B, [_P] * 4 + [_I] * 2 + [_F]),
     "anima_hip_cross_attention_scratch_bytes": (ct.c_size_t, [_P, _I, _I]),
     "anima_hip_cross_attention_dev": (_B, [_P] * 5 + [ct.c_size_t] + [_I] * 2 + [_F, _P]),
+    "anima_hip_cross_attention_terms_dev": (_B, [_P] * 4 + [ct.c_int64] * 2 + [_P, ct.c_size_t]
+                                            + [_I] * 2 + [_F, _P]),
 }
 
 

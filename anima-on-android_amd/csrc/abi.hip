@@ -1444,6 +1444,25 @@ size_t anima_hip_attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H
 }
 
 namespace {
+// Term-output rules shared by anima_hip_attention_terms_dev and
+// anima_hip_cross_attention_terms_dev.
+bool check_term_rows(const char *who, const uint16_t *out_terms, int64_t ld_terms,
+                     int64_t lo_offset, int H, int D)
+{
+    const std::string w(who);
+    if (D != 128)
+        return fail(w + ": the term output needs D == 128");
+    const int64_t HD = int64_t(H) * D;
+    if (ld_terms < HD || lo_offset < 0 || (lo_offset > 0 && (lo_offset < HD ||
+                                                             lo_offset + HD > ld_terms)))
+        return fail(w + ": a row of ld_terms elements must hold the hi block [0, H*D) and, "
+                        "when lo_offset > 0, the lo block [lo_offset, lo_offset + H*D)");
+    if (ld_terms % 8 || lo_offset % 8 || (reinterpret_cast<uintptr_t>(out_terms) & 15u))
+        return fail(w + ": out_terms must be 16-byte aligned, ld_terms and lo_offset "
+                        "multiples of 8");
+    return true;
+}
+
 // anima_hip_attention_dev and its term-output form: O goes to out (f32) or,
 // when out_t is set, to bf16 term rows (AttnInputs::out_t).
 bool attention_dev_call(const char *name, const float *q, const float *k, const float *v,
@@ -1504,16 +1523,8 @@ bool anima_hip_attention_terms_dev(const float *q, const float *k, const float *
                                    int S_q, int Bk, int S_kv, int H, int D, float eps, int mode,
                                    void *stream)
 {
-    if (D != 128)
-        return fail("attention_terms_dev: the term output needs D == 128");
-    const int64_t HD = int64_t(H) * D;
-    if (ld_terms < HD || lo_offset < 0 || (lo_offset > 0 && (lo_offset < HD ||
-                                                             lo_offset + HD > ld_terms)))
-        return fail("attention_terms_dev: a row of ld_terms elements must hold the hi block "
-                    "[0, H*D) and, when lo_offset > 0, the lo block [lo_offset, lo_offset + H*D)");
-    if (ld_terms % 8 || lo_offset % 8 || (reinterpret_cast<uintptr_t>(out_terms) & 15u))
-        return fail("attention_terms_dev: out_terms must be 16-byte aligned, ld_terms and "
-                    "lo_offset multiples of 8");
+    if (!check_term_rows("attention_terms_dev", out_terms, ld_terms, lo_offset, H, D))
+        return false;
     return attention_dev_call("attention_terms_dev", q, k, v, q_norm_w, k_norm_w, freqs, nullptr,
                               out_terms, ld_terms, lo_offset, scratch, scratch_bytes, B, S_q, Bk,
                               S_kv, H, D, eps, mode, stream);
@@ -1761,30 +1772,38 @@ size_t anima_hip_cross_attention_scratch_bytes(const anima_hip_ctx_kv *kv, int B
                                    true);
 }
 
-bool anima_hip_cross_attention_dev(const float *q, const float *q_norm_w,
-                                   const anima_hip_ctx_kv *kv, float *out, void *scratch,
-                                   size_t scratch_bytes, int B, int S_q, float eps, void *stream)
+namespace {
+// anima_hip_cross_attention_dev and its term-output form.
+bool cross_dev_call(const char *name, const float *q, const float *q_norm_w,
+                    const anima_hip_ctx_kv *kv, float *out, uint16_t *out_t, int64_t ld_t,
+                    int64_t lo_t, void *scratch, size_t scratch_bytes, int B, int S_q, float eps,
+                    void *stream)
 {
     if (!ready_for_device_call())
         return false;
+    const std::string who(name);
     if (!kv)
-        return fail("cross_attention_dev: null cache handle");
+        return fail(who + ": null cache handle");
     if (B < 0 || S_q < 0)
-        return fail("cross_attention_dev: negative dimension");
+        return fail(who + ": negative dimension");
+    if (out_t && !check_term_rows(name, out_t, ld_t, lo_t, kv->H, kv->D))
+        return false;
     if (int64_t(B) * S_q == 0)
         return true;
-    if (!q || !out || !scratch)
-        return fail("cross_attention_dev: null pointer");
+    if (!q || !(out || out_t) || !scratch)
+        return fail(who + ": null pointer");
     const AttnMode am = AttnMode(kv->mode);
     if (scratch_bytes < attention_scratch_bytes(B, S_q, kv->Bc, kv->S_kv, kv->H, kv->D, am, true))
-        return fail("cross_attention_dev: scratch smaller than "
-                    "anima_hip_cross_attention_scratch_bytes()");
+        return fail(who + ": scratch smaller than anima_hip_cross_attention_scratch_bytes()");
     AttnInputs in;
     in.q = q;
     in.q_norm_w = q_norm_w;
     in.k_prep = kv->k;
     in.v_prep = kv->v;
     in.out = out;
+    in.out_t = out_t;
+    in.ld_t = ld_t;
+    in.lo_t = lo_t;
     in.B = B;
     in.Bk = kv->Bc;
     in.S_q = S_q;
@@ -1794,6 +1813,25 @@ bool anima_hip_cross_attention_dev(const float *q, const float *q_norm_w,
     in.eps = eps;
     in.mode = am;
     return run_attention(in, scratch, pick_stream(stream));
+}
+}  // namespace
+
+bool anima_hip_cross_attention_dev(const float *q, const float *q_norm_w,
+                                   const anima_hip_ctx_kv *kv, float *out, void *scratch,
+                                   size_t scratch_bytes, int B, int S_q, float eps, void *stream)
+{
+    return cross_dev_call("cross_attention_dev", q, q_norm_w, kv, out, nullptr, 0, 0, scratch,
+                          scratch_bytes, B, S_q, eps, stream);
+}
+
+bool anima_hip_cross_attention_terms_dev(const float *q, const float *q_norm_w,
+                                         const anima_hip_ctx_kv *kv, uint16_t *out_terms,
+                                         int64_t ld_terms, int64_t lo_offset, void *scratch,
+                                         size_t scratch_bytes, int B, int S_q, float eps,
+                                         void *stream)
+{
+    return cross_dev_call("cross_attention_terms_dev", q, q_norm_w, kv, nullptr, out_terms,
+                          ld_terms, lo_offset, scratch, scratch_bytes, B, S_q, eps, stream);
 }
 
 bool anima_hip_cross_attention(const float *q, const float *q_norm_w, const anima_hip_ctx_kv *kv,

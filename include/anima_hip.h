@@ -366,6 +366,17 @@ bool anima_hip_cross_attention_dev(const float *q, const float *q_norm_w,
                                    const anima_hip_ctx_kv *kv, float *out, void *scratch,
                                    size_t scratch_bytes, int B, int S_q, float eps, void *stream);
 
+/* anima_hip_cross_attention_dev writing O as the bf16 terms of the output
+ * projection's input instead of f32 (no counterpart in the reference, like
+ * anima_hip_attention_terms_dev, whose out_terms / ld_terms / lo_offset rules
+ * it follows; D of the cache must be 128).  The DiT's cross-attention
+ * sub-layer runs this form. */
+bool anima_hip_cross_attention_terms_dev(const float *q, const float *q_norm_w,
+                                         const anima_hip_ctx_kv *kv, uint16_t *out_terms,
+                                         int64_t ld_terms, int64_t lo_offset, void *scratch,
+                                         size_t scratch_bytes, int B, int S_q, float eps,
+                                         void *stream);
+
 /* One attention sub-block of a DiT block on the device-resident residual
  * stream (NumpyBlock.forward, anima_rt/scripts/numpy_dit.py:236-247):
  *   x += gate[b] * output_proj(attention(layernorm(x) * (1 + scale[b]) + shift[b]))

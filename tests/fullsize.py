@@ -13,6 +13,10 @@ flash_attention.h:55-208) over all 32 slices on up to 16 host threads.
             V = ctx Wv^T, no RoPE, no mask).
   config 5: self-attention at 6144 tokens (96x64 grid, rectangular RoPE)
             and cross-attention 6144 x 512 over a cached context.
+
+block_ref restates one attention sub-layer of NumpyBlock.forward
+(numpy_dit.py:236-247) with float64 projections, for the full-size block
+tests.
 """
 import functools
 import os
@@ -106,3 +110,36 @@ def check_all_slices(out, ref, mode, what, f32_tol=1e-4, bf16_rel=2e-2):
     print(f"{what} mode={mode}: worst slice {'normwise' if mode == rt.BF16 else 'max_abs'} "
           f"{worst:.3e} over {out.shape[0] * out.shape[2]} slices", flush=True)
     return worst
+
+
+def proj_f64(a, w_bits):
+    """a[M, K] . W[N, K]^T as a float64 product of the f32 activations and
+    the bf16-decoded weights, rounded to f32: the exact mathematics of
+    anima_rt's bf16 GEMM (gemm_backend.cpp:117-131) without its float32
+    accumulation rounding, fast enough for M = 8192 on the host."""
+    w = oracle.bf16_bits_to_f32(w_bits).astype(np.float64)
+    return (np.asarray(a, np.float64) @ w.T).astype(np.float32)
+
+
+def block_ref(x, mod, wq, wk, wv, wo, qw, kw, freqs, ctx, heads=H, head_dim=D):
+    """One attention sub-layer of NumpyBlock.forward (numpy_dit.py:236-247,
+    NumpyAttention.forward 268-297) on the host:
+    x + gate * output_proj(attention(LayerNorm(x) * (1 + scale) + shift)).
+    LayerNorm, modulate, q/k RMSNorm, RoPE and flash attention (all slices,
+    THREADS host threads) through the oracle; the projections through
+    proj_f64.  Self-attention when ctx is None (K/V from the modulated x,
+    RoPE with freqs), else K/V projected from ctx [Bc, S_kv, C], no RoPE."""
+    B, S, Dm = x.shape
+    shift, scale, gate = (np.ascontiguousarray(mod[:, i]) for i in range(3))
+    xm = oracle.modulate(oracle.layernorm(x, 1e-6), scale, shift).reshape(B * S, Dm)
+    q = proj_f64(xm, wq).reshape(B, S, heads, head_dim)
+    src = xm.reshape(B, S, Dm) if ctx is None else np.asarray(ctx, np.float32)
+    k = np.stack([proj_f64(s, wk) for s in src]).reshape(len(src), -1, heads, head_dim)
+    v = np.stack([proj_f64(s, wv) for s in src]).reshape(len(src), -1, heads, head_dim)
+    if len(src) != B:
+        k = np.broadcast_to(k, (B,) + k.shape[1:])
+        v = np.broadcast_to(v, (B,) + v.shape[1:])
+    attn = oracle.attention_dataflow(q, k, v, qw, kw, freqs if ctx is None else None, 1e-6,
+                                     sdpa=threaded_sdpa)
+    out = proj_f64(attn.reshape(B * S, heads * head_dim), wo).reshape(B, S, Dm)
+    return oracle.gate_residual(x, gate, out)

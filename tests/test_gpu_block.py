@@ -31,7 +31,7 @@ def _weights(rng, n_out, n_in):
     return oracle.f32_to_bf16_bits(rng.standard_normal((n_out, n_in), dtype=np.float32) * 0.02)
 
 
-def _inputs(seed, B):
+def _inputs(seed, B, S=S):
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((B, S, DM), dtype=np.float32)
     mod = (rng.standard_normal((B, 3, DM)) * 0.5).astype(np.float32)
@@ -43,7 +43,7 @@ def _inputs(seed, B):
 def _run_block(x, mod, w, qw, kw, freqs, kv, mode):
     from devmem import DevBuf
     lib = _lib.load()
-    B = x.shape[0]
+    B, S = x.shape[:2]
     bufs = {name: DevBuf.of(a) for name, a in
             (("x", x), ("mod", mod), ("wq", w[0]), ("wk", w[1]), ("wv", w[2]), ("wo", w[3]),
              ("qw", qw), ("kw", kw))}

@@ -118,3 +118,34 @@ def test_timing_hook_reports_the_last_host_call():
     rt.softmax(q[0])
     k2, t2 = rt.last_call_ms()
     assert 0.0 < k2 <= t2 and (k2, t2) != (k_ms, t_ms)
+
+
+def test_numpyrt_sdpa_and_rmsnorm_on_numpy_attention_views():
+    """AnimaRT.run_rmsnorm / run_sdpa called the way NumpyAttention.forward
+    calls NumpyRT (numpy_dit.py:283-292, phone_pipeline_nd.py:53-68): the
+    per-head RMSNorm on [B,S,H,D] projections, one of them a column block of
+    a fused [B*S, 3*H*D] projection (a strided view), then SDPA on the
+    non-contiguous q/k/v.transpose(0,2,1,3) views.  The result must equal the
+    reference's marshaling (ascontiguousarray of the [B*H,S,D] reshape, flash
+    attention with scale 1/sqrt(D)) as the oracle computes it."""
+    B, S, H, D = 2, 96, 4, 128
+    rng = np.random.default_rng(88)
+    fused = rng.standard_normal((B * S, 3 * H * D)).astype(np.float32)
+    q = fused[:, :H * D].reshape(B, S, H, D)          # a strided view
+    k = np.ascontiguousarray(fused[:, H * D:2 * H * D]).reshape(B, S, H, D)
+    v = np.ascontiguousarray(fused[:, 2 * H * D:]).reshape(B, S, H, D)
+    qw = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    r = rt.AnimaRT({"blk.q_norm.weight": qw, "blk.k_norm.weight": np.ones(D, np.float32)})
+    qn = r.run_rmsnorm(q, "blk.q_norm")
+    kn = r.run_rmsnorm(k, "blk.k_norm")
+    np.testing.assert_array_equal(qn, oracle.rmsnorm(np.ascontiguousarray(q), qw))
+    np.testing.assert_array_equal(kn, oracle.rmsnorm(k, np.ones(D, np.float32)))
+
+    qs, ks, vs = (t.transpose(0, 2, 1, 3) for t in (qn, kn, v))
+    assert not qs.flags.c_contiguous
+    out = r.run_sdpa(qs, ks, vs)
+    assert out.shape == (B, H, S, D)
+    ref = oracle.flash_sdpa(*(np.ascontiguousarray(t.reshape(B * H, S, D)) for t in (qs, ks, vs)))
+    assert np.abs(out.reshape(B * H, S, D) - ref).max() <= 1e-4
+    # The caller's arrays are left as they were.
+    np.testing.assert_array_equal(qs, qn.transpose(0, 2, 1, 3))

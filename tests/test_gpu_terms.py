@@ -105,3 +105,65 @@ def test_term_output_argument_errors():
     assert not call(2 * HD, HD + 8) and "lo block" in _lib.last_error()
     assert not call(2 * HD + 4, HD) and "multiples of 8" in _lib.last_error()
     assert not call(2 * HD, HD) and "null pointer" in _lib.last_error()
+
+
+# Cross-attention over a cached 512-token context at the 1024x1024 image's
+# 4096 query tokens (B = 2): an 8-wave grid, so in the f32 and f32x3 modes the
+# flash kernel normalises the raw query rows itself and writes the terms --
+# the combination the DiT's cross-attention sub-layer runs.  Also a 4-wave
+# grid (256 query tokens) with a broadcast context, and a ragged tile.
+@pytest.mark.parametrize("mode", [rt.F32, rt.F32X3, rt.BF16])
+@pytest.mark.parametrize("B,S_q,Bc", [(2, 4096, 2), (2, 256, 1), (2, 2000, 2)])
+def test_cross_term_output_is_the_split_of_the_f32_output(mode, B, S_q, Bc):
+    from devmem import DevBuf
+    lib = _lib.load()
+    rng = np.random.default_rng(9100 + S_q + Bc + mode)
+    q = rng.standard_normal((B, S_q, H, D), dtype=np.float32)
+    qw = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    ctx = (rng.standard_normal((Bc, 512, 1024)) * 0.5).astype(np.float32)
+    wk, wv = (oracle.f32_to_bf16_bits(rng.standard_normal((HD, 1024), dtype=np.float32) * 0.02)
+              for _ in range(2))
+    kv = rt.ContextKV(ctx, wk, wv, None, heads=H, head_dim=D, mode=mode)
+    print(f"cross attention terms B={B} S_q={S_q} Bc={Bc} mode={mode}", flush=True)
+    try:
+        dq, dw = DevBuf.of(q), DevBuf.of(qw)
+        n = lib.anima_hip_cross_attention_scratch_bytes(kv.handle, B, S_q)
+        scratch = DevBuf(n)
+        eps = ct.c_float(1e-6)
+        out = DevBuf(q.nbytes)
+        _lib.check(lib.anima_hip_cross_attention_dev(dq.addr, dw.addr, kv.handle, out.addr,
+                                                     scratch.addr, n, B, S_q, eps, None),
+                   "cross_attention_dev")
+        o = out.get((B * S_q, HD), np.float32)
+        hi, lo = _split_terms(o)
+        ld, lo_off = 2 * HD + 16, HD + 8
+        t = DevBuf.of(np.full((B * S_q, ld), SENTINEL, np.uint16))
+        _lib.check(lib.anima_hip_cross_attention_terms_dev(dq.addr, dw.addr, kv.handle, t.addr,
+                                                           ld, lo_off, scratch.addr, n, B, S_q,
+                                                           eps, None),
+                   "cross_attention_terms_dev")
+        got = t.get((B * S_q, ld), np.uint16)
+        np.testing.assert_array_equal(got[:, :HD], hi)
+        np.testing.assert_array_equal(got[:, lo_off:lo_off + HD], lo)
+        assert np.all(got[:, HD:lo_off] == SENTINEL) and np.all(got[:, lo_off + HD:] == SENTINEL)
+        if S_q == 4096:
+            # One (batch, head) slice of the f32 output against the oracle.
+            k, v = (np.stack([oracle.gemm_bf16(ctx[b], w) for b in range(Bc)])
+                    .reshape(Bc, 512, H, D) for w in (wk, wv))
+            ref = oracle.attention_dataflow(q[1:2, :, 5:6], k[1:2, :, 5:6], v[1:2, :, 5:6],
+                                            qw, None, None)
+            err = np.abs(o.reshape(B, S_q, H, D)[1:2, :, 5:6] - ref).max()
+            if mode == rt.BF16:
+                err /= np.abs(ref).max()
+            print(f"  slice (1, 5) error {err:.3e}", flush=True)
+            assert err <= (2e-2 if mode == rt.BF16 else 1e-4)
+    finally:
+        kv.close()
+
+
+def test_cross_term_output_argument_errors():
+    lib = _lib.load()
+    eps = ct.c_float(1e-6)
+    assert not lib.anima_hip_cross_attention_terms_dev(None, None, None, None, HD, 0, None, 0, 1,
+                                                       4, eps, None)
+    assert "null cache handle" in _lib.last_error()

@@ -169,3 +169,35 @@ def test_rope_tables_match_reference_builder_bitwise(grid):
             np.testing.assert_array_equal(table, g[f"table_{key}"])
         digest = hashlib.sha256(np.ascontiguousarray(table).tobytes()).hexdigest()
         assert digest == str(g[f"sha256_{key}"])
+
+
+@pytest.mark.parametrize("cross", [False, True])
+def test_float64_block_checker_matches_oracle_composition(cross):
+    """fullsize.block_ref (float64 projections, used by the full-size block
+    tests where the scalar bf16 GEMM would take minutes) against the oracle's
+    own composition of the sub-layer (oracle.attention_block, anima_rt's
+    float32-accumulating bf16 GEMM) at 64 tokens: the two differ only by the
+    projections' accumulation rounding."""
+    import fullsize
+    rng = np.random.default_rng(4403 + cross)
+    B, S, Dm, H, D = 2, 64, 2048, 16, 128
+    x = rng.standard_normal((B, S, Dm), dtype=np.float32)
+    mod = (rng.standard_normal((B, 3, Dm)) * 0.5).astype(np.float32)
+
+    def w(n, k):
+        return oracle.f32_to_bf16_bits(rng.standard_normal((n, k), dtype=np.float32) * 0.02)
+
+    wq, wo = w(H * D, Dm), w(Dm, H * D)
+    qw, kw = (rng.uniform(0.5, 1.5, D).astype(np.float32) for _ in range(2))
+    if cross:
+        ctx = (rng.standard_normal((1, 96, 1024)) * 0.5).astype(np.float32)
+        wk, wv, f = w(H * D, 1024), w(H * D, 1024), None
+    else:
+        ctx, wk, wv, f = None, w(H * D, Dm), w(H * D, Dm), oracle.rope_freqs(8, 8)
+    ours = fullsize.block_ref(x, mod, wq, wk, wv, wo, qw, kw, f, ctx)
+    theirs = oracle.attention_block(x, mod, wq, wk, wv, wo, qw, kw, f, ctx, heads=H, head_dim=D)
+    d_ours, d_theirs = ours - x, theirs - x
+    err = np.abs(d_ours - d_theirs).max() / np.abs(d_theirs).max()
+    assert err <= 1e-5, err
+    # A dropped term is far outside that: the gate alone moves the update by its own size.
+    assert np.abs(d_theirs).max() > 0.05
