@@ -26,6 +26,10 @@ step and one whole-DiT sampler step) are reported beside it.
 `cpu_baseline` times anima_rt's own flash attention (the reference built from
 source in oracle/_ref when present, else the bit-identical C restatement) on a
 bounded sample of the same heads on this host's CPU.
+`sustained_mfma` is what the bf16 MFMA pipe of this GPU sustains in the same
+run with nothing else issued beside it (libanima_probe.so), on N(0,1)
+operands and on zeros, with the shader clock it held; the f32x3 and bf16
+rooflines also carry their executed bf16 MFMA rate as a fraction of it.
 """
 import argparse
 import ctypes as ct
@@ -90,7 +94,9 @@ def parse():
                          "every mode; prints one JSON line of its own")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 256 MiB device copy (calibrates "
-                         "FETCH_SIZE/WRITE_SIZE) then 2 steps of each variant; prints no JSON")
+                         "FETCH_SIZE/WRITE_SIZE) then 2 steps of each variant (with "
+                         "--cross-step: cached-context cross-attention calls of each mode "
+                         "instead); prints no JSON")
     return ap.parse_args()
 
 
@@ -234,6 +240,53 @@ def headline(c, variant, q, k, v, freqs, ones, steps, warmup):
                      "flops_per_launch": flops},
         "qn": qn, "kn": kn,
     }
+
+
+def sustained_mfma(c, launch_ms=5.0, timed=20):
+    """What the bf16 MFMA pipe sustains on this GPU, now, with nothing else
+    issued beside it (libanima_probe.so: one 8-wave workgroup per CU, each
+    wave an unrolled loop of independent v_mfma_f32_32x32x16_bf16 on
+    operands read once from HBM), for N(0,1) operands -- the benchmark's
+    data -- and for zeros.  The published peak assumes the 2.4 GHz peak
+    clock; under sustained MFMA load the GPU lowers its clock to its power
+    limit, by how much depending on the operands' bit activity.  Each run
+    pre-warms for PREWARM_S seconds like the headline, then times `timed`
+    launches of about `launch_ms` each with HIP events on the bench
+    stream."""
+    torch = c.torch
+    path = os.path.join(ROOT, "anima-on-android_amd", "anima_hip", "libanima_probe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} missing: run make -C anima-on-android_amd")
+    L = ct.CDLL(path)
+    L.anima_probe_mfma_src_bytes.restype = ct.c_size_t
+    L.anima_probe_mfma_src_bytes.argtypes = [ct.c_int]
+    L.anima_probe_mfma.restype = ct.c_bool
+    L.anima_probe_mfma.argtypes = [ct.c_void_p] + [ct.c_int] * 4 + [
+        ct.c_void_p, ct.POINTER(ct.c_float), ct.POINTER(ct.c_double), ct.POINTER(ct.c_double)]
+    cus = torch.cuda.get_device_properties(c.dev).multi_processor_count
+    n = L.anima_probe_mfma_src_bytes(cus) // 2
+    out = {"kernel": "v_mfma_f32_32x32x16_bf16 only, 16 independent MFMAs per loop iteration, "
+                     "one 8-wave workgroup per CU (%d CUs)" % cus}
+    for name in ("n01", "zeros"):
+        src = (c.randn((n,), 4242) if name == "n01"
+               else torch.zeros(n, device=c.dev)).to(torch.bfloat16)
+        ms, tf, ghz = ct.c_float(), ct.c_double(), ct.c_double()
+        # Calibrate the loop count to about launch_ms per launch.
+        iters = 2000
+        if not L.anima_probe_mfma(src.data_ptr(), cus, iters, 1, 1, c.stp, ms, tf, ghz):
+            raise RuntimeError("anima_probe_mfma failed")
+        iters = max(100, int(iters * launch_ms / max(ms.value, 1e-3)))
+        warm = max(1, int(PREWARM_S * 1e3 / launch_ms))
+        if not L.anima_probe_mfma(src.data_ptr(), cus, iters, warm, timed, c.stp, ms, tf, ghz):
+            raise RuntimeError("anima_probe_mfma failed")
+        out[name] = {"tflops": round(tf.value, 1), "clock_ghz": round(ghz.value, 3),
+                     "frac_of_peak": round(tf.value / PEAK_TFLOPS["bf16"], 4),
+                     "ms_per_launch": round(ms.value, 3)}
+        log(f"[bench] sustained bf16 MFMA ({name} operands): {tf.value:.1f} TFLOP/s at "
+            f"{ghz.value:.3f} GHz ({100 * tf.value / PEAK_TFLOPS['bf16']:.1f}% of the published "
+            f"peak)")
+        del src
+    return out
 
 
 def self_attention_timer(c, mode, B, S, grid, seed, H=16, D=128):
@@ -568,37 +621,51 @@ def cpu_model():
     return platform.processor() or platform.machine()
 
 
-def cpu_per_config(fn, rate_tflops, sample):
+def cpu_per_config(fn, c3_slice_s, sample):
     """anima_rt's flash attention per configuration on one host core.
     Configs 1 and 2 are small enough to time whole (median of 3 runs, seeded
-    N(0,1) slices of their shapes); config 3 is the headline's measured
-    sample; configs 4 and 5 are extrapolated from that sample's rate."""
+    N(0,1) slices of their shapes).  Config 3 is the headline's measured
+    sample, scaled to its 32 (batch, head) slices.  The other shapes are
+    timed on a sample of their own slices and scaled to 32 (every slice of a
+    shape does the same work; flash_attention.h:55-208 has no data-dependent
+    branch): the 4096 x 512 cross-attention (config 4 = 28 x (config 3 +
+    that)), 6144 x 6144 and 6144 x 512 (config 5)."""
     import numpy as np
     rng = np.random.default_rng(77)
     out = {}
+
+    def slices(bh, sq, sk):
+        return [rng.standard_normal((bh, n, 128), dtype=np.float32) for n in (sq, sk, sk)]
+
+    def timed(q, k, v):
+        t0 = time.perf_counter()
+        fn(q, k, v, 1.0 / math.sqrt(128))
+        return time.perf_counter() - t0
+
     for key, bh, sq, sk, what in (("c1", 16, 256, 256, "self-attention B=1 H=16 256x256"),
                                   ("c2", 32, 256, 512, "cross-attention B=2 H=16 256x512")):
-        q = rng.standard_normal((bh, sq, 128), dtype=np.float32)
-        k = rng.standard_normal((bh, sk, 128), dtype=np.float32)
-        v = rng.standard_normal((bh, sk, 128), dtype=np.float32)
-        runs = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            fn(q, k, v, 1.0 / math.sqrt(128))
-            runs.append(time.perf_counter() - t0)
-        out[key] = {"seconds": round(sorted(runs)[1], 4), "how": "measured, median of 3",
+        q, k, v = slices(bh, sq, sk)
+        runs = sorted(timed(q, k, v) for _ in range(3))
+        out[key] = {"seconds": round(runs[1], 4), "how": "measured, median of 3",
                     "workload": what}
-    fl = {"c3": 4.0 * 32 * 4096 * 4096 * 128,
-          "c4": 28 * 4.0 * 32 * 4096 * 128 * (4096 + 512),
-          "c5": 4.0 * 32 * 6144 * 128 * (6144 + 512)}
-    out["c3"] = {"seconds": round(fl["c3"] / (rate_tflops * 1e12), 2),
+    # Per-slice one-core seconds of the other shapes, from samples.
+    per_slice = {"self4096": (c3_slice_s, sample)}
+    for key, n, sq, sk in (("cross4096x512", 4, 4096, 512), ("self6144", 1, 6144, 6144),
+                           ("cross6144x512", 4, 6144, 512)):
+        dt = timed(*slices(n, sq, sk))
+        per_slice[key] = (dt / n, f"{n} slice(s) of {sq}x{sk} measured, {dt:.2f} s")
+    out["c3"] = {"seconds": round(32 * c3_slice_s, 2),
                  "how": f"sample ({sample}), scaled to all 32 slices",
                  "workload": "self-attention B=2 H=16 4096x4096"}
-    out["c4"] = {"seconds": round(fl["c4"] / (rate_tflops * 1e12), 1),
-                 "how": "extrapolated from the config-3 sample's rate",
+    c4 = 28 * 32 * (per_slice["self4096"][0] + per_slice["cross4096x512"][0])
+    out["c4"] = {"seconds": round(c4, 1),
+                 "how": "28 blocks x 32 slices x (4096x4096 per-slice time of the config-3 "
+                        "sample + 4096x512 per-slice time, " + per_slice["cross4096x512"][1] + ")",
                  "workload": "28 x (self 4096x4096 + cross 4096x512), B=2 H=16"}
-    out["c5"] = {"seconds": round(fl["c5"] / (rate_tflops * 1e12), 1),
-                 "how": "extrapolated from the config-3 sample's rate",
+    c5 = 32 * (per_slice["self6144"][0] + per_slice["cross6144x512"][0])
+    out["c5"] = {"seconds": round(c5, 1),
+                 "how": "32 slices x (" + per_slice["self6144"][1] + "; " +
+                        per_slice["cross6144x512"][1] + ")",
                  "workload": "self 6144x6144 + cross 6144x512, B=2 H=16"}
     return out
 
@@ -635,7 +702,7 @@ def cpu_baseline(qn, kn, v, B, H, S, D, heads):
               "sample": sample, "seconds": round(dt, 3), "nproc": os.cpu_count(),
               "cpu_model": cpu_model(), "threads": 1}
     log("[bench] cpu baseline per config")
-    single["per_config"] = cpu_per_config(fn, single["value"], f"{n1} of {B * H} slices")
+    single["per_config"] = cpu_per_config(fn, dt / n1, f"{n1} of {B * H} slices")
 
     threads = max(1, min(16, os.cpu_count() or 1, B * H))
     multi = None
@@ -681,6 +748,23 @@ def main():
     lib = _lib.load()
     _lib.check(lib.anima_rt_init(), "anima_rt_init")
     c = Ctx(torch, lib, _lib)
+
+    if args.pmc_pass and args.cross_step:
+        # Counter pass over the cached-context cross-attention: the
+        # calibration copy, then a few calls of every mode.
+        src = torch.empty(COPY_BYTES // 4, device=c.dev).normal_()
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        for v in ("bf16", "f32x3", "f32"):
+            cache = context_cache(c, MODE[v], 2, 4000)
+            run, _ = cross_attention_timer(c, MODE[v], cache, 2, 4096, 77)
+            c.time(run, 5, 1, prewarm_s=0.5)
+            cache.close()
+        log("[bench] cross pmc pass done")
+        return
 
     if args.cross_step:
         res = {}
@@ -738,6 +822,17 @@ def main():
                 qk_f32 = (r["qn"], r["kn"])
             del r
 
+    # The bf16 MFMA rate this GPU sustains right now on N(0,1) operands,
+    # beside which the f32x3 and bf16 kernels' executed MFMA rates are read.
+    sustained = sustained_mfma(c)
+    sus = sustained["n01"]["tflops"]
+    for var, roof in [(args.variant, main_res["roofline"])] + [
+            (k, r["roofline"]) for k, r in variants.items()]:
+        if var in ("f32x3", "bf16"):
+            executed = roof["achieved"] * (3 if var == "f32x3" else 1)
+            roof["executed_bf16_mfma_tflops"] = round(executed, 1)
+            roof["frac_of_sustained_mfma"] = round(executed / sus, 4)
+
     dropin = None if args.headline_only else dropin_call(c, host, B, H, S, D)
 
     cpu = multi = None
@@ -778,6 +873,7 @@ def main():
                    else "v_mfma_f32_32x32x16_bf16"},
         "pct_mfma_peak": round(100.0 * value / peak, 2),
         "roofline": main_res["roofline"],
+        "sustained_mfma": sustained,
         "cpu_baseline": cpu,
         "cpu_baseline_multicore": multi,
         "speedup_vs_cpu": None if cpu is None else round(value / cpu["value"], 1),

@@ -306,7 +306,12 @@ bool anima_hip_attention_terms_dev(const float *q, const float *k, const float *
  * hipMalloc).  Same arguments, kernels and results as
  * anima_hip_attention_dev; the scratch is a static device array of
  * ANIMA_HIP_STATIC_SCRATCH_BYTES that each GPU holds from the first call
- * made on it until the process ends.  A problem whose
+ * made on it until the process ends (measured on MI355X: the library's
+ * other entries leave it unreserved; free device memory drops by 194 MiB
+ * at the first static call).  The array's device address is looked up once
+ * per GPU, at that first call, and kept: resetting a device
+ * (hipDeviceReset) while the library is loaded is not supported.  The first
+ * call may itself be captured into a HIP graph.  A problem whose
  * anima_hip_attention_scratch_bytes() exceeds that size is rejected (false,
  * with a message) before anything is enqueued; 192 MiB covers the
  * 1024x1024 image's self-attention (B = 2, 4096 tokens, 16 x 128) in every

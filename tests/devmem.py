@@ -77,3 +77,45 @@ class DevBuf:
             self.close()
         except Exception:
             pass
+
+
+class CapturedCall:
+    """One HIP graph captured on a stream of its own (hipStreamBeginCapture,
+    thread-local mode) around `fn(stream)`, instantiated and replayable."""
+
+    MODE_THREAD_LOCAL = 1
+
+    def __init__(self, fn):
+        h = hip()
+        for f in (h.hipStreamCreate, h.hipStreamBeginCapture, h.hipStreamEndCapture,
+                  h.hipGraphInstantiate, h.hipGraphLaunch, h.hipStreamSynchronize,
+                  h.hipGraphExecDestroy, h.hipGraphDestroy, h.hipStreamDestroy):
+            f.restype = ct.c_int
+        self.stream = ct.c_void_p()
+        _ok(h.hipStreamCreate(ct.byref(self.stream)), "hipStreamCreate")
+        self.graph, self.exec = ct.c_void_p(), ct.c_void_p()
+        _ok(h.hipStreamBeginCapture(self.stream, self.MODE_THREAD_LOCAL), "hipStreamBeginCapture")
+        try:
+            fn(self.stream)
+        finally:
+            end = h.hipStreamEndCapture(self.stream, ct.byref(self.graph))
+        _ok(end, "hipStreamEndCapture")
+        _ok(h.hipGraphInstantiate(ct.byref(self.exec), self.graph, None, None, ct.c_size_t(0)),
+            "hipGraphInstantiate")
+
+    def replay(self):
+        h = hip()
+        _ok(h.hipGraphLaunch(self.exec, self.stream), "hipGraphLaunch")
+        _ok(h.hipStreamSynchronize(self.stream), "hipStreamSynchronize")
+
+    def close(self):
+        h = hip()
+        if self.exec.value:
+            h.hipGraphExecDestroy(self.exec)
+            self.exec = ct.c_void_p()
+        if self.graph.value:
+            h.hipGraphDestroy(self.graph)
+            self.graph = ct.c_void_p()
+        if self.stream.value:
+            h.hipStreamDestroy(self.stream)
+            self.stream = ct.c_void_p()

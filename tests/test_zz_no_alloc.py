@@ -4,7 +4,13 @@ anima_hip_attention_dev with caller scratch on the same inputs.
 
 The two entries run the same kernels on the same inputs, so their outputs
 must agree bit for bit: on two calls in a row, the second one smaller (so it
-reuses scratch that the first call left filled), in every arithmetic mode.
+reuses scratch that the first call left filled), in every arithmetic mode;
+at the 1024x1024 image's self-attention (B=2, 4096 tokens, f32x3), whose
+scratch is exactly the static size; and captured into a HIP graph (stream
+capture, thread-local mode) by the module's first test, so that the
+process's first static call -- the one that looks the array's device
+address up -- happens under capture, with the graph replayed three times
+beside direct calls.
 The smaller call also goes through split-KV partials, which live in the
 static array too, and is held to the oracle's tolerance (max-abs 1e-4 for
 the f32 and f32x3 modes, normwise 2e-2 for bf16).  A problem beyond the
@@ -28,6 +34,34 @@ STATIC_BYTES = 192 * 1024 * 1024
 @pytest.fixture(scope="module", autouse=True)
 def _init():
     rt.init()
+
+
+@pytest.mark.parametrize("mode", [rt.F32X3, rt.BF16, rt.F32])
+def test_static_entry_under_graph_capture(mode):
+    from devmem import CapturedCall
+    lib = _lib.load()
+    B, S, grid = 2, 1024, (32, 32)
+    q, k, v, qw, kw, freqs = _case(7500 + mode, B, S, B, S, grid)
+    dev = _Dev(q, k, v, qw, kw, freqs)
+    print(f"  capture attention_static_dev B={B} S={S} mode={mode}", flush=True)
+
+    def call(stream):
+        ok = lib.anima_hip_attention_static_dev(*dev.args(), B, S, B, S, H, D, ct.c_float(1e-6),
+                                                mode, stream)
+        _lib.check(ok, "attention_static_dev (captured)")
+
+    g = CapturedCall(call)
+    try:
+        for _ in range(3):
+            dev.out.put(np.full(q.shape, np.nan, np.float32), 0)
+            g.replay()
+            got = dev.out.get(q.shape)
+            direct = _static(dev, B, S, B, S, mode)
+            assert np.array_equal(got, direct)
+    finally:
+        g.close()
+    ref, _ = _with_scratch(dev, B, S, B, S, mode)
+    assert np.array_equal(got, ref)
 
 
 def _case(seed, B, S_q, Bk, S_kv, grid):
@@ -120,3 +154,15 @@ def test_static_scratch_refuses_oversized_problem():
     assert not ok
     assert "static" in _lib.last_error()
     assert np.isnan(dev.out.get(dev.shape)).all()
+
+
+def test_static_entry_at_the_1024_image_self_attention():
+    # B=2, 4096 tokens (64x64 grid), f32x3: exactly the static size.
+    lib = _lib.load()
+    B, S = 2, 4096
+    assert lib.anima_hip_attention_scratch_bytes(B, S, B, S, H, D, rt.F32X3) == STATIC_BYTES
+    q, k, v, qw, kw, freqs = _case(7600, B, S, B, S, (64, 64))
+    dev = _Dev(q, k, v, qw, kw, freqs)
+    ref, n = _with_scratch(dev, B, S, B, S, rt.F32X3)
+    out = _static(dev, B, S, B, S, rt.F32X3)
+    assert np.isfinite(out).all() and np.array_equal(out, ref)
