@@ -11,6 +11,7 @@ namespace anima_hip {
 namespace flash_tile {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -161,7 +162,10 @@ __device__ __forceinline__ void store_out4(const f32x4 &v, float *o, u16 *t, int
 // reference's flash attention leaves there (flash_attention.h:148-152 skips
 // such rows and :194-201 divides only positive sums of a zero-filled output).
 // With trow0 set, the rows go out as bf16 terms (split_terms4) at trow0 +
-// r * tstride instead of f32 at row0 + r * stride, in 16-byte stores.
+// r * tstride instead of f32 at row0 + r * stride, in 16-byte stores.  The
+// stores are nontemporal (streaming): this kernel never reads O back
+// (4096 tokens, B=2, H=16: step 0.6779 -> 0.6745 ms f32x3, 4096 x 512
+// cross-attention 109.9 -> 108.1 us f32x3 and 68.1 -> 67.2 us bf16).
 // The caller guarantees no other wave uses `lds` (kOWaveFloats floats).
 constexpr int kOPitch = 68;  // floats per staged half row: 64 d + 4 against bank conflicts
 constexpr int kOWaveFloats = 32 * kOPitch;
@@ -205,9 +209,11 @@ __device__ __forceinline__ void store_o_rows(float *lds, const f32x16 &o0, const
                 split_terms4(*reinterpret_cast<const f32x4 *>(src + 4), h1, l1);
                 u16 *dst = trow0 + r * tstride + 64 * p + 8 * c;
                 if (r < nrows) {
-                    *reinterpret_cast<uint4 *>(dst) = uint4{h0.x, h0.y, h1.x, h1.y};
+                    __builtin_nontemporal_store(u32x4{h0.x, h0.y, h1.x, h1.y},
+                                                reinterpret_cast<u32x4 *>(dst));
                     if (tlo > 0)
-                        *reinterpret_cast<uint4 *>(dst + tlo) = uint4{l0.x, l0.y, l1.x, l1.y};
+                        __builtin_nontemporal_store(u32x4{l0.x, l0.y, l1.x, l1.y},
+                                                    reinterpret_cast<u32x4 *>(dst + tlo));
                 }
             }
         } else {
@@ -217,7 +223,8 @@ __device__ __forceinline__ void store_o_rows(float *lds, const f32x16 &o0, const
                 const int r = 4 * i + (lane >> 4);
                 const f32x4 v = *reinterpret_cast<const f32x4 *>(lds + r * kOPitch + 4 * c);
                 if (r < nrows)
-                    *reinterpret_cast<f32x4 *>(row0 + r * stride + 64 * p + 4 * c) = v;
+                    __builtin_nontemporal_store(
+                        v, reinterpret_cast<f32x4 *>(row0 + r * stride + 64 * p + 4 * c));
             }
         }
         // This pass's reads complete before the next pass overwrites the rows.
