@@ -168,6 +168,21 @@ bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, 
 uint16_t *launch_split_interleaved(const float *a, int64_t lda, int M, int K, void *scratch,
                                    size_t scratch_bytes, hipStream_t st);
 
+// Large-M bf16 GEMM (gemm_large.hip): C[M,N] = a0 . W^T (+ a1 . W^T) with
+// bf16 terms [M][lda] and weights [N][ldw], f32 accumulation, 256 x 256 (one
+// term) or 128 x 256 (two terms) tiles of C.  Epilogue kGemmOutF32: C f32
+// [M][ldc]; kGemmOutBf16: C bf16 (round to nearest even); kGemmOutResidual:
+// c is the f32 residual x [M][ldc], x += gate[(m / S) * gate_stride + n] * C.
+// gemm_large_supported says whether the shape, alignments and grid (at least
+// 256 tiles) suit it; out_bytes is the output element size.
+enum GemmOut { kGemmOutF32 = 0, kGemmOutBf16 = 1, kGemmOutResidual = 2 };
+bool gemm_large_supported(int M, int N, int K, int terms, int64_t lda, int64_t ldw, int64_t ldc,
+                          const void *a0, const void *a1, const void *w, const void *c,
+                          int out_bytes);
+bool launch_gemm_large(const uint16_t *a0, const uint16_t *a1, int64_t lda, const uint16_t *w,
+                       int64_t ldw, void *c, int64_t ldc, int M, int N, int K, int epilogue,
+                       const float *gate, int64_t gate_stride, int S, hipStream_t st);
+
 // Small-M bf16 GEMM (gemm_bf16.hip): C[M,N] = a0 . W^T (+ a1 . W^T) with bf16
 // activation terms a0 (a1 null for one term) [M][lda], bf16 W [N][ldw], f32
 // C [M][ldc], for M <= 1024 and K a multiple of 64 (K per term), split over K

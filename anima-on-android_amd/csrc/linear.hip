@@ -207,6 +207,9 @@ bool launch_linear_terms(const uint16_t *hi, const uint16_t *lo, const uint16_t 
     if (ws && small_m_path(M, K, lo != nullptr) &&
         gemm_bf16_supported(M, N, K, padded_k(K), ldw, ldc, hi, lo, w, c, ws_bytes))
         return launch_gemm_bf16(hi, lo, padded_k(K), w, ldw, c, ldc, M, N, K, ws, ws_bytes, st);
+    if (lo && gemm_large_supported(M, N, K, 2, padded_k(K), ldw, ldc, hi, lo, w, c, 4))
+        return launch_gemm_large(hi, lo, padded_k(K), w, ldw, c, ldc, M, N, K, kGemmOutF32,
+                                 nullptr, 0, 0, st);
     if (!linear_terms_supported(M, N, K, w, ldw, c, ldc))
         return fail("linear: no bf16 GEMM for this shape");
     if ((reinterpret_cast<uintptr_t>(hi) & 15u) != 0 || (reinterpret_cast<uintptr_t>(lo) & 15u) != 0)
@@ -352,6 +355,13 @@ bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, 
         const uint16_t *lo = reinterpret_cast<const uint16_t *>(s.lo);
         if (gemm_bf16_supported(M, N, K, kp, ldw, ldc, hi, lo, w, c, wsb))
             return launch_gemm_bf16(hi, lo, kp, w, ldw, c, ldc, M, N, K, ws, wsb, st);
+    }
+    {
+        const uint16_t *hi = reinterpret_cast<const uint16_t *>(s.hi);
+        const uint16_t *lo = reinterpret_cast<const uint16_t *>(s.lo);
+        if (exact && gemm_large_supported(M, N, K, 2, kp, ldw, ldc, hi, lo, w, c, 4))
+            return launch_gemm_large(hi, lo, kp, w, ldw, c, ldc, M, N, K, kGemmOutF32, nullptr, 0,
+                                     0, st);
     }
     std::lock_guard<std::mutex> g(g_lt_mu);
     if (!lt_matmul(plan, w, s.hi, c, 0.0f, st))

@@ -120,6 +120,33 @@ def test_linear_projection_8192x2048x2048_sampled_rows():
         assert err <= tol
 
 
+# Shapes of the large-M kernel (at least 256 output tiles of 256 x 256, or
+# of 128 x 256 with two terms): the 1024x1024 image's projections at
+# M = 8192 -- q/k/v/o (N = 2048), the fused q/k/v (N = 6144), fc1 (N = 8192)
+# and fc2 (K = 8192) -- and ragged M and N with the last rows and columns
+# of the tile clamped.  Rows are sampled for the oracle, including both ends
+# of every ragged edge.
+LARGE_M = [(8192, 6144, 2048), (8192, 8192, 2048), (8192, 2048, 8192), (8000, 2100, 512),
+           (8200, 2048, 1024)]
+
+
+@pytest.mark.parametrize("M,N,K", LARGE_M)
+def test_large_m_kernel_vs_oracle(M, N, K):
+    a, w = _data(M * 3 + N + K, M, N, K)
+    rows = np.unique(np.concatenate([[0, 1, 255, 256, M - 257, M - 256, M - 2, M - 1],
+                                     np.random.default_rng(M + N).integers(0, M, 24)]))
+    ref = oracle.gemm_bf16(np.ascontiguousarray(a[rows]), w)
+    print(f"large-M linear M={M} N={N} K={K}", flush=True)
+    e = {}
+    for mode, tol in ((rt.F32, REL_F32), (rt.BF16, REL_BF16)):
+        out = run_linear(a, w, mode)
+        assert np.isfinite(out).all()
+        e[mode] = rel_err(out[rows], ref)
+        print(f"  mode {mode}: rel err {e[mode]:.2e} on {len(rows)} rows", flush=True)
+        assert e[mode] <= tol
+    assert e[rt.F32] * 20 < e[rt.BF16]
+
+
 def test_linear_drop_in_gemm_bf16_is_split_path():
     """anima_rt_run_gemm_bf16 (host drop-in) runs the F32 split mode on shapes
     the library GEMM supports, within the drop-in's 1e-5 bound."""
