@@ -25,8 +25,10 @@
 //   final layer       LN + modulate (2 chunks) -> linear (numpy_dit.py:186-201);
 //   unpatchify_kernel _rearrange_unpatchify + crop (numpy_dit.py:24-31, 128-129);
 //   cfg_euler_kernel  sampler only: v = v_u + cfg (v_c - v_u), x += v dt.
-// Linear layers over tokens run on hipBLASLt (linear.hip); f32 mode feeds them
-// exact hi + lo bf16 terms of the f32 activations, bf16 mode rounds the
+// Linear layers over tokens run through linear.hip: the hand-written small-M
+// kernel (gemm_bf16.hip) at M <= 1024, the large-M kernel (gemm_large.hip)
+// for products of two term planes, hipBLASLt for the rest.  f32 mode feeds
+// them exact hi + lo bf16 terms of the f32 activations, bf16 mode rounds the
 // activations to bf16.
 #include "common.h"
 
