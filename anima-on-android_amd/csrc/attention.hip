@@ -209,7 +209,10 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     // Self-attention keeps it too, where the RoPE table's reads at each
     // workgroup's start cost more than the pass.
     // The f32 kernel, which reads Q as f32 rows anyway, does the same (RMSNorm
-    // only: its rows carry no terms; 4096 x 512: 307.5 -> 286.5 us).
+    // only: its rows carry no terms; 4096 x 512: 307.5 -> 286.5 us).  The
+    // bf16 kernel keeps the row pass: with raw rows it reads twice the Q
+    // bytes at each workgroup's start, and the call measured the same
+    // (4096 x 512, B = 2: 65.7 against 65.9 us, bit-identical).
     const auto a16 = [](const void *x) { return (reinterpret_cast<uintptr_t>(x) & 15u) == 0; };
     const FlashPlan raw_plan = flash_plan(int64_t(B) * H, S_q, S_kv, D,
                                           mode == kAttnF32X3 ? kTileUsX3 : kTileUsF32);
