@@ -27,7 +27,11 @@
 //     t run;
 //   * one barrier per chunk, after its last K step's MFMAs are issued: by
 //     then every wave has read all of the chunk, so its stage takes the
-//     chunk after next while those MFMAs run;
+//     chunk after next while those MFMAs run.  The waves copying A rows
+//     issue those copies right after the barrier, the waves copying W rows
+//     after the next chunk's first K step, so the two waves of a SIMD do not
+//     stall at copy issue together (8192 x 2048 x 8192 with two terms:
+//     428 -> 411 us);
 //   * workgroups in XCD-major order with the N tiles of one M tile
 //     consecutive: the workgroups of one XCD share W chunks and A chunks
 //     through its L2.
@@ -154,10 +158,12 @@ __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs 
             for (int nb = 0; nb < 2; ++nb)
                 acc[b % MB][nb] = mfma_bf16(af[set][b], wf[set][nb], acc[b % MB][nb]);
     };
+    // Waves 0-3 (A rows) issue chunk c + 2's copies right after the barrier
+    // that frees its stage, waves 4-7 (W rows) after the next chunk's first
+    // K step, so the two waves of a SIMD do not stall at copy issue together.
+    const bool late_copies = !copies_a;
     for (int c = 0; c < total; ++c) {
         const u16 *st = smem + (c & 1) * kLgStage;
-        // Steps 0..2: the 6 fragment reads of step j + 1 interleaved with the
-        // 8 MFMAs of step j, so each read has a step's MFMAs to land.
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
             frags(st, j + 1, af[(j + 1) & 1], wf[(j + 1) & 1]);
@@ -168,18 +174,18 @@ __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs 
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
             }
             __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            if (j == 0 && late_copies && c >= 1 && c + 1 < total) {
+                __builtin_amdgcn_sched_barrier(0);
+                dma(c + 1, (c + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-        // Step 3's MFMAs go out before the barrier and run while the wave
-        // waits there.  Then chunk c + 1's copies (the only ones in flight)
-        // have landed for every wave, and every wave holds its last fragments
-        // of chunk c: its stage takes chunk c + 2, and chunk c + 1's first
-        // fragments load.
         mfmas(1);
         __builtin_amdgcn_sched_barrier(0);
         if (c + 1 < total) {
             wait_vmcnt<0>();
             ring_barrier();
-            if (c + 2 < total)
+            if (c + 2 < total && !late_copies)
                 dma(c + 2, c & 1);
             frags(smem + ((c + 1) & 1) * kLgStage, 0, af[0], wf[0]);
         }
