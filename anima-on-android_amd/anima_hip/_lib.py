@@ -41,6 +41,8 @@ SIGNATURES = {
                                      + [_F, _B, _P]),
     "anima_hip_flash_x3_rawq_dev": (_B, [_P] * 3 + [_F] + [_P] * 3 + [_I] * 5 + [_I64P] * 4
                                     + [_F, _B, _P]),
+    "anima_hip_flash_bf16_rawq_dev": (_B, [_P] * 3 + [_F] + [_P] * 3 + [_I] * 5 + [_I64P] * 4
+                                      + [_F, _B, _P]),
     "anima_hip_pack_vt_terms_dev": (_B, [_P, _P] + [_I] * 4 + [_I64P] * 2 + [_P]),
     "anima_hip_vt_padded_len": (ct.c_int64, [_I]),
     "anima_hip_pack_vt_dev": (_B, [_P, _P] + [_I] * 4 + [_I64P] * 2 + [_P]),

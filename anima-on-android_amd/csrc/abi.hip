@@ -1321,6 +1321,45 @@ bool anima_hip_flash_x3_rawq_dev(const float *q, const float *q_norm_w, const fl
     return launch_flash_x3(p, pick_stream(stream));
 }
 
+bool anima_hip_flash_bf16_rawq_dev(const float *q, const float *q_norm_w, const float *freqs,
+                                   float eps, const uint16_t *k, const uint16_t *vt, float *o,
+                                   int B, int H, int S_q, int S_kv, int D,
+                                   const int64_t *q_strides, const int64_t *k_strides,
+                                   const int64_t *vt_strides, const int64_t *o_strides,
+                                   float scale, bool is_causal, void *stream)
+{
+    if (!(scale > 0.0f) || !std::isfinite(scale))
+        return fail("flash_bf16_rawq_dev: scale must be positive and finite");
+    if (!ready_for_device_call() || !check_dims(B, H, S_q, S_kv, D))
+        return false;
+    if (int64_t(B) * H * S_q * D > 0 && (!q || !o || (S_kv > 0 && (!k || !vt))))
+        return fail("flash_bf16_rawq_dev: null pointer");
+    const int64_t sp = vt_padded_len(S_kv);
+    FlashProblem p;
+    p.q = nullptr;
+    p.k = k;
+    p.v = vt;
+    p.o = o;
+    p.qs = Strides{0, 0, 0};
+    p.ks = from_array(k_strides, H, S_kv, D);
+    p.vs = vt_strides ? Strides{vt_strides[0], vt_strides[1], vt_strides[2]}
+                      : Strides{int64_t(H) * D * sp, int64_t(D) * sp, sp};
+    p.os = from_array(o_strides, H, S_q, D);
+    p.rq.x = q;
+    p.rq.s = from_array(q_strides, H, S_q, D);
+    p.rq.w = q_norm_w;
+    p.rq.freqs = freqs;
+    p.rq.eps = eps;
+    p.B = B;
+    p.H = H;
+    p.S_q = S_q;
+    p.S_kv = S_kv;
+    p.D = D;
+    p.scale = scale;
+    p.causal = is_causal;
+    return launch_flash_bf16(p, pick_stream(stream));
+}
+
 bool anima_hip_pack_vt_terms_dev(const float *v, uint16_t *vt, int B, int H, int S_kv, int D,
                                  const int64_t *v_strides, const int64_t *vt_strides,
                                  void *stream)

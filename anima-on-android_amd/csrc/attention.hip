@@ -210,16 +210,19 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     // workgroup's start cost more than the pass.
     // The f32 kernel, which reads Q as f32 rows anyway, does the same (RMSNorm
     // only: its rows carry no terms; 4096 x 512: 307.5 -> 286.5 us).  The
-    // bf16 kernel keeps the row pass: with raw rows it reads twice the Q
-    // bytes at each workgroup's start, and the call measured the same
-    // (4096 x 512, B = 2: 65.7 against 65.9 us, bit-identical).
+    // bf16 kernel does it where it runs two 4-wave workgroups per CU (short
+    // key ranges, flash_bf16_raw_q): there the doubled Q read at a
+    // workgroup's start overlaps the other workgroup's tiles.  With one
+    // 8-wave workgroup per CU it measured the same as the row pass (4096 x
+    // 512, B = 2: 65.7 against 65.9 us, bit-identical).
     const auto a16 = [](const void *x) { return (reinterpret_cast<uintptr_t>(x) & 15u) == 0; };
     const FlashPlan raw_plan = flash_plan(int64_t(B) * H, S_q, S_kv, D,
                                           mode == kAttnF32X3 ? kTileUsX3 : kTileUsF32);
-    const bool raw_q = prepared && !in.freqs && (mode == kAttnF32X3 || mode == kAttnF32) &&
-                       D == 128 && a16(in.q) && ld_q % 4 == 0 &&
-                       (!in.q_norm_w || a16(in.q_norm_w)) && raw_plan.waves == 8 &&
-                       raw_plan.splits == 1;
+    const bool raw_kernel =
+        mode == kAttnBF16 ? flash_bf16_raw_q(int64_t(B) * H, S_q, S_kv)
+                          : raw_plan.waves == 8 && raw_plan.splits == 1;
+    const bool raw_q = prepared && !in.freqs && D == 128 && a16(in.q) && ld_q % 4 == 0 &&
+                       (!in.q_norm_w || a16(in.q_norm_w)) && raw_kernel;
 
     // Q rows, and K rows unless prepared, in one launch.
     const RowProblem pq =

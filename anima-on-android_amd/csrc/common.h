@@ -57,7 +57,7 @@ struct FlashProblem {
     float scale;       // softmax scale applied to q.k
     bool causal;       // mask key j > query i (top-left aligned, like anima_rt)
     TermOut ot;        // bf16 term output in place of o
-    RawQ rq;           // f32x3 kernel only: q given as raw projection rows
+    RawQ rq;           // f32x3, f32 and bf16 kernels: q given as raw projection rows
 };
 bool term_out_ok(const TermOut &t);  // alignment of a set term output
 
@@ -117,6 +117,11 @@ bool flash_f32_fast_path(const FlashProblem &p);
 // strides (the d-row stride is vt_padded_len(S_kv)).
 bool launch_flash_bf16(const FlashProblem &p, hipStream_t st, void *part = nullptr,
                        size_t part_bytes = 0);
+// True when launch_flash_bf16 runs this shape as two 4-wave workgroups per CU
+// (large grids over short key ranges), where the kernel also takes raw query
+// rows (FlashProblem::rq) at no cost: their larger load overlaps the other
+// workgroup's tiles.
+bool flash_bf16_raw_q(int64_t BH, int S_q, int S_kv);
 
 // V^T layout of the bf16 path: per (batch, head) a [D][Sp] bf16 matrix with
 // Sp = vt_padded_len(S_kv), zero beyond S_kv, and within every group of 16

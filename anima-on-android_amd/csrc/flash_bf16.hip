@@ -27,7 +27,7 @@
 //     running max m is updated lazily (only when a tile max exceeds it by
 //     more than 8 in log2 units), so the O rescale is usually skipped.
 // Also here: the V -> packed V^T conversion kernel of this path.
-#include "flash_tile.h"
+#include "qrow.h"
 
 #include <cmath>
 
@@ -36,8 +36,13 @@ namespace {
 
 using namespace flash_tile;
 
-constexpr int kStages = 3;           // depth of the K and V^T LDS rings
 constexpr int kTileElems = kBN * kD;  // bf16 per K or V^T tile (16 KiB)
+// Short key ranges (cross-attention over a 512-token context: 8 tiles per
+// workgroup) on grids of at least one 8-wave workgroup per CU run as 4-wave
+// workgroups with two-stage rings (64 KiB of LDS, at most 256 VGPRs), two
+// per CU: one workgroup's query load and output stores, which a workgroup of
+// 8 tiles cannot hide behind its own MFMA work, overlap the other's tiles.
+constexpr int kPairMaxTiles = 16;
 
 struct Bf16Args {
     const u16 *q, *k, *vt;
@@ -49,20 +54,28 @@ struct Bf16Args {
     int dma32;  // K/V^T tile rows fit 32-bit byte offsets from the tile start
     FlashSplitArgs split;  // n == 1: write O; n > 1: write this split's partial
     TermOut ot;            // n == 1 and ot.t set: O as bf16 terms
+    // Raw query rows (RawQ) in place of q's bf16 rows when qx is set.
+    const float *qx, *qw, *qf;
+    int64_t rqb, rqh, rqs;
+    float eps;
 };
 
-template <int NW>
-__global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
+// NW waves x 32 query rows per workgroup, K/V^T rings of ST stages.  The
+// two-stage form is held to two waves per SIMD (256 VGPRs), so that two
+// 4-wave workgroups share a CU.
+template <int NW, int ST>
+__global__ __launch_bounds__(NW * 64, ST == 2 ? 2 : 1) void flash_bf16_d128(Bf16Args a)
 {
     constexpr int NT = NW * 64;
     constexpr int BM = NW * 32;
     constexpr int DMA = kTileElems / 8 / NT;  // 16-byte copies per thread per tile
     static_assert(kTileElems / 8 % NT == 0, "tiles must split evenly");
+    static_assert(ST == 2 || ST == 3, "two- or three-stage rings");
 
     // K ring, then V^T ring, in one array: the epilogue reuses it whole.
-    __shared__ __attribute__((aligned(16))) u16 smem[2 * kStages * kTileElems];
+    __shared__ __attribute__((aligned(16))) u16 smem[2 * ST * kTileElems];
     u16 (*const Ks)[kTileElems] = reinterpret_cast<u16 (*)[kTileElems]>(smem);
-    u16 (*const Vs)[kTileElems] = reinterpret_cast<u16 (*)[kTileElems]>(smem + kStages * kTileElems);
+    u16 (*const Vs)[kTileElems] = reinterpret_cast<u16 (*)[kTileElems]>(smem + ST * kTileElems);
     static_assert(NW * kOWaveFloats * 4 <= int(sizeof(smem)), "O staging fits the rings");
 
     const int tid = threadIdx.x;
@@ -86,20 +99,22 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
 
     // Q fragment: Q[qrow][64*half + 8t .. +7], t = 0..7.
     bf16x8 qf[8];
-    if (qrow < a.S_q) {
-        const bf16x8 *src = reinterpret_cast<const bf16x8 *>(qp + qrow * a.qs + 64 * half);
+    if (!a.qx) {
+        if (qrow < a.S_q) {
+            const bf16x8 *src = reinterpret_cast<const bf16x8 *>(qp + qrow * a.qs + 64 * half);
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-            qf[t] = src[t];
-    } else {
+            for (int t = 0; t < 8; ++t)
+                qf[t] = src[t];
+        } else {
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-            qf[t] = bf16x8{};
+            for (int t = 0; t < 8; ++t)
+                qf[t] = bf16x8{};
+        }
+        // Retire the Q loads here.  Otherwise the compiler still counts them
+        // as outstanding inside the tile loop and waits for vmcnt(0) before
+        // the first MFMAs, which also waits for the next tile's prefetch.
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
     }
-    // Retire the Q loads here.  Otherwise the compiler still counts them as
-    // outstanding inside the tile loop and waits for vmcnt(0) before the
-    // first MFMAs, which also waits for the next tile's prefetch.
-    __builtin_amdgcn_s_waitcnt(kVmcnt0);
 
     int kv_end = a.S_kv;
     if (a.causal)
@@ -108,10 +123,11 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     const int j0 = sp * a.split.tiles;
     const int ntiles = max(0, min((kv_end + kBN - 1) / kBN - j0, a.split.tiles));
 
-    // K and V^T tiles reach LDS by DMA through rings of kStages buffers:
-    // tile t lives in stage t % 3.  Iteration j reads K(j+1) (scores of the
-    // next tile) and V^T(j) (P.V of this tile) and starts the copies of
-    // K(j+3) and V^T(j+2), which have two iterations to land.
+    // K and V^T tiles reach LDS by DMA through rings of ST buffers: tile t
+    // lives in stage t % ST.  Iteration j reads K(j+1) (scores of the next
+    // tile) and V^T(j) (P.V of this tile) and starts the copies of K(j+ST) and
+    // V^T(j+ST-1): with three stages they have two iterations to land, with
+    // two stages one.
     // Layouts, unpadded, XOR-swizzled so every 16-lane group of a fragment
     // read hits distinct banks:
     //   K   [64 keys][128 d]: 16-byte chunk c of key row r at chunk c ^ (r & 15);
@@ -197,14 +213,25 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
             dma_k(1, 1);
         dma_v(0, 0);
     }
+    // Raw query rows are prepared while the first tiles' copies are in
+    // flight.
+    if (a.qx) {
+        const int r = min(qrow, a.S_q - 1);
+        bf16x8 unused[8];
+        q_terms_from_raw<false>(a.qx + b * a.rqb + h * a.rqh + int64_t(r) * a.rqs, a.qw,
+                                a.qf ? a.qf + int64_t(r) * 4 * kD / 2 : nullptr, a.eps,
+                                qrow < a.S_q, half, qf, unused);
+    }
     wait_vmcnt<0>();
     ring_barrier();
     if (ntiles > 0)
         scores(0, sa0, sa1);
-    if (ntiles > 2)
-        dma_k(2, 2);
-    if (ntiles > 1)
-        dma_v(1, 1);
+    if (ST == 3) {
+        if (ntiles > 2)
+            dma_k(2, 2);
+        if (ntiles > 1)
+            dma_v(1, 1);
+    }
     ring_barrier();  // K stage 0 is rewritten in the first iteration
 
     // Raw-score tile max over a lane's 32 scores, combined across the two
@@ -225,12 +252,12 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
     // Tile j: consumes the scores sc0/sc1 of tile j, produces sn0/sn1 of
     // tile j+1.
     auto tile = [&](const int j, f32x16 &sc0, f32x16 &sc1, f32x16 &sn0, f32x16 &sn1) {
-        const int sv = j % kStages, sk = (j + 1) % kStages;  // stages of V^T(j), K(j+1)
-        const bool dk = j + 3 < ntiles, dv = j + 2 < ntiles;
+        const int sv = j % ST, sk = (j + 1) % ST;  // stages of V^T(j), K(j+1)
+        const bool dk = j + ST < ntiles, dv = j + ST - 1 < ntiles;
         if (dk)
-            dma_k(j + 3, sv);
+            dma_k(j + ST, sv);
         if (dv)
-            dma_v(j + 2, (j + 2) % kStages);
+            dma_v(j + ST - 1, (j + ST - 1) % ST);
 
         float mx = mx_next;
         const int key0 = (j0 + j) * kBN;
@@ -341,9 +368,11 @@ __global__ __launch_bounds__(NW * 64, 1) void flash_bf16_d128(Bf16Args a)
         __builtin_amdgcn_s_setprio(0);
         mx_next = row_pair_max(fmaxf(a0, a1));
 
-        // K(j+2) and V^T(j+1) were started one iteration ago: wait until only
-        // this iteration's copies are outstanding, then let every wave see them.
-        const int inflight = DMA * (int(dk) + int(dv));
+        // The next iteration reads K(j+2) and V^T(j+1).  With three stages
+        // they were started one iteration ago: wait until only this
+        // iteration's copies are outstanding.  With two stages they are this
+        // iteration's: wait for all.  Then let every wave see them.
+        const int inflight = ST == 3 ? DMA * (int(dk) + int(dv)) : 0;
         if (inflight == 2 * DMA)
             wait_vmcnt<2 * DMA>();
         else if (inflight == DMA)
@@ -433,7 +462,7 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(PackArgs a)
     }
 }
 
-template <int NW>
+template <int NW, int ST>
 bool launch_d128(const Bf16Args &a, int64_t BH, hipStream_t st)
 {
     constexpr int BM = NW * 32;
@@ -442,11 +471,23 @@ bool launch_d128(const Bf16Args &a, int64_t BH, hipStream_t st)
     const int64_t nblk = BH * g.n_qtiles * g.split.n;
     if (nblk > INT32_MAX)
         return fail("flash_bf16: problem too large for one launch");
-    hipLaunchKernelGGL(flash_bf16_d128<NW>, dim3(unsigned(nblk)), dim3(NW * 64), 0, st, g);
+    hipLaunchKernelGGL((flash_bf16_d128<NW, ST>), dim3(unsigned(nblk)), dim3(NW * 64), 0, st, g);
     return hip_ok(hipGetLastError(), "flash_bf16_d128 launch");
 }
 
+// Two 4-wave workgroups per CU with two-stage rings: large unsplit grids over
+// at most kPairMaxTiles key tiles.
+bool paired_plan(const FlashPlan &pl, int S_kv)
+{
+    return pl.waves == 8 && pl.splits == 1 && (S_kv + kBN - 1) / kBN <= kPairMaxTiles;
+}
+
 }  // namespace
+
+bool flash_bf16_raw_q(int64_t BH, int S_q, int S_kv)
+{
+    return paired_plan(flash_plan(BH, S_q, S_kv, kD, kTileUsBF16), S_kv);
+}
 
 bool launch_flash_bf16(const FlashProblem &p, hipStream_t st, void *part, size_t part_bytes)
 {
@@ -461,9 +502,16 @@ bool launch_flash_bf16(const FlashProblem &p, hipStream_t st, void *part, size_t
     if (p.vs.s != sp)
         return fail("flash_bf16: V^T row stride must equal the padded key count");
     const auto s8 = [](const Strides &x) { return x.b % 8 == 0 && x.h % 8 == 0 && x.s % 8 == 0; };
-    if (!aligned(p.q, 16) || !aligned(p.k, 16) || !aligned(p.v, 16) || !aligned(p.o, 16) ||
-        !s8(p.qs) || !s8(p.ks) || !s8(p.vs) || p.os.b % 4 || p.os.h % 4 || p.os.s % 4)
+    const bool raw_q = p.rq.x != nullptr;  // q's bf16 rows unused
+    if ((!raw_q && (!aligned(p.q, 16) || !s8(p.qs))) || !aligned(p.k, 16) || !aligned(p.v, 16) ||
+        !aligned(p.o, 16) || !s8(p.ks) || !s8(p.vs) || p.os.b % 4 || p.os.h % 4 || p.os.s % 4)
         return fail("flash_bf16: operands must be 16-byte aligned with 16-byte row strides");
+    if (raw_q) {
+        const Strides &x = p.rq.s;
+        if (!aligned(p.rq.x, 16) || x.b % 4 || x.h % 4 || x.s % 4 ||
+            (p.rq.w && !aligned(p.rq.w, 16)) || (p.rq.freqs && !aligned(p.rq.freqs, 16)))
+            return fail("flash_bf16: raw query rows must be 16-byte aligned with 16-byte strides");
+    }
     if (p.ot.t && !term_out_ok(p.ot))
         return fail("flash_bf16: term output must be 16-byte aligned with strides of 8 elements");
     Bf16Args a;
@@ -485,9 +533,17 @@ bool launch_flash_bf16(const FlashProblem &p, hipStream_t st, void *part, size_t
     // r*ks, V^T d-rows r < 128 at r*Sp, plus 256 bytes.
     a.dma32 = (int64_t(kBN) * p.ks.s * 2 + 256 < (int64_t(1) << 31)) &&
               (int64_t(kD) * sp * 2 + 256 < (int64_t(1) << 31));
+    a.qx = p.rq.x;
+    a.qw = p.rq.w;
+    a.qf = p.rq.freqs;
+    a.rqb = p.rq.s.b; a.rqh = p.rq.s.h; a.rqs = p.rq.s.s;
+    a.eps = p.rq.eps;
     const FlashPlan pl = flash_plan(BH, p.S_q, p.S_kv, p.D, kTileUsBF16);
     a.split = flash_split_args(pl, BH, p.S_q, part, part_bytes);
-    if (!(pl.waves == 4 ? launch_d128<4>(a, BH, st) : launch_d128<8>(a, BH, st)))
+    const bool ok = paired_plan(pl, p.S_kv) ? launch_d128<4, 2>(a, BH, st)
+                    : pl.waves == 4        ? launch_d128<4, 3>(a, BH, st)
+                                           : launch_d128<8, 3>(a, BH, st);
+    if (!ok)
         return false;
     return a.split.n == 1 || launch_flash_combine(p, a.split, st);
 }

@@ -202,6 +202,22 @@ bool anima_hip_flash_x3_rawq_dev(const float *q, const float *q_norm_w, const fl
                                  const int64_t *vt_strides, const int64_t *o_strides,
                                  float scale, bool is_causal, void *stream);
 
+/* anima_hip_flash_bf16_dev with q given as raw f32 projection rows
+ * ([B,S_q,H,D] through q_strides, NULL = contiguous; 16-byte aligned rows):
+ * the kernel applies the per-head RMSNorm (q_norm_w may be NULL) and the RoPE
+ * of freqs ([S_q, D/2, 2, 2] or NULL) and rounds the rows to bf16 itself,
+ * bit-identical to anima_hip_qk_prologue_dev (flags 1 | 2) followed by
+ * anima_hip_flash_bf16_dev.  NumpyAttention.forward's q path
+ * (anima_rt/scripts/numpy_dit.py:285-291) and its attention in one launch;
+ * the bf16 cross-attention entries use it where the kernel runs two 4-wave
+ * workgroups per CU (large grids over at most 1024 keys). */
+bool anima_hip_flash_bf16_rawq_dev(const float *q, const float *q_norm_w, const float *freqs,
+                                   float eps, const uint16_t *k, const uint16_t *vt, float *o,
+                                   int B, int H, int S_q, int S_kv, int D,
+                                   const int64_t *q_strides, const int64_t *k_strides,
+                                   const int64_t *vt_strides, const int64_t *o_strides,
+                                   float scale, bool is_causal, void *stream);
+
 /* Pack f32 V into the term V^T layout of anima_hip_flash_x3_dev: per (batch,
  * head) the [D][anima_hip_vt_padded_len(S_kv)] hi matrix of
  * anima_hip_pack_vt_dev's layout followed by the same matrix of lo terms

@@ -181,3 +181,98 @@ def test_f32_rawq_matches_prologue_then_flash(B, S_q, S_kv, H, fused, weights, c
     out = o_raw.get((B, S_q, H, D))
     assert np.isfinite(ref[0, 1]).all()
     assert np.array_equal(_bits(out), _bits(ref))
+
+
+BF16_CASES = [  # B, S_q, S_kv, H, grid (None: no RoPE), fused projection layout, weights, causal
+    (2, 4096, 512, 16, None, False, True, False),     # two 4-wave workgroups per CU
+    (2, 4096, 700, 16, None, True, True, False),      # the same with a ragged key tile
+    (2, 4096, 4096, 16, (64, 64), False, True, False),  # 8-wave grid, RoPE
+    (1, 520, 100, 4, None, True, False, True),        # 4-wave grid, causal
+    (2, 77, 77, 3, (7, 11), True, True, False),
+]
+
+
+@pytest.mark.parametrize("B,S_q,S_kv,H,grid,fused,weights,causal", BF16_CASES)
+def test_bf16_rawq_matches_prologue_then_flash(B, S_q, S_kv, H, grid, fused, weights, causal):
+    """anima_hip_flash_bf16_rawq_dev (q RMSNorm, RoPE and bf16 rounding
+    inside the bf16 kernel) against anima_hip_qk_prologue_dev (flags 1 | 2,
+    bf16 rows) + anima_hip_flash_bf16_dev, bit for bit; one row carries a NaN
+    and one an infinity."""
+    lib = _lib.load()
+    rng = np.random.default_rng(B * 15485863 + S_q * 13 + S_kv + H)
+    print(f"bf16 rawq case B={B} S_q={S_q} S_kv={S_kv} H={H} grid={grid} fused={fused} "
+          f"weights={weights} causal={causal}", flush=True)
+    ld = 3 * H * D if fused else H * D
+    qraw = rng.standard_normal((B, S_q, ld), dtype=np.float32)
+    qraw[0, S_q // 3, :D] *= 40.0
+    qraw[B - 1, S_q // 2, 5] = np.nan
+    qraw[0, S_q - 1, D + 7 if H > 1 else 7] = np.inf
+    qb = DevBuf.of(qraw)
+    k = DevBuf.of(rng.standard_normal((B, S_kv, H, D), dtype=np.float32))
+    v = DevBuf.of(rng.standard_normal((B, S_kv, H, D), dtype=np.float32))
+    wq = DevBuf.of(rng.uniform(0.5, 1.5, D).astype(np.float32)) if weights else None
+    wk = DevBuf.of(rng.uniform(0.5, 1.5, D).astype(np.float32)) if weights else None
+    fr = DevBuf.of(generate_rope_freqs(*grid)) if grid else None
+    eps = ct.c_float(1e-6)
+    scale = ct.c_float(1.0 / math.sqrt(D))
+    sp = lib.anima_hip_vt_padded_len(S_kv)
+    qx_s = _lib.strides([S_q * ld, D, ld])
+    qs = _lib.strides([S_q * H * D, D, H * D])
+    kvs = _lib.strides([S_kv * H * D, D, H * D])
+    qn, kn = DevBuf(B * S_q * H * D * 2), DevBuf(B * S_kv * H * D * 2)
+    vt = DevBuf(B * H * D * sp * 2)
+    _lib.check(lib.anima_hip_qk_prologue_dev(qb.addr, qn.addr, _ptr(wq), _ptr(fr), B, S_q, H, D,
+                                             qx_s, qs, eps, 1 | 2, None), "q prologue")
+    _lib.check(lib.anima_hip_qk_prologue_dev(k.addr, kn.addr, _ptr(wk),
+                                             _ptr(fr) if S_q == S_kv else None, B, S_kv, H, D,
+                                             kvs, kvs, eps, 1 | 2, None), "k prologue")
+    _lib.check(lib.anima_hip_pack_vt_dev(v.addr, vt.addr, B, H, S_kv, D, kvs, None, None), "pack")
+    o_ref, o_raw = DevBuf(B * S_q * H * D * 4), DevBuf(B * S_q * H * D * 4)
+    _lib.check(lib.anima_hip_flash_bf16_dev(qn.addr, kn.addr, vt.addr, o_ref.addr, B, H, S_q,
+                                            S_kv, D, qs, kvs, None, qs, scale, causal, None),
+               "flash_bf16_dev")
+    _lib.check(lib.anima_hip_flash_bf16_rawq_dev(qb.addr, _ptr(wq), _ptr(fr), eps, kn.addr,
+                                                 vt.addr, o_raw.addr, B, H, S_q, S_kv, D, qx_s,
+                                                 kvs, None, qs, scale, causal, None),
+               "flash_bf16_rawq_dev")
+    ref = o_ref.get((B, S_q, H, D))
+    out = o_raw.get((B, S_q, H, D))
+    assert np.isfinite(ref[0, 1]).all()
+    assert np.array_equal(_bits(out), _bits(ref))
+
+
+def test_bf16_paired_workgroups_equal_three_stage_rings():
+    """The 4096 x 512 cross-attention shape (B=2, H=16) runs as two 4-wave
+    workgroups per CU with two-stage K/V rings; each (batch, head) called on
+    its own is a small grid that runs 4-wave workgroups with three-stage
+    rings.  Every query row's arithmetic is the same, so the outputs agree
+    bit for bit."""
+    lib = _lib.load()
+    rng = np.random.default_rng(2718)
+    B, S_q, S_kv, H = 2, 4096, 512, 16
+    q = rng.standard_normal((B, S_q, H, D), dtype=np.float32)
+    k = rng.standard_normal((B, S_kv, H, D), dtype=np.float32)
+    v = rng.standard_normal((B, S_kv, H, D), dtype=np.float32)
+    bits16 = lambda x: ((x.view(np.uint32).astype(np.uint64) + 0x7FFF +
+                         ((x.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    qd, kd = DevBuf.of(bits16(q)), DevBuf.of(bits16(k))
+    sp = lib.anima_hip_vt_padded_len(S_kv)
+    vd, vt = DevBuf.of(v), DevBuf(B * H * D * sp * 2)
+    kvs = _lib.strides([S_kv * H * D, D, H * D])
+    qs = _lib.strides([S_q * H * D, D, H * D])
+    _lib.check(lib.anima_hip_pack_vt_dev(vd.addr, vt.addr, B, H, S_kv, D, kvs, None, None), "pack")
+    scale = ct.c_float(1.0 / math.sqrt(D))
+    o_all, o_one = DevBuf(B * S_q * H * D * 4), DevBuf(B * S_q * H * D * 4)
+    _lib.check(lib.anima_hip_flash_bf16_dev(qd.addr, kd.addr, vt.addr, o_all.addr, B, H, S_q,
+                                            S_kv, D, qs, kvs, None, qs, scale, False, None),
+               "flash all heads")
+    vts = _lib.strides([H * D * sp, D * sp, sp])
+    for b in range(B):
+        for h in range(H):
+            off = (b * S_q * H + h) * D  # element offset of (b, 0, h, 0)
+            koff = (b * S_kv * H + h) * D
+            _lib.check(lib.anima_hip_flash_bf16_dev(
+                qd.addr + 2 * off, kd.addr + 2 * koff, vt.addr + 2 * (b * H + h) * D * sp,
+                o_one.addr + 4 * off, 1, 1, S_q, S_kv, D, qs, kvs, vts, qs, scale, False, None),
+                "flash one head")
+    assert np.array_equal(_bits(o_all.get((B, S_q, H, D))), _bits(o_one.get((B, S_q, H, D))))
