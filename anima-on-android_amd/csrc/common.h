@@ -187,6 +187,13 @@ bool gemm_large_supported(int M, int N, int K, int terms, int64_t lda, int64_t l
 bool launch_gemm_large(const uint16_t *a0, const uint16_t *a1, int64_t lda, const uint16_t *w,
                        int64_t ldw, void *c, int64_t ldc, int M, int N, int K, int epilogue,
                        const float *gate, int64_t gate_stride, int S, hipStream_t st);
+// The two-term product on f32 activations a [M][lda] (lda % 4 == 0): the
+// kernel splits a into hi = bf16(a), lo = bf16(a - hi) itself, so C (f32) is
+// bit-identical to the split pass plus launch_gemm_large with both terms.
+bool gemm_large_f32a_supported(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
+                               const float *a, const void *w, const void *c);
+bool launch_gemm_large_f32a(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *c,
+                            int64_t ldc, int M, int N, int K, hipStream_t st);
 
 // Small-M bf16 GEMM (gemm_bf16.hip): C[M,N] = a0 . W^T (+ a1 . W^T) with bf16
 // activation terms a0 (a1 null for one term) [M][lda], bf16 W [N][ldw], f32

@@ -37,6 +37,14 @@
 //     through its L2.
 // Epilogues: C as f32 (plain store), C as bf16 (round to nearest even), or
 // x[m][n] += gate[m / S][n] * C[m][n] (the gated residual of a DiT block).
+//
+// f32 activations (F32A): the two-term tile stages the 128 f32 rows of A
+// themselves (256 bytes per row and chunk, the bytes of the hi and lo rows
+// together, 16-byte pieces XOR-swizzled by row & 15) and every wave splits
+// its fragments into hi = bf16(a) and lo = bf16(a - hi) in registers, the
+// split pass's arithmetic (linear.hip), so C is bit-identical to the split
+// pass followed by the two-term product and the pass's HBM round trip of the
+// terms is gone.
 #include "flash_tile.h"
 #include "rowmath.h"
 
@@ -58,6 +66,7 @@ constexpr int kLgF32 = kGemmOutF32, kLgBf16 = kGemmOutBf16, kLgResidual = kGemmO
 
 struct LargeArgs {
     const u16 *a0, *a1;  // activation terms [M][lda]; a1 null for one term
+    const float *af;     // F32A: f32 activations [M][lda] (a0, a1 unused)
     const u16 *w;        // [N][ldw]
     void *c;             // f32 or bf16 [M][ldc]; the residual x for kLgResidual
     const float *gate;   // kLgResidual: gate[b * gate_stride + n], b = m / S
@@ -68,11 +77,17 @@ struct LargeArgs {
 
 __device__ __forceinline__ int lg_swizzle(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-template <int TERMS, int EPI>
+template <int TERMS, int EPI, bool F32A>
 __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs g)
 {
+    static_assert(!F32A || TERMS == 2, "f32 activations take the two-term tile");
     constexpr int BM = kLgRows / TERMS;        // rows of C per tile
-    constexpr int MB = 4 / TERMS;              // 32-row accumulator blocks per wave
+    // Waves as WM x WN over the tile: 2 x 4 (a wave owns BM / 2 rows of C and
+    // 64 columns), or with F32A 4 x 2 (32 rows, 128 columns), so that each
+    // row block of A is split in registers by two waves instead of four.
+    constexpr int WM = F32A ? 4 : 2, WN = kLgWaves / WM;
+    constexpr int MB = F32A ? 1 : 4 / TERMS;   // 32-row accumulator blocks per wave
+    constexpr int NB = kLgBN / WN / 32;        // 32-column accumulator blocks per wave
     constexpr int A_EL = kLgRows * kLgBK;      // A part of a stage
     __shared__ __attribute__((aligned(16))) u16 smem[2 * kLgStage];
 
@@ -80,7 +95,7 @@ __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs 
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 31, half = lane >> 5;
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wm = wave % WM, wn = wave / WM;
 
     const int blk = xcd_major_block();
     const int tn = blk % g.tiles_n, tm = blk / g.tiles_n;
@@ -88,17 +103,24 @@ __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs 
 
     // Copies: window i of wave w is window 8w + i of the stage (8 rows of one
     // operand): windows 0..31 hold the A rows (term-major: term t's BM rows
-    // at staged rows t * BM ..), 32..63 the W rows.  Waves 0-3 copy A, 4-7
-    // copy W, so a wave's source operand and term are uniform.  Rows past M
-    // or N re-read the last row (their results are not stored).  Byte
-    // offsets from the operand's tile row at the chunk's first column.
+    // at staged rows t * BM ..; F32A: 4 f32 rows of 256 bytes per window),
+    // 32..63 the W rows.  Waves 0-3 copy A, 4-7 copy W, so a wave's source
+    // operand and term are uniform.  Rows past M or N re-read the last row
+    // (their results are not stored).  Byte offsets from the operand's tile
+    // row at the chunk's first column.
     const bool copies_a = wave < 4;
-    const int term = copies_a ? (wave * kLgCopies * 8) / BM : 0;
+    const int term = copies_a && !F32A ? (wave * kLgCopies * 8) / BM : 0;
     unsigned off_b[kLgCopies];
 #pragma unroll
     for (int i = 0; i < kLgCopies; ++i) {
         const int win = (wave & 3) * kLgCopies + i;  // window within the operand
         const int f = win * 64 + lane;
+        if (F32A && copies_a) {
+            const int r = f >> 4, lc = (f & 15) ^ (r & 15);
+            const int rr = min(row0 + r, g.M - 1) - row0;
+            off_b[i] = unsigned(int64_t(rr) * g.lda * 4 + 16 * lc);
+            continue;
+        }
         const int r = f >> 3, lc = (f & 7) ^ lg_swizzle(r);
         int rr;
         if (copies_a)
@@ -107,11 +129,14 @@ __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs 
             rr = min(col0 + r, g.N - 1) - col0;
         off_b[i] = unsigned(int64_t(rr) * (copies_a ? g.lda : g.ldw) * 2 + 16 * lc);
     }
-    const u16 *src0 = copies_a ? (term ? g.a1 : g.a0) + int64_t(row0) * g.lda
-                               : g.w + int64_t(col0) * g.ldw;
+    const char *src0 =
+        F32A && copies_a ? reinterpret_cast<const char *>(g.af + int64_t(row0) * g.lda)
+        : copies_a       ? reinterpret_cast<const char *>((term ? g.a1 : g.a0) + int64_t(row0) * g.lda)
+                         : reinterpret_cast<const char *>(g.w + int64_t(col0) * g.ldw);
+    const int64_t chunk_bytes = int64_t(kLgBK) * (F32A && copies_a ? 4 : 2);
     u16 *dst0 = smem + (copies_a ? 0 : A_EL) + (wave & 3) * kLgCopies * 512;
     auto dma = [&](int c, int stage) {
-        const u16 *src = src0 + int64_t(c) * kLgBK;
+        const char *src = src0 + int64_t(c) * chunk_bytes;
 #pragma unroll
         for (int i = 0; i < kLgCopies; ++i)
             dma16s(src, off_b[i], dst0 + stage * kLgStage + i * 512);
@@ -121,13 +146,30 @@ __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs 
     // wm * 128 + 32 b for one term; term b / 2, rows wm * 64 + 32 (b % 2) for
     // two), W blocks nb (rows wn * 64 + 32 nb), piece 2t + half of row col.
     const int sw = lg_swizzle(col);
-    auto frags = [&](const u16 *st, int t, bf16x8 (&af)[4], bf16x8 (&wf)[2]) {
+    auto frags = [&](const u16 *st, int t, bf16x8 (&af)[4], bf16x8 (&wf)[NB]) {
         const int pc = ((2 * t + half) ^ sw) * 8;
         // W first: the step's first MFMA takes W block 0 and A block 0.
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-            wf[nb] = *reinterpret_cast<const bf16x8 *>(st + A_EL + (wn * 64 + 32 * nb + col) *
-                                                                       kLgBK + pc);
+        for (int nb = 0; nb < NB; ++nb)
+            wf[nb] = *reinterpret_cast<const bf16x8 *>(st + A_EL +
+                                                       (wn * 32 * NB + 32 * nb + col) * kLgBK + pc);
+        if (F32A) {
+            // The 8 f32 of the wave's row block: pieces 2 (2t + half) and the
+            // next of its 256-byte row, split into the hi (af[0]) and lo
+            // (af[1]) fragments.
+            const int srow = wm * 32 + col;
+            const int p0 = 2 * (2 * t + half);
+            const f32x4 x0 =
+                *reinterpret_cast<const f32x4 *>(st + srow * 128 + 8 * (p0 ^ (srow & 15)));
+            const f32x4 x1 =
+                *reinterpret_cast<const f32x4 *>(st + srow * 128 + 8 * ((p0 + 1) ^ (srow & 15)));
+            uint2 h0, l0, h1, l1;
+            split_terms4(x0, h0, l0);
+            split_terms4(x1, h1, l1);
+            af[0] = __builtin_bit_cast(bf16x8, uint4{h0.x, h0.y, h1.x, h1.y});
+            af[1] = __builtin_bit_cast(bf16x8, uint4{l0.x, l0.y, l1.x, l1.y});
+            return;
+        }
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const int srow = TERMS == 1 ? wm * 128 + 32 * b : (b >> 1) * BM + wm * 64 + 32 * (b & 1);
@@ -135,10 +177,12 @@ __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs 
         }
     };
 
-    f32x16 acc[MB][2];
+    f32x16 acc[MB][NB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
-        acc[mb][0] = acc[mb][1] = f32x16{};
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            acc[mb][nb] = f32x16{};
     const int total = g.chunks;
     dma(0, 0);
     if (total > 1) {
@@ -148,10 +192,20 @@ __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs 
         wait_vmcnt<0>();
     }
     ring_barrier();
-    bf16x8 af[2][4], wf[2][2];
+    bf16x8 af[2][4], wf[2][NB];
     frags(smem, 0, af[0], wf[0]);
     // The 8 MFMAs of one K step on fragment set `set`.
     auto mfmas = [&](int set) {
+        if (F32A) {
+            // Per accumulator the hi product, then the lo product (the order
+            // of the two-term kernel on term rows, so C is bit-identical).
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                acc[0][nb] = mfma_bf16(af[set][0], wf[set][nb], acc[0][nb]);
+                acc[0][nb] = mfma_bf16(af[set][1], wf[set][nb], acc[0][nb]);
+            }
+            return;
+        }
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
@@ -192,10 +246,10 @@ __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs 
     }
 
     // Lane (col, half) of accumulator (mb, nb) holds C[m][n] for n = col0 +
-    // wn * 64 + 32 nb + col and m = row0 + wm * (BM / 2) + 32 mb + 8 (r >> 2)
+    // wn * 32 NB + 32 nb + col and m = row0 + wm * 32 MB + 32 mb + 8 (r >> 2)
     // + 4 half + (r & 3): for one register, 32 lanes cover 128 consecutive
     // bytes of a row.
-    const int mw = row0 + wm * (BM / 2);
+    const int mw = row0 + wm * (32 * MB);
     const bool full = row0 + BM <= g.M && col0 + kLgBN <= g.N;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -205,8 +259,8 @@ __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs 
         const int b_lo = EPI == kLgResidual ? mbase / g.S : 0;
         const int bnd = (b_lo + 1) * g.S;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            const int n = col0 + wn * 64 + 32 * nb + col;
+        for (int nb = 0; nb < NB; ++nb) {
+            const int n = col0 + wn * 32 * NB + 32 * nb + col;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = mbase + acc_row(r, half);
@@ -251,6 +305,45 @@ bool gemm_large_supported(int M, int N, int K, int terms, int64_t lda, int64_t l
            int64_t(kLgRows) * std::max(lda, ldw) * 2 < (int64_t(1) << 31);
 }
 
+bool gemm_large_f32a_supported(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
+                               const float *a, const void *w, const void *c)
+{
+    const auto al = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (M <= 0 || N <= 0 || K <= 0 || K % kLgBK)
+        return false;
+    const int64_t tiles = ((M + 127) / 128) * int64_t((N + kLgBN - 1) / kLgBN);
+    return tiles >= 256 && tiles < (int64_t(1) << 31) && lda >= K && ldw >= K && ldc >= N &&
+           lda % 4 == 0 && ldw % 8 == 0 && al(a) && al(w) &&
+           (reinterpret_cast<uintptr_t>(c) & 3) == 0 &&
+           int64_t(128) * lda * 4 < (int64_t(1) << 31) &&
+           int64_t(kLgBN) * ldw * 2 < (int64_t(1) << 31);
+}
+
+bool launch_gemm_large_f32a(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *c,
+                            int64_t ldc, int M, int N, int K, hipStream_t st)
+{
+    if (!gemm_large_f32a_supported(M, N, K, lda, ldw, ldc, a, w, c))
+        return fail("gemm_large_f32a: unsupported shape or alignment");
+    LargeArgs g;
+    g.a0 = g.a1 = nullptr;
+    g.af = a;
+    g.w = w;
+    g.c = c;
+    g.gate = nullptr;
+    g.lda = lda;
+    g.ldw = ldw;
+    g.ldc = ldc;
+    g.gate_stride = 0;
+    g.M = M;
+    g.N = N;
+    g.S = M;
+    g.tiles_n = (N + kLgBN - 1) / kLgBN;
+    g.chunks = K / kLgBK;
+    const dim3 grid(unsigned(((M + 127) / 128) * g.tiles_n)), block(kLgWaves * 64);
+    hipLaunchKernelGGL((gemm_large_kernel<2, kLgF32, true>), grid, block, 0, st, g);
+    return hip_ok(hipGetLastError(), "gemm_large_kernel (f32 activations) launch");
+}
+
 bool launch_gemm_large(const uint16_t *a0, const uint16_t *a1, int64_t lda, const uint16_t *w,
                        int64_t ldw, void *c, int64_t ldc, int M, int N, int K, int epilogue,
                        const float *gate, int64_t gate_stride, int S, hipStream_t st)
@@ -264,6 +357,7 @@ bool launch_gemm_large(const uint16_t *a0, const uint16_t *a1, int64_t lda, cons
     LargeArgs g;
     g.a0 = a0;
     g.a1 = a1;
+    g.af = nullptr;
     g.w = w;
     g.c = c;
     g.gate = gate;
@@ -279,7 +373,8 @@ bool launch_gemm_large(const uint16_t *a0, const uint16_t *a1, int64_t lda, cons
     g.tiles_n = (N + kLgBN - 1) / kLgBN;
     g.chunks = K / kLgBK;
     const dim3 grid(unsigned(tiles_m * g.tiles_n)), block(kLgWaves * 64);
-#define ANIMA_LG_LAUNCH(T, E) hipLaunchKernelGGL((gemm_large_kernel<T, E>), grid, block, 0, st, g)
+#define ANIMA_LG_LAUNCH(T, E) \
+    hipLaunchKernelGGL((gemm_large_kernel<T, E, false>), grid, block, 0, st, g)
     if (terms == 1) {
         if (epilogue == kLgBf16)
             ANIMA_LG_LAUNCH(1, kLgBf16);

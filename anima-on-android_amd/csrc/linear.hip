@@ -326,6 +326,10 @@ bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, 
     if (!scratch || scratch_bytes < linear_scratch_bytes(M, K, exact) ||
         (reinterpret_cast<uintptr_t>(scratch) & 15u) != 0)
         return fail("linear: scratch smaller than linear_scratch_bytes() or not 16-byte aligned");
+    // Large M, f32 mode: the two-term kernel splits f32 A in registers (no
+    // pass over HBM for the terms), bit-identical to the split + product below.
+    if (exact && gemm_large_f32a_supported(M, N, K, lda, ldw, ldc, a, w, c))
+        return launch_gemm_large_f32a(a, lda, w, ldw, c, ldc, M, N, K, st);
     SplitArgs s;
     s.a = a;
     s.lda = lda;

@@ -147,6 +147,21 @@ def test_large_m_kernel_vs_oracle(M, N, K):
     assert e[rt.F32] * 20 < e[rt.BF16]
 
 
+@pytest.mark.parametrize("M,N,K", [(8192, 2048, 2048), (8000, 2100, 512), (8200, 2048, 1024)])
+def test_large_m_f32_activations_equal_split_path(M, N, K):
+    """F32 mode at large M with 16-byte aligned A rows: the two-term kernel
+    splits the f32 activations into hi/lo bf16 terms in registers.  The same
+    values with a row stride of K + 2 floats take the split pass and the same
+    kernel on its term rows; the outputs agree bit for bit (ragged M and N
+    included)."""
+    a, w = _data(M + 7 * N + K, M, N, K)
+    print(f"f32-activation large-M linear M={M} N={N} K={K}", flush=True)
+    fused = run_linear(a, w, rt.F32)
+    split = run_linear(a, w, rt.F32, lda=K + 2)
+    assert np.isfinite(fused).all()
+    assert np.array_equal(fused.view(np.uint32), split.view(np.uint32))
+
+
 def test_linear_drop_in_gemm_bf16_is_split_path():
     """anima_rt_run_gemm_bf16 (host drop-in) runs the F32 split mode on shapes
     the library GEMM supports, within the drop-in's 1e-5 bound."""
