@@ -194,6 +194,14 @@ bool gemm_large_f32a_supported(int M, int N, int K, int64_t lda, int64_t ldw, in
                                const float *a, const void *w, const void *c);
 bool launch_gemm_large_f32a(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *c,
                             int64_t ldc, int M, int N, int K, hipStream_t st);
+// Large-M product on f32 activations in 256 x 256 tiles (gemm_f32a.hip): a
+// [M][lda] (lda % 4 == 0, K % 32 == 0) split into bf16 hi + lo terms
+// (two_terms) or rounded to bf16 in registers, C f32.  With two terms C is
+// bit-identical to the split pass plus launch_gemm_large on the term rows.
+bool gemm_f32a_supported(int M, int N, int K, int64_t lda, int64_t ldw, int64_t ldc,
+                         const float *a, const void *w, const void *c);
+bool launch_gemm_f32a(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *c,
+                      int64_t ldc, int M, int N, int K, bool two_terms, hipStream_t st);
 
 // Small-M bf16 GEMM (gemm_bf16.hip): C[M,N] = a0 . W^T (+ a1 . W^T) with bf16
 // activation terms a0 (a1 null for one term) [M][lda], bf16 W [N][ldw], f32

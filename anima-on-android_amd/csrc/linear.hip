@@ -326,8 +326,14 @@ bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, 
     if (!scratch || scratch_bytes < linear_scratch_bytes(M, K, exact) ||
         (reinterpret_cast<uintptr_t>(scratch) & 15u) != 0)
         return fail("linear: scratch smaller than linear_scratch_bytes() or not 16-byte aligned");
-    // Large M, f32 mode: the two-term kernel splits f32 A in registers (no
-    // pass over HBM for the terms), bit-identical to the split + product below.
+    // Large M, f32 modes: the kernel splits f32 A into its hi and lo terms in
+    // registers, so the terms make no round trip through HBM; bit-identical to
+    // the split + two-term product below.  256 x 256 tiles where they fill the
+    // GPU, else 128 x 256.  (One term stays on the split + library product:
+    // staging f32 rows doubles its A bytes, past what L2 feeds LDS at the
+    // MFMA rate.)
+    if (exact && gemm_f32a_supported(M, N, K, lda, ldw, ldc, a, w, c))
+        return launch_gemm_f32a(a, lda, w, ldw, c, ldc, M, N, K, true, st);
     if (exact && gemm_large_f32a_supported(M, N, K, lda, ldw, ldc, a, w, c))
         return launch_gemm_large_f32a(a, lda, w, ldw, c, ldc, M, N, K, st);
     SplitArgs s;

@@ -147,13 +147,15 @@ def test_large_m_kernel_vs_oracle(M, N, K):
     assert e[rt.F32] * 20 < e[rt.BF16]
 
 
-@pytest.mark.parametrize("M,N,K", [(8192, 2048, 2048), (8000, 2100, 512), (8200, 2048, 1024)])
+@pytest.mark.parametrize("M,N,K", [(8192, 2048, 2048), (8000, 2100, 512), (8200, 2048, 1024),
+                                   (8192, 6144, 64), (4096, 2048, 512), (4000, 2100, 128)])
 def test_large_m_f32_activations_equal_split_path(M, N, K):
-    """F32 mode at large M with 16-byte aligned A rows: the two-term kernel
-    splits the f32 activations into hi/lo bf16 terms in registers.  The same
-    values with a row stride of K + 2 floats take the split pass and the same
-    kernel on its term rows; the outputs agree bit for bit (ragged M and N
-    included)."""
+    """F32 mode at large M with 16-byte aligned A rows: the product kernels
+    split the f32 activations into hi/lo bf16 terms in registers (256 x 256
+    tiles where they fill the GPU, 128 x 256 at 4096 rows).  The same values
+    with a row stride of K + 2 floats take the split pass and the two-term
+    kernel on its term rows; the outputs agree bit for bit (ragged M and N,
+    and K of one to two chunks, included)."""
     a, w = _data(M + 7 * N + K, M, N, K)
     print(f"f32-activation large-M linear M={M} N={N} K={K}", flush=True)
     fused = run_linear(a, w, rt.F32)
