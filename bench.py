@@ -411,7 +411,7 @@ def denoise_step(c, mode, blocks=28, B=2, S=4096, H=16, D=128):
                                                          caches[i].handle, o.data_ptr(),
                                                          scratch.data_ptr(), n_x, B, S, eps,
                                                          c.stp), "cross_attention_dev")
-    ms = c.time(step, 3, 1)
+    ms = c.time(step, 5, 1, prewarm_s=0.5)
     flops = blocks * 4.0 * B * H * S * D * (S + 512)
     for cache in caches:
         cache.close()
@@ -486,7 +486,7 @@ def denoise_step_blocks(c, mode, blocks=28, B=2, S=4096, H=16, D=128, Dm=2048):
                 x.data_ptr(), mx.data_ptr(), wqx.data_ptr(), None, None, wox.data_ptr(),
                 ones.data_ptr(), ones.data_ptr(), None, caches[i].handle, B, S, Dm, H, D, eps,
                 mode, scratch.data_ptr(), n_x, c.stp), "attention_block_dev (cross)")
-    ms_step = c.time(step, 3, 1)
+    ms_step = c.time(step, 5, 1, prewarm_s=0.5)
     if not torch.isfinite(x).all():
         raise RuntimeError("non-finite residual stream")
     attn = blocks * 4.0 * B * H * S * D * (S + 512)
@@ -503,7 +503,7 @@ def denoise_step_blocks(c, mode, blocks=28, B=2, S=4096, H=16, D=128, Dm=2048):
                         "resident stream"}
 
 
-def sampler_step(c, mode, H=128, W=128, steps=3):
+def sampler_step(c, mode, H=128, W=128, steps=5):
     """One Euler/CFG sampler step of the whole DiT at 1024x1024
     (EulerSampler.sample, sampling.py:115-140, on NumpyDiT.forward): the
     latent [1,16,128,128] runs as the CFG pair through patch embedding, 28
