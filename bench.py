@@ -92,6 +92,10 @@ def parse():
     ap.add_argument("--cross-step", action="store_true",
                     help="only the cached-context cross-attention at 4096 x 512 (B=2, H=16), "
                          "every mode; prints one JSON line of its own")
+    ap.add_argument("--gemm-step", action="store_true",
+                    help="only the M = 8192 projection GEMMs (anima_hip_linear_dev on f32 "
+                         "activations: q/k/v/o, fused qkv, fc1, fc2 shapes), every mode; prints "
+                         "one JSON line of its own")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 256 MiB device copy (calibrates "
                          "FETCH_SIZE/WRITE_SIZE) then 2 steps of each variant (with "
@@ -441,6 +445,12 @@ class Linear:
                                                 self.nbytes, c.stp), "linear_dev")
 
 
+# The DiT's token-level projections at 1024x1024 (M = 8192 tokens for the CFG
+# pair): q/k/v/o and the cross q/o (2048 x 2048), fused q/k/v (6144 x 2048),
+# fc1 (8192 x 2048) and fc2 (2048 x 8192), as N x K.
+GEMM_SHAPES = ((8192, 2048, 2048), (8192, 6144, 2048), (8192, 8192, 2048), (8192, 2048, 8192))
+
+
 def projection_gemm(c, mode, M=8192, N=2048, K=2048):
     """One q/k/v/output projection of a block at 4096 tokens, B=2."""
     x = c.randn((M, K), 7001)
@@ -775,6 +785,15 @@ def main():
             cache.close()
             res[v] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 2)}
         print(json.dumps({"config": "cross_attention_4096x512_B2_cached", "results": res}),
+              flush=True)
+        return
+
+    if args.gemm_step:
+        res = {}
+        for v in ("bf16", "f32x3", "f32"):
+            res[v] = {f"{M}x{N}x{K}": projection_gemm(c, MODE[v], M, N, K)
+                      for M, N, K in GEMM_SHAPES}
+        print(json.dumps({"config": "projection_gemm_f32_activations", "results": res}),
               flush=True)
         return
 
