@@ -127,7 +127,10 @@ def test_linear_projection_8192x2048x2048_sampled_rows():
 # of the tile clamped.  Rows are sampled for the oracle, including both ends
 # of every ragged edge.
 LARGE_M = [(8192, 6144, 2048), (8192, 8192, 2048), (8192, 2048, 8192), (8000, 2100, 512),
-           (8200, 2048, 1024)]
+           (8200, 2048, 1024),
+           # the f32-activation kernel's 32-element K chunks: one, three and five
+           # chunks (prologue only; the three-stage ring filled; copies in the loop)
+           (8192, 2048, 32), (8192, 2048, 96), (8192, 2048, 160)]
 
 
 @pytest.mark.parametrize("M,N,K", LARGE_M)
