@@ -167,6 +167,18 @@ def test_large_m_f32_activations_equal_split_path(M, N, K):
     assert np.array_equal(fused.view(np.uint32), split.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,N,K,lda", [(8192, 2048, 512, 516), (4096, 2048, 256, 260)])
+def test_large_m_f32_activations_wide_rows(M, N, K, lda):
+    """The in-register split on A rows inside a wider buffer (row stride K + 4
+    floats, still 16-byte aligned), 256 x 256 and 128 x 256 tiles: the same
+    bits as the split path (row stride K + 2, which the kernels do not take)."""
+    a, w = _data(M + N + lda, M, N, K)
+    print(f"f32-activation large-M linear M={M} N={N} K={K} lda={lda}", flush=True)
+    fused = run_linear(a, w, rt.F32, lda=lda)
+    split = run_linear(a, w, rt.F32, lda=K + 2)
+    assert np.array_equal(fused.view(np.uint32), split.view(np.uint32))
+
+
 def test_linear_drop_in_gemm_bf16_is_split_path():
     """anima_rt_run_gemm_bf16 (host drop-in) runs the F32 split mode on shapes
     the library GEMM supports, within the drop-in's 1e-5 bound."""
