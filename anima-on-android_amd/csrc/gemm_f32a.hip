@@ -214,7 +214,11 @@ __global__ __launch_bounds__(kFaWaves * 64, 1) void gemm_f32a_kernel(FaArgs g)
 
     // Lane (col, half) of accumulator nb holds C[m][n] for n = col0 + 32 nb +
     // col and m = row0 + wave * 32 + acc_row(r, half): for one register, 32
-    // lanes cover 128 consecutive bytes of a row.
+    // lanes cover 128 consecutive bytes of a row.  Nontemporal (streaming)
+    // stores: C goes to the next kernel through HBM, and the stores of one
+    // round of tiles then overlap the next round's loads better (8192 x 8192
+    // x 2048: 0.498 -> 0.480 ms, 8192 x 2048 x 2048 0.1203 -> 0.1188 ms on one
+    // box).
     const bool full = row0 + kFaBM <= g.M && col0 + kFaBN <= g.N;
 #pragma unroll
     for (int nb = 0; nb < kFaNB; ++nb) {
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(kFaWaves * 64, 1) void gemm_f32a_kernel(FaArgs g)
             const int m = row0 + wave * 32 + acc_row(r, half);
             if (!full && (m >= g.M || n >= g.N))
                 continue;
-            g.c[int64_t(m) * g.ldc + n] = acc[nb][r];
+            __builtin_nontemporal_store(acc[nb][r], g.c + int64_t(m) * g.ldc + n);
         }
     }
 }
