@@ -35,8 +35,9 @@
 //   * workgroups in XCD-major order with the N tiles of one M tile
 //     consecutive: the workgroups of one XCD share W chunks and A chunks
 //     through its L2.
-// Epilogues: C as f32 (plain store), C as bf16 (round to nearest even), or
-// x[m][n] += gate[m / S][n] * C[m][n] (the gated residual of a DiT block).
+// Epilogues: C as f32, C as bf16 (round to nearest even), both through
+// nontemporal (streaming) stores, or x[m][n] += gate[m / S][n] * C[m][n] (the
+// gated residual of a DiT block).
 //
 // f32 activations (F32A): the two-term tile stages the 128 f32 rows of A
 // themselves (256 bytes per row and chunk, the bytes of the hi and lo rows
@@ -269,9 +270,9 @@ __global__ __launch_bounds__(kLgWaves * 64, 1) void gemm_large_kernel(LargeArgs 
                 const float v = acc[mb][nb][r];
                 const int64_t o = int64_t(m) * g.ldc + n;
                 if (EPI == kLgF32) {
-                    static_cast<float *>(g.c)[o] = v;
+                    __builtin_nontemporal_store(v, static_cast<float *>(g.c) + o);
                 } else if (EPI == kLgBf16) {
-                    static_cast<u16 *>(g.c)[o] = f32_to_bf16_rne(v);
+                    __builtin_nontemporal_store(f32_to_bf16_rne(v), static_cast<u16 *>(g.c) + o);
                 } else {
                     const int b = g.S >= 32 ? (m >= bnd ? b_lo + 1 : b_lo) : m / g.S;
                     const float gv = g.gate[int64_t(b) * g.gate_stride + n];
