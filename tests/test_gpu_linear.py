@@ -179,6 +179,30 @@ def test_large_m_f32_activations_wide_rows(M, N, K, lda):
     assert np.array_equal(fused.view(np.uint32), split.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,N,K", [(8192, 2048, 256), (4096, 2048, 256), (8192, 2048, 128)])
+@pytest.mark.parametrize("mode", [rt.F32, rt.BF16])
+def test_large_m_output_rows_in_a_wider_buffer(M, N, K, mode):
+    """C rows with a pitch of N + 64 floats: the same values as packed rows,
+    and the 64 columns past N of every row keep the caller's bytes (the large-M
+    epilogues store no column past N)."""
+    from devmem import DevBuf
+    lib = _lib.load()
+    a, w = _data(M + N + K + mode, M, N, K)
+    ldc = N + 64
+    da, dw = DevBuf.of(a), DevBuf.of(w)
+    sentinel = np.full((M, ldc), np.float32(-7.25))
+    dc = DevBuf.of(sentinel)
+    sb = lib.anima_hip_linear_scratch_bytes(M, K, mode)
+    scratch = DevBuf(max(sb, 256))
+    print(f"large-M linear into rows of {ldc} floats, M={M} N={N} K={K} mode {mode}", flush=True)
+    _lib.check(lib.anima_hip_linear_dev(da.addr, K, dw.addr, K, dc.addr, ldc, M, N, K, mode,
+                                        scratch.addr, sb, None), "linear_dev")
+    wide = dc.get((M, ldc))
+    packed = run_linear(a, w, mode)
+    assert np.array_equal(wide[:, :N].view(np.uint32), packed.view(np.uint32))
+    assert np.array_equal(wide[:, N:], sentinel[:, N:])
+
+
 def test_linear_drop_in_gemm_bf16_is_split_path():
     """anima_rt_run_gemm_bf16 (host drop-in) runs the F32 split mode on shapes
     the library GEMM supports, within the drop-in's 1e-5 bound."""
