@@ -13,9 +13,12 @@
 //               |r| <= 2^-16 |A| per element; C = hi.W^T + lo.W^T
 //               (two products, f32 accumulation);
 //   bf16 mode   hi only (|A - hi| <= 2^-8 |A|).
-// The products are plain bf16 x bf16 -> f32 GEMMs and go to hipBLASLt.  A
-// shape without a hipBLASLt solution falls back to gemm_kernel (f32 MFMA
-// on the exact f32 values).
+// The products are plain bf16 x bf16 -> f32 GEMMs: hipBLASLt, or the
+// hand-written kernels where they measured faster (small M: gemm_bf16.hip;
+// large M: gemm_large.hip on term planes and gemm_f32a.hip, which splits f32
+// A in registers so the split pass does not run).  A shape without a
+// hipBLASLt solution falls back to gemm_kernel (f32 MFMA on the exact f32
+// values).
 #include "common.h"
 
 #include <hipblaslt/hipblaslt.h>
@@ -329,11 +332,17 @@ bool launch_linear(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, 
     // Large M, f32 modes: the kernel splits f32 A into its hi and lo terms in
     // registers, so the terms make no round trip through HBM; bit-identical to
     // the split + two-term product below.  256 x 256 tiles where they fill the
-    // GPU, else 128 x 256.  (One term stays on the split + library product:
-    // staging f32 rows doubles its A bytes, past what L2 feeds LDS at the
-    // MFMA rate.)
+    // GPU, else 128 x 256.
     if (exact && gemm_f32a_supported(M, N, K, lda, ldw, ldc, a, w, c))
         return launch_gemm_f32a(a, lda, w, ldw, c, ldc, M, N, K, true, st);
+    // One term (bf16 mode): the same kernel rounding A to bf16 in registers
+    // beats the split pass + library product where N and K are at most 2048
+    // (8192 x 2048 x 2048: 78.5 against 80.2 us, 8192 x 2048 x 1024: 45.4
+    // against 50.0, 16384 x 2048 x 2048: 149.5 against 156.4).  Elsewhere the
+    // split + library product stays: staging f32 rows doubles the A bytes,
+    // and at larger N or K the kernel ran up to 34 % slower.
+    if (!exact && N <= 2048 && K <= 2048 && gemm_f32a_supported(M, N, K, lda, ldw, ldc, a, w, c))
+        return launch_gemm_f32a(a, lda, w, ldw, c, ldc, M, N, K, false, st);
     if (exact && gemm_large_f32a_supported(M, N, K, lda, ldw, ldc, a, w, c))
         return launch_gemm_large_f32a(a, lda, w, ldw, c, ldc, M, N, K, st);
     SplitArgs s;
