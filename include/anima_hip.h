@@ -277,8 +277,13 @@ bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, 
  * (f32 modes, or bf16 mode with K >= 8192) the size includes 16 MiB for the
  * split-K partials of the hand-written small-M GEMM, which then runs instead
  * of the library GEMM; the partials are added in a fixed order, so results
- * are deterministic.  Shapes without a library solution (e.g. ldw not a
- * multiple of 8) run the exact f32-MFMA kernel instead. */
+ * are deterministic.  At large M (a grid of at least 256 tiles of 256 x 256
+ * or 128 x 256, K a multiple of 32, 16-byte aligned A rows with lda % 4 == 0)
+ * the f32 modes, and the bf16 mode where N and K are at most 2048, run a
+ * kernel that stages the f32 rows of a and splits (or rounds) them in
+ * registers, with the same result bits as the split path.  Shapes without a
+ * library solution (e.g. ldw not a multiple of 8) run the exact f32-MFMA
+ * kernel instead. */
 size_t anima_hip_linear_scratch_bytes(int M, int K, int mode);
 bool anima_hip_linear_dev(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, float *c,
                           int64_t ldc, int M, int N, int K, int mode, void *scratch,
