@@ -281,7 +281,8 @@ bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, 
  * or 128 x 256, K a multiple of 32, 16-byte aligned A rows with lda % 4 == 0)
  * the f32 modes, and the bf16 mode where N and K are at most 2048, run a
  * kernel that stages the f32 rows of a and splits (or rounds) them in
- * registers, with the same result bits as the split path.  Shapes without a
+ * registers (in the f32 modes bit-identical to the split pass followed by a
+ * two-term product on the term rows).  Shapes without a
  * library solution (e.g. ldw not a multiple of 8) run the exact f32-MFMA
  * kernel instead. */
 size_t anima_hip_linear_scratch_bytes(int M, int K, int mode);
