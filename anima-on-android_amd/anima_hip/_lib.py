@@ -49,6 +49,8 @@ SIGNATURES = {
     "anima_hip_qk_prologue_dev": (_B, [_P] * 4 + [_I] * 4 + [_I64P] * 2 + [_F, _I, _P]),
     "anima_hip_qkv_prologue_dev": (_B, [_P] * 3 + [ct.c_int64] + [_P] * 6 + [_I] * 4
                                    + [_F, _I, _P]),
+    "anima_hip_qkv_projection_dev": (_B, [_P, ct.c_int64, _P, ct.c_int64, _I] + [_P] * 6
+                                     + [_I] * 3 + [_F, _I, _P]),
     "anima_hip_attention": (_B, [_P] * 7 + [_I] * 5 + [_F, _I]),
     "anima_hip_gemm_dev": (_B, [_P, ct.c_int64, _P, _I, ct.c_int64, _P, ct.c_int64] + [_I] * 3
                            + [_P]),

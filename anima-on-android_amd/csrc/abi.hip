@@ -1444,6 +1444,35 @@ bool anima_hip_qkv_prologue_dev(const float *q, const float *k, const float *v, 
     return launch_prep_qkv(p, pick_stream(stream));
 }
 
+bool anima_hip_qkv_projection_dev(const float *x, int64_t ldx, const uint16_t *w_qkv,
+                                  int64_t ldw, int K, const float *q_norm_w,
+                                  const float *k_norm_w, const float *freqs, void *qo, void *ko,
+                                  void *vo, int B, int S, int H, float eps, int mode,
+                                  void *stream)
+{
+    if (!ready_for_device_call())
+        return false;
+    if (mode != ANIMA_HIP_F32 && mode != ANIMA_HIP_F32X3)
+        return fail("qkv_projection_dev: the f32 and f32x3 modes only");
+    if (B <= 0 || S <= 0 || H <= 0 || K <= 0)
+        return fail("qkv_projection_dev: dimensions must be positive");
+    if (!x || !w_qkv || !qo || !ko || !vo)
+        return fail("qkv_projection_dev: null pointer");
+    QkvPrep p;
+    p.qo = qo;
+    p.ko = ko;
+    p.vo = vo;
+    p.w[0] = q_norm_w;
+    p.w[1] = k_norm_w;
+    p.freqs = freqs;
+    p.B = B;
+    p.S = S;
+    p.H = H;
+    p.eps = eps;
+    p.mode = mode == ANIMA_HIP_F32 ? kAttnF32 : kAttnF32X3;
+    return launch_gemm_f32a_qkv(x, ldx, w_qkv, ldw, K, p, pick_stream(stream));
+}
+
 bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, int64_t ldw,
                         float *c, int64_t ldc, int M, int N, int K, void *stream)
 {

@@ -140,8 +140,11 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     if (in.freqs && S_q != S_kv)
         return fail("attention: RoPE needs S_q == S_kv (self-attention)");
     const bool prepared = in.k_prep != nullptr;
+    const bool q_ready = in.q_prep != nullptr;
+    if (q_ready && (!prepared || !in.v_prep))
+        return fail("attention: prepared Q rows need prepared K and V");
     char *cur = static_cast<char *>(scratch);
-    void *qn = cur;
+    void *qn = q_ready ? const_cast<void *>(in.q_prep) : static_cast<void *>(cur);
     cur += round_up(size_t(B) * S_q * H * D * qk_elem_bytes(mode));
 
     const void *kp = in.k_prep, *vp = in.v_prep;
@@ -221,13 +224,14 @@ bool run_attention(const AttnInputs &in, void *scratch, hipStream_t st)
     const bool raw_kernel =
         mode == kAttnBF16 ? flash_bf16_raw_q(int64_t(B) * H, S_q, S_kv)
                           : raw_plan.waves == 8 && raw_plan.splits == 1;
-    const bool raw_q = prepared && !in.freqs && D == 128 && a16(in.q) && ld_q % 4 == 0 &&
-                       (!in.q_norm_w || a16(in.q_norm_w)) && raw_kernel;
+    const bool raw_q = !q_ready && prepared && !in.freqs && D == 128 && a16(in.q) &&
+                       ld_q % 4 == 0 && (!in.q_norm_w || a16(in.q_norm_w)) && raw_kernel;
 
     // Q rows, and K rows unless prepared, in one launch.
     const RowProblem pq =
         qk_rows(in.q, in.q_norm_w, in.freqs, qn, B, S_q, H, D, in.eps, mode, in.ld_q);
-    if (!fused && !raw_q && !(prepared ? launch_rows(pq, st) : launch_rows_pair(pk, pq, st)))
+    if (!fused && !raw_q && !q_ready &&
+        !(prepared ? launch_rows(pq, st) : launch_rows_pair(pk, pq, st)))
         return false;
 
     const bool bcast = in.Bk == 1 && B > 1;

@@ -63,6 +63,8 @@ struct LnArgs {
     int64_t res_ld;
     float *xw;  // x itself, writable (set with res_y)
     unsigned int *hi, *lo;  // [M][kp] bf16 (addressed as pairs); lo may be null
+    float *yf;              // or, when set, the modulated rows as f32 [M][ldy]
+    int64_t ldy;
     int64_t kp;
     int64_t tld;  // term row stride (elements): kp, or 2*kp for [hi | lo] rows
     int64_t M;
@@ -156,6 +158,19 @@ __global__ __launch_bounds__(256) void ln_modulate_kernel(LnArgs a)
         return;
     const float *shift = a.mod + int64_t(b) * a.mod_ld;
     const float *scale = shift + a.Dm;
+    if (a.yf) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const int c = 64 * seg + lane + 64 * WPR * i;
+            if (c < n4) {
+                const f32x4 sc = *reinterpret_cast<const f32x4 *>(scale + 4 * c);
+                const f32x4 sh = *reinterpret_cast<const f32x4 *>(shift + 4 * c);
+                const f32x4 xn = (v[i] - mean) * rstd;
+                *reinterpret_cast<f32x4 *>(a.yf + r * a.ldy + 4 * c) = xn * (1.0f + sc) + sh;
+            }
+        }
+        return;
+    }
     unsigned int *hrow = a.hi + r * (a.tld >> 1);
     unsigned int *lrow = a.lo ? a.lo + r * (a.tld >> 1) : nullptr;
 #pragma unroll
@@ -245,14 +260,14 @@ size_t attention_block_scratch_bytes(int B, int S, int Dm, int H, int D, int Bk,
 bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t mod_ld,
                         uint16_t *hi, uint16_t *lo, int64_t M, int S, int Dm, float eps,
                         hipStream_t st, float *res_x, const float *res_y, const float *res_gate,
-                        int64_t res_ld, int64_t tld, int res_parts)
+                        int64_t res_ld, int64_t tld, int res_parts, float *y_f32)
 {
     if (M == 0)
         return true;
     if (Dm <= 0 || Dm % 4 || Dm > 256 * 16 || S <= 0)
         return fail("ln_modulate: the model width must be a positive multiple of 4, at most 4096");
     if (!aligned16(x) || ldx % 4 || !aligned16(mod) || mod_ld % 4 || !aligned16(hi) ||
-        !aligned16(lo))
+        !aligned16(lo) || !aligned16(y_f32))
         return fail("ln_modulate: operands must be 16-byte aligned");
     if (res_y && (res_x != x || ldx != Dm || !aligned16(res_y) || !aligned16(res_gate) ||
                   res_ld % 4 || res_parts < 1))
@@ -271,6 +286,8 @@ bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t m
     a.xw = res_y ? res_x : nullptr;
     a.hi = reinterpret_cast<unsigned int *>(hi);
     a.lo = reinterpret_cast<unsigned int *>(lo);
+    a.yf = y_f32;
+    a.ldy = Dm;
     a.kp = linear_terms_ld(Dm);
     a.tld = tld > 0 ? tld : a.kp;
     if (a.tld < a.kp || a.tld % 8)

@@ -311,6 +311,9 @@ struct AttnInputs {
     const float *k_norm_w = nullptr;
     const void *k_prep = nullptr;     // prepared K/V (context cache), or null
     const void *v_prep = nullptr;
+    // Prepared Q rows in the mode's layout (with k_prep / v_prep): the
+    // attention runs the flash kernel alone.
+    const void *q_prep = nullptr;
     float *out = nullptr;             // [B, S_q, H, D] f32
     // Or O as bf16 projection terms (D == 128): token rows ld_t elements
     // apart, hi at column h*D + d, lo (when lo_t > 0) lo_t elements after it.
@@ -344,6 +347,29 @@ struct PrepProblem {
 };
 bool prep_qkv_supported(const PrepProblem &p);  // D == 128, 16-byte alignment
 bool launch_prep_qkv(const PrepProblem &p, hipStream_t st);
+// A self-attention's fused q/k/v projection with that one-launch prologue as
+// its epilogue (gemm_f32a.hip): a [B*S][lda] f32 activations times the
+// stacked bf16 weights w [3*H*128][ldw] (q rows, then k, then v), in the f32
+// modes' exact two-term product.  Instead of the product's f32 columns the
+// kernel writes the attention operands: qo / ko as launch_prep_qkv writes
+// them (RMSNorm with w[0] / w[1], RoPE with freqs), and vo as the x3
+// kernel's term V^T (kAttnF32X3) or dense f32 V rows [B, S, H, 128]
+// (kAttnF32).  Bit-identical to launch_gemm_f32a (two terms) into [M][3HD]
+// followed by launch_prep_qkv on its column blocks.  S % 64 == 0 (no V^T
+// padding), H even (a 256-column tile holds two whole heads of one operand),
+// and the f32a grid conditions.
+struct QkvPrep {
+    void *qo = nullptr, *ko = nullptr, *vo = nullptr;
+    const float *w[2] = {nullptr, nullptr};
+    const float *freqs = nullptr;
+    int B = 0, S = 0, H = 0;
+    float eps = 1e-6f;
+    AttnMode mode = kAttnF32X3;
+};
+bool gemm_f32a_qkv_supported(const float *a, int64_t lda, const void *w, int64_t ldw, int K,
+                             const QkvPrep &p);
+bool launch_gemm_f32a_qkv(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, int K,
+                          const QkvPrep &p, hipStream_t st);
 size_t prepared_k_bytes(int Bk, int S_kv, int H, int D, AttnMode mode);
 size_t prepared_v_bytes(int Bk, int S_kv, int H, int D, AttnMode mode);
 size_t attention_scratch_bytes(int B, int S_q, int Bk, int S_kv, int H, int D, AttnMode mode,
@@ -383,11 +409,13 @@ bool run_attention_block(const BlockProblem &p, void *scratch, size_t scratch_by
 // back to x (res_x must be x).  tld: term row stride in elements (0:
 // linear_terms_ld(Dm)); [hi | lo] rows in one buffer use tld = 2 *
 // linear_terms_ld(Dm) and lo = hi + linear_terms_ld(Dm).
+// y_f32 != null: the modulated rows are written there as dense f32 [M][Dm]
+// instead (hi and lo unused), the input of the f32-activation GEMMs.
 bool launch_ln_modulate(const float *x, int64_t ldx, const float *mod, int64_t mod_ld,
                         uint16_t *hi, uint16_t *lo, int64_t M, int S, int Dm, float eps,
                         hipStream_t st, float *res_x = nullptr, const float *res_y = nullptr,
                         const float *res_gate = nullptr, int64_t res_ld = 0, int64_t tld = 0,
-                        int res_parts = 1);
+                        int res_parts = 1, float *y_f32 = nullptr);
 // x += gate[b] * y for rows of S per batch entry.
 bool launch_gate_residual(float *x, const float *y, const float *mod, int64_t M, int S, int Dm,
                           hipStream_t st);

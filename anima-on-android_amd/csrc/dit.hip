@@ -654,8 +654,45 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
     uint16_t *terms = reinterpret_cast<uint16_t *>(cur);
     char *ra = cur + l.terms, *rb = ra + l.a, *rattn = rb + l.b, *rlin = rattn + l.attn;
     char *rws = rlin + l.lin;
-    if (!dit_norm(d, x, mod, pend_y, pend_parts, pend_mod, terms, M, int(S), st))
+    // Self-attention in the f32x3 mode where the 256 x 256 f32-activation
+    // grid fills the GPU: LayerNorm + modulate leave f32 rows, and the fused
+    // q/k/v product writes the attention's prepared Q, K and V itself (its
+    // epilogue is the one-launch prologue), so no prologue pass reads the
+    // projection back.  The three operands take the projection's region.
+    // Against the library product on term rows plus the prologue this is
+    // even in time (1024 x 1024 sampler step 67.41 / 67.49 -> 67.30 / 67.31
+    // ms, interleaved): the hand-written product is slower than the library
+    // by about what the prologue took.  In the f32 mode, whose prologue
+    // writes f32 rows and no V^T (52 against 75 us), it was slower, and the
+    // library product stays.
+    float *proj = reinterpret_cast<float *>(ra), *o = reinterpret_cast<float *>(rb);
+    QkvPrep qp;
+    const size_t op_bytes = size_t(M) * c.heads * c.head_dim * 4;
+    const bool try_fused = kind == 0 && d->reps == 2 && d->attn == kAttnF32X3 &&
+                           c.head_dim == 128;
+    if (try_fused) {
+        qp.qo = proj;
+        qp.ko = reinterpret_cast<char *>(proj) + op_bytes;
+        qp.vo = reinterpret_cast<char *>(proj) + 2 * op_bytes;
+        qp.w[0] = bw.sa_qn;
+        qp.w[1] = bw.sa_kn;
+        qp.freqs = freqs;
+        qp.B = B;
+        qp.S = int(S);
+        qp.H = c.heads;
+        qp.mode = d->attn;
+    }
+    const bool fused_qkv = try_fused &&
+                           gemm_f32a_qkv_supported(reinterpret_cast<const float *>(terms), D,
+                                                   bw.w_qkv, d->ld_d, D, qp);
+    if (fused_qkv) {
+        if (!launch_ln_modulate(x, D, mod, 3 * int64_t(D), nullptr, nullptr, M, int(S), D, 1e-6f,
+                                st, x, pend_y, pend_y ? pend_mod + 2 * int64_t(D) : nullptr,
+                                3 * int64_t(D), 0, pend_parts, reinterpret_cast<float *>(terms)))
+            return false;
+    } else if (!dit_norm(d, x, mod, pend_y, pend_parts, pend_mod, terms, M, int(S), st)) {
         return false;
+    }
     if (kind == 2) {  // NumpyMLP (numpy_dit.py:304-317)
         const int hid = c.mlp_hidden;
         const bool ok1 = d->bf16 ? launch_linear_terms_bf16out(terms, bw.w_fc1, d->ld_d,
@@ -685,7 +722,6 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
     // NumpyAttention.forward (numpy_dit.py:268-297): self-attention projects
     // q, k and v in one product; cross-attention projects q and reads the
     // block's context cache.
-    float *proj = reinterpret_cast<float *>(ra), *o = reinterpret_cast<float *>(rb);
     AttnInputs in;
     in.B = B;
     in.S_q = int(S);
@@ -694,7 +730,16 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
     in.eps = 1e-6f;
     in.mode = d->attn;
     in.out = o;
-    if (kind == 0) {
+    if (fused_qkv) {
+        if (!launch_gemm_f32a_qkv(reinterpret_cast<const float *>(terms), D, bw.w_qkv, d->ld_d, D,
+                                  qp, st))
+            return false;
+        in.q_prep = qp.qo;
+        in.k_prep = qp.ko;
+        in.v_prep = qp.vo;
+        in.Bk = B;
+        in.S_kv = int(S);
+    } else if (kind == 0) {
         if (!dit_product(d, terms, d->ld_d, bw.w_qkv, d->ld_d, proj, 3 * HD, M, rws, l.ws, st))
             return false;
         in.q = proj;

@@ -37,6 +37,7 @@
 // order, K steps ascending: the order of the two-term kernel on term rows
 // (gemm_large.hip), so C is bit-identical to the split pass plus that kernel.
 #include "flash_tile.h"
+#include "rowmath.h"
 
 #include <algorithm>
 
@@ -57,18 +58,213 @@ constexpr int kFaACopies = kFaAEl / 512 / kFaWaves;  // 1 KiB windows per wave: 
 constexpr int kFaWCopies = kFaWEl / 512 / kFaWaves;  // 2
 constexpr int kFaNB = kFaBN / 32;                // accumulator blocks per wave
 
+// The attention operands written in place of C by the fused q/k/v
+// projection (launch_gemm_f32a_qkv): columns [0, HD) are q, [HD, 2HD) k,
+// [2HD, 3HD) v, HD = H * 128, so a 256-column tile holds two whole heads of
+// one of them.
+struct FaQkv {
+    void *qo, *ko, *vo;  // q / k rows; term V^T (terms) or f32 V rows
+    const float *w[2];   // RMSNorm weights of q / k, or null
+    const float *freqs;  // [S, 64, 2, 2] or null
+    int64_t sp;          // V^T row length (= S)
+    int S, H, HD;
+    float eps;
+    int terms;           // 1: [hi | lo] term rows and term V^T; 0: f32 rows
+};
+
 struct FaArgs {
     const float *a;   // [M][lda]
     const u16 *w;     // [N][ldw]
     float *c;         // [M][ldc]
     int64_t lda, ldw, ldc;
     int M, N, tiles_n, chunks;
+    FaQkv qkv;        // QKV kernels only
 };
+
+constexpr int kQkvPitch = 132;  // floats per staged row of a head block (128 + 4 against conflicts)
+static_assert(kFaWaves * 32 * kQkvPitch * 4 <= kFaStages * kFaStage * 2,
+              "a head block per wave fits the rings");
 
 __device__ __forceinline__ int fa_swz_a(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 __device__ __forceinline__ int fa_swz_w(int row) { return (row >> 2) & 3; }
 
-template <int TERMS>
+// Wait for this wave's LDS accesses; the compiler moves no memory access
+// across (rows written by other lanes of the wave are read next).
+__device__ __forceinline__ void wave_lds_fence()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+}
+
+// Epilogue of the fused q/k/v projection: this wave's 32 token rows of the
+// tile's two heads, in place of C.  Accumulators 4 hh .. 4 hh + 3 hold head
+// hh: lane (col, half) has column d = 32 (nb % 4) + col of the rows
+// acc_row(r, half).
+//   q, k: RMSNorm, RoPE and the row layout of prep_qkv_kernel (prologue.hip)
+//     with its arithmetic (no contraction): each head block goes through an
+//     LDS region of the wave; one lane per row sums the squares in index
+//     order, then 16 lanes per row take four rotation pairs each;
+//   v, terms: the term V^T straight from the accumulators.  In the key order
+//     vt_key_pos (bits 2 and 3 of the key swapped) the keys of registers
+//     8i .. 8i + 7 are positions 8 (2i + half) .. + 7 of the wave's 32-key
+//     block: one 16-byte chunk per term and register group;
+//   v, f32: dense V rows.
+// M and S are multiples of 32, so a wave's 32 rows lie in one batch entry
+// and are all inside or all past M (those write nothing).
+__device__ __forceinline__ void qkv_epilogue(const FaQkv &e, f32x16 (&acc)[kFaNB], float *lds,
+                                             int M, int row0, int col0, int wave, int lane)
+{
+#pragma clang fp contract(off)
+    const int col = lane & 31, half = lane >> 5;
+    const int mw = row0 + wave * 32;
+    const int part = col0 / e.HD;                // 0 q, 1 k, 2 v (uniform per workgroup)
+    const int head0 = (col0 - part * e.HD) / kD;  // the tile's first head
+    const int bb = mw / e.S, s0 = mw - bb * e.S;
+    if (part == 2) {
+        if (mw >= M)
+            return;
+        if (!e.terms) {
+            float *vo = static_cast<float *>(e.vo);
+#pragma unroll
+            for (int nb = 0; nb < kFaNB; ++nb) {
+                const int n = (head0 + (nb >> 2)) * kD + 32 * (nb & 3) + col;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    vo[int64_t(mw + acc_row(r, half)) * e.HD + n] = acc[nb][r];
+            }
+            return;
+        }
+        u16 *vt = static_cast<u16 *>(e.vo);
+#pragma unroll
+        for (int nb = 0; nb < kFaNB; ++nb) {
+            const int d = 32 * (nb & 3) + col;
+            u16 *vrow = vt + (int64_t(bb) * e.H + head0 + (nb >> 2)) * (2 * kD) * e.sp +
+                        int64_t(d) * e.sp + s0;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                unsigned hw[4], lw[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float x0 = acc[nb][8 * i + 2 * j], x1 = acc[nb][8 * i + 2 * j + 1];
+                    const unsigned short h0 = f32_to_bf16_rne(x0), h1 = f32_to_bf16_rne(x1);
+                    hw[j] = unsigned(h0) | (unsigned(h1) << 16);
+                    lw[j] = unsigned(bf16_lo_term(x0, h0)) | (unsigned(bf16_lo_term(x1, h1)) << 16);
+                }
+                u16 *dst = vrow + 8 * (2 * i + half);
+                *reinterpret_cast<u32x4 *>(dst) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+                *reinterpret_cast<u32x4 *>(dst + kD * e.sp) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+            }
+        }
+        return;
+    }
+    // Every wave has read its last fragments: the rings are free.
+    __syncthreads();
+    if (mw >= M)
+        return;
+    float *stg = lds + wave * (32 * kQkvPitch);
+    const float *w = e.w[part];
+    const int p0 = 4 * (lane & 15);
+    f32x4 wl = f32x4{1.f, 1.f, 1.f, 1.f}, wh = wl;
+    if (w) {
+        wl = *reinterpret_cast<const f32x4 *>(w + p0);
+        wh = *reinterpret_cast<const f32x4 *>(w + 64 + p0);
+    }
+    // The RoPE table entries of four of this lane's rows at a time, loaded
+    // together (the first four while the sums of squares run) instead of
+    // paying the load latency row by row.
+    f32x4 tab[2][4];
+    auto load_tab = [&](int it0) {
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const f32x4 *fq = reinterpret_cast<const f32x4 *>(
+                e.freqs + int64_t(s0 + (lane >> 4) + 4 * (it0 + it)) * 256 + 4 * p0);
+#pragma unroll
+            for (int ee = 0; ee < 4; ++ee)
+                tab[it][ee] = fq[ee];
+        }
+    };
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                stg[acc_row(r, half) * kQkvPitch + 32 * q + col] = acc[4 * hh + q][r];
+        wave_lds_fence();
+        if (e.freqs)
+            load_tab(0);
+        float inv = 0.0f;
+        if (lane < 32) {
+            float ss = 0.0f;
+            const float *row = stg + lane * kQkvPitch;
+#pragma unroll 8
+            for (int j = 0; j < 32; ++j) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(row + 4 * j);
+                ss = ss + v.x * v.x;
+                ss = ss + v.y * v.y;
+                ss = ss + v.z * v.z;
+                ss = ss + v.w * v.w;
+            }
+            inv = inv_rms(ss, kD, e.eps);
+        }
+        const int64_t h = head0 + hh;
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            if (it % 2 == 0 && it > 0 && e.freqs)
+                load_tab(it);
+            const int rr = (lane >> 4) + 4 * it;
+            const float fi = __shfl(inv, rr);
+            const float *row = stg + rr * kQkvPitch;
+            f32x4 ya = *reinterpret_cast<const f32x4 *>(row + p0);
+            f32x4 yb = *reinterpret_cast<const f32x4 *>(row + 64 + p0);
+            ya = ya * fi;
+            yb = yb * fi;
+            if (w) {
+                ya = ya * wl;
+                yb = yb * wh;
+            }
+            f32x4 lo = ya, hi = yb;
+            if (e.freqs) {
+#pragma unroll
+                for (int ee = 0; ee < 4; ++ee) {
+                    const f32x4 c = tab[it & 1][ee];  // [c00, c01, c10, c11] of pair p0 + ee
+                    lo[ee] = c.x * ya[ee] + c.y * yb[ee];
+                    hi[ee] = c.z * ya[ee] + c.w * yb[ee];
+                }
+            }
+            const int64_t orow = int64_t(mw + rr) * e.H + h;
+            void *out = part == 0 ? e.qo : e.ko;
+            if (e.terms) {
+                u16 *ob = static_cast<u16 *>(out) + orow * (2 * kD) + p0;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const f32x4 &y = k ? hi : lo;
+                    unsigned short hb[4];
+                    unsigned lb[4];
+#pragma unroll
+                    for (int ee = 0; ee < 4; ++ee) {
+                        hb[ee] = f32_to_bf16_rne(y[ee]);
+                        lb[ee] = bf16_lo_term(y[ee], hb[ee]);
+                    }
+                    *reinterpret_cast<uint2 *>(ob + 64 * k) =
+                        uint2{hb[0] | (unsigned(hb[1]) << 16), hb[2] | (unsigned(hb[3]) << 16)};
+                    *reinterpret_cast<uint2 *>(ob + 64 * k + kD) =
+                        uint2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
+                }
+            } else {
+                float *of = static_cast<float *>(out) + orow * kD + p0;
+                *reinterpret_cast<f32x4 *>(of) = lo;
+                *reinterpret_cast<f32x4 *>(of + 64) = hi;
+            }
+        }
+        // This wave's reads of the block are done before the next head's
+        // block overwrites it.
+        wave_lds_fence();
+    }
+}
+
+template <int TERMS, bool QKV>
 __global__ __launch_bounds__(kFaWaves * 64, 1) void gemm_f32a_kernel(FaArgs g)
 {
     __shared__ __attribute__((aligned(16))) u16 smem[kFaStages * kFaStage];
@@ -212,6 +408,10 @@ __global__ __launch_bounds__(kFaWaves * 64, 1) void gemm_f32a_kernel(FaArgs g)
             frags(smem + ((c + 1) % kFaStages) * kFaStage, 0, af[0], wf[0]);
     }
 
+    if (QKV) {
+        qkv_epilogue(g.qkv, acc, reinterpret_cast<float *>(smem), g.M, row0, col0, wave, lane);
+        return;
+    }
     // Lane (col, half) of accumulator nb holds C[m][n] for n = col0 + 32 nb +
     // col and m = row0 + wave * 32 + acc_row(r, half): for one register, 32
     // lanes cover 128 consecutive bytes of a row.  Nontemporal (streaming)
@@ -270,10 +470,58 @@ bool launch_gemm_f32a(const float *a, int64_t lda, const uint16_t *w, int64_t ld
     g.chunks = K / kFaBK;
     const dim3 grid(unsigned(((M + kFaBM - 1) / kFaBM) * g.tiles_n)), block(kFaWaves * 64);
     if (two_terms)
-        hipLaunchKernelGGL(gemm_f32a_kernel<2>, grid, block, 0, st, g);
+        hipLaunchKernelGGL((gemm_f32a_kernel<2, false>), grid, block, 0, st, g);
     else
-        hipLaunchKernelGGL(gemm_f32a_kernel<1>, grid, block, 0, st, g);
+        hipLaunchKernelGGL((gemm_f32a_kernel<1, false>), grid, block, 0, st, g);
     return hip_ok(hipGetLastError(), "gemm_f32a_kernel launch");
+}
+
+bool gemm_f32a_qkv_supported(const float *a, int64_t lda, const void *w, int64_t ldw, int K,
+                             const QkvPrep &p)
+{
+    const auto al = [](const void *x) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0; };
+    if ((p.mode != kAttnF32 && p.mode != kAttnF32X3) || p.B <= 0 || p.S <= 0 || p.H <= 0 ||
+        p.H % 2 || p.S % 64)
+        return false;
+    const int64_t M = int64_t(p.B) * p.S, HD = int64_t(p.H) * 128;
+    if (M > INT32_MAX || 3 * HD > INT32_MAX)
+        return false;
+    return p.qo && p.ko && p.vo && al(p.qo) && al(p.ko) && al(p.vo) && (!p.w[0] || al(p.w[0])) &&
+           (!p.w[1] || al(p.w[1])) && (!p.freqs || al(p.freqs)) &&
+           gemm_f32a_supported(int(M), int(3 * HD), K, lda, ldw, 3 * HD, a, w, p.qo);
+}
+
+bool launch_gemm_f32a_qkv(const float *a, int64_t lda, const uint16_t *w, int64_t ldw, int K,
+                          const QkvPrep &p, hipStream_t st)
+{
+    if (!gemm_f32a_qkv_supported(a, lda, w, ldw, K, p))
+        return fail("gemm_f32a_qkv: unsupported mode, shape or alignment (f32 or f32x3 mode, "
+                    "S a multiple of 64, an even head count, 16-byte aligned operands, a grid "
+                    "of at least 256 tiles)");
+    FaArgs g{};
+    g.a = a;
+    g.w = w;
+    g.lda = lda;
+    g.ldw = ldw;
+    g.M = p.B * p.S;
+    g.N = 3 * p.H * 128;
+    g.tiles_n = g.N / kFaBN;
+    g.chunks = K / kFaBK;
+    g.qkv.qo = p.qo;
+    g.qkv.ko = p.ko;
+    g.qkv.vo = p.vo;
+    g.qkv.w[0] = p.w[0];
+    g.qkv.w[1] = p.w[1];
+    g.qkv.freqs = p.freqs;
+    g.qkv.sp = p.S;
+    g.qkv.S = p.S;
+    g.qkv.H = p.H;
+    g.qkv.HD = p.H * 128;
+    g.qkv.eps = p.eps;
+    g.qkv.terms = p.mode == kAttnF32X3 ? 1 : 0;
+    const dim3 grid(unsigned(((g.M + kFaBM - 1) / kFaBM) * g.tiles_n)), block(kFaWaves * 64);
+    hipLaunchKernelGGL((gemm_f32a_kernel<2, true>), grid, block, 0, st, g);
+    return hip_ok(hipGetLastError(), "gemm_f32a_kernel (q/k/v) launch");
 }
 
 }  // namespace anima_hip

@@ -258,6 +258,29 @@ bool anima_hip_qkv_prologue_dev(const float *q, const float *k, const float *v, 
                                 const float *freqs, void *qo, void *ko, uint16_t *vt, int B,
                                 int S, int H, int D, float eps, int mode, void *stream);
 
+/* A self-attention's q/k/v projection and that prologue in one launch, for
+ * the f32 modes at large token counts: x [B*S][ldx] f32 activations times
+ * the stacked weights w_qkv [3*H*128][ldw] (bf16 bit patterns; q rows, then k,
+ * then v: NumpyAttention.forward's q_proj, k_proj, v_proj,
+ * anima_rt/scripts/numpy_dit.py:273-281) in anima_hip_linear_dev's exact
+ * two-term product, whose epilogue writes the attention operands in place of
+ * the projection: qo and ko as anima_hip_qkv_prologue_dev writes them (with
+ * RMSNorm weights q_norm_w / k_norm_w, NULL meaning 1, and RoPE with freqs
+ * [S, 64, 2, 2] or NULL) and vo as the term V^T (ANIMA_HIP_F32X3) or as
+ * dense f32 V rows [B, S, H, 128] (ANIMA_HIP_F32).  Bit-identical to
+ * anima_hip_linear_dev into [B*S][3*H*128] followed by
+ * anima_hip_qkv_prologue_dev on its column blocks (whose f32-mode V is the
+ * projection's v block itself).  Needs S a multiple of 64, H even, K a
+ * multiple of 32, ldx % 4 == 0, ldw % 8 == 0, 16-byte aligned operands, and
+ * (B*S/256) * (3*H/2) >= 256 (a grid that fills the GPU); other shapes are
+ * refused with a message (use the two separate entries).  No counterpart in
+ * the reference, whose projections and prologue are separate host steps. */
+bool anima_hip_qkv_projection_dev(const float *x, int64_t ldx, const uint16_t *w_qkv,
+                                  int64_t ldw, int K, const float *q_norm_w,
+                                  const float *k_norm_w, const float *freqs, void *qo, void *ko,
+                                  void *vo, int B, int S, int H, float eps, int mode,
+                                  void *stream);
+
 /* C[M,N] = A[M,K] . W[N,K]^T on device memory; W is bf16 bit patterns when
  * w_bf16 != 0, else f32; leading dimensions in elements. */
 bool anima_hip_gemm_dev(const float *a, int64_t lda, const void *w, int w_bf16, int64_t ldw,

@@ -160,6 +160,34 @@ def test_full_width_block_vs_oracle():
         assert err <= TOL[mode]
 
 
+def test_full_width_block_at_4096_tokens_vs_oracle(monkeypatch):
+    """One block at the Anima 2B widths on a 2 x 16 x 128 x 64 latent (2048
+    tokens per entry, M = 4096): the whole DiT's large-M paths, i.e. in the
+    f32x3 mode the fused q/k/v product whose epilogue writes the attention's
+    prepared operands (anima_hip_qkv_projection_dev's kernel), in the f32 mode
+    the library product on term rows plus the one-launch prologue, in bf16 the
+    bf16 ones; the 8-wave flash grids.  Against the oracle's composition with
+    its bf16 GEMMs taken as float64 products of the decoded weights
+    (tests/fullsize.py proj_f64: the same mathematics, rounded once) so that it
+    finishes in seconds, and its attention on host threads."""
+    import fullsize
+    monkeypatch.setattr(oracle, "gemm_bf16", fullsize.proj_f64)
+    cfg = dict(dim=2048, blocks=1, heads=16, head_dim=128, mlp_hidden=8192, ctx_dim=1024)
+    w = dit_weights.make(7301, **cfg)
+    rng = np.random.default_rng(7302)
+    x = rng.standard_normal((2, 16, 1, 128, 64), dtype=np.float32)
+    sigma = np.array([0.9, 0.6], np.float32)
+    ctx = rng.standard_normal((2, 64, 1024), dtype=np.float32) * np.float32(0.5)
+    print("dit full-width block, 4096 tokens", flush=True)
+    ref = oracle.dit_forward(x, sigma, ctx, w, 1, 16, 128, sdpa=fullsize.threaded_sdpa)
+    table, keep = _device_table(w)
+    for mode in (rt.F32X3, rt.F32, rt.BF16):
+        with AnimaDiT(table, DiTConfig.anima_2b(blocks=1), mode) as m:
+            err = _err(m.forward(x, sigma, ctx), ref)
+        print(f"  mode {mode}: normwise error {err:.3e}", flush=True)
+        assert err <= TOL[mode]
+
+
 def test_create_and_call_errors(gold):
     g, cfg, w = gold
     table, keep = _device_table(w)
