@@ -29,7 +29,9 @@
 // kernel (gemm_bf16.hip) at M <= 1024, the large-M kernel (gemm_large.hip)
 // for products of two term planes, hipBLASLt for the rest.  f32 mode feeds
 // them exact hi + lo bf16 terms of the f32 activations, bf16 mode rounds the
-// activations to bf16.
+// activations to bf16.  In the f32x3 mode at large M the self-attention's
+// q/k/v product is the f32-activation kernel's fused form (gemm_f32a.hip),
+// which writes the attention's prepared Q, K and V^T itself.
 #include "common.h"
 
 #include "anima_hip.h"
