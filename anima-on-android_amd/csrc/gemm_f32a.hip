@@ -41,9 +41,11 @@
 // projection whose epilogue writes the attention's prepared operands instead
 // of C: q and k rows after RMSNorm and RoPE with the one-launch prologue's
 // arithmetic, and the packed V^T, so no prologue pass reads the projection
-// back (4096 tokens, B = 2, H = 16: 363 us against 338 + 74 us for this
-// kernel's plain form plus the prologue; the epilogue costs about 24 us, 10 of
-// them the RoPE table's loads).
+// back (4096 tokens, B = 2, H = 16: 363-367 us against 338-345 + 74-75 us
+// for this kernel's plain form plus the prologue; the epilogue costs about
+// 24 us, 10 of them the RoPE table's loads, and is latency-bound: the
+// hardware bf16 conversion in place of the prologue's integer rounding,
+// which takes a third of its VALU work, did not change its time).
 #include "flash_tile.h"
 #include "rowmath.h"
 
@@ -112,7 +114,10 @@ __device__ __forceinline__ void wave_lds_fence()
 //   q, k: RMSNorm, RoPE and the row layout of prep_qkv_kernel (prologue.hip)
 //     with its arithmetic (no contraction): each head block goes through an
 //     LDS region of the wave; one lane per row sums the squares in index
-//     order, then 16 lanes per row take four rotation pairs each;
+//     order, then 16 lanes per row take four rotation pairs each.  The bf16
+//     terms come from the hardware conversion (split_terms4), which rounds
+//     to nearest even like the prologue's integer form: the same bits for
+//     every finite value and for the quiet NaNs that arithmetic produces;
 //   v, terms: the term V^T straight from the accumulators.  In the key order
 //     vt_key_pos (bits 2 and 3 of the key swapped) the keys of registers
 //     8i .. 8i + 7 are positions 8 (2i + half) .. + 7 of the wave's 32-key
@@ -151,17 +156,16 @@ __device__ __forceinline__ void qkv_epilogue(const FaQkv &e, f32x16 (&acc)[kFaNB
                         int64_t(d) * e.sp + s0;
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                unsigned hw[4], lw[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float x0 = acc[nb][8 * i + 2 * j], x1 = acc[nb][8 * i + 2 * j + 1];
-                    const unsigned short h0 = f32_to_bf16_rne(x0), h1 = f32_to_bf16_rne(x1);
-                    hw[j] = unsigned(h0) | (unsigned(h1) << 16);
-                    lw[j] = unsigned(bf16_lo_term(x0, h0)) | (unsigned(bf16_lo_term(x1, h1)) << 16);
-                }
+                uint2 h0, l0, h1, l1;
+                split_terms4(f32x4{acc[nb][8 * i], acc[nb][8 * i + 1], acc[nb][8 * i + 2],
+                                   acc[nb][8 * i + 3]},
+                             h0, l0);
+                split_terms4(f32x4{acc[nb][8 * i + 4], acc[nb][8 * i + 5], acc[nb][8 * i + 6],
+                                   acc[nb][8 * i + 7]},
+                             h1, l1);
                 u16 *dst = vrow + 8 * (2 * i + half);
-                *reinterpret_cast<u32x4 *>(dst) = u32x4{hw[0], hw[1], hw[2], hw[3]};
-                *reinterpret_cast<u32x4 *>(dst + kD * e.sp) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+                *reinterpret_cast<u32x4 *>(dst) = u32x4{h0.x, h0.y, h1.x, h1.y};
+                *reinterpret_cast<u32x4 *>(dst + kD * e.sp) = u32x4{l0.x, l0.y, l1.x, l1.y};
             }
         }
         return;
@@ -247,18 +251,10 @@ __device__ __forceinline__ void qkv_epilogue(const FaQkv &e, f32x16 (&acc)[kFaNB
                 u16 *ob = static_cast<u16 *>(out) + orow * (2 * kD) + p0;
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
-                    const f32x4 &y = k ? hi : lo;
-                    unsigned short hb[4];
-                    unsigned lb[4];
-#pragma unroll
-                    for (int ee = 0; ee < 4; ++ee) {
-                        hb[ee] = f32_to_bf16_rne(y[ee]);
-                        lb[ee] = bf16_lo_term(y[ee], hb[ee]);
-                    }
-                    *reinterpret_cast<uint2 *>(ob + 64 * k) =
-                        uint2{hb[0] | (unsigned(hb[1]) << 16), hb[2] | (unsigned(hb[3]) << 16)};
-                    *reinterpret_cast<uint2 *>(ob + 64 * k + kD) =
-                        uint2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
+                    uint2 th, tl;
+                    split_terms4(k ? hi : lo, th, tl);
+                    *reinterpret_cast<uint2 *>(ob + 64 * k) = th;
+                    *reinterpret_cast<uint2 *>(ob + 64 * k + kD) = tl;
                 }
             } else {
                 float *of = static_cast<float *>(out) + orow * kD + p0;
