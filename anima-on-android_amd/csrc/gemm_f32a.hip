@@ -182,9 +182,10 @@ __device__ __forceinline__ void qkv_epilogue(const FaQkv &e, f32x16 (&acc)[kFaNB
         wl = *reinterpret_cast<const f32x4 *>(w + p0);
         wh = *reinterpret_cast<const f32x4 *>(w + 64 + p0);
     }
-    // The RoPE table entries of four of this lane's rows at a time, loaded
-    // together (the first four while the sums of squares run) instead of
-    // paying the load latency row by row.
+    // The RoPE table entries of two of this lane's rows at a time, loaded
+    // together (the first two while the sums of squares run) instead of
+    // paying the load latency row by row; four rows at a time no longer fit
+    // the registers beside the second head's accumulators.
     f32x4 tab[2][4];
     auto load_tab = [&](int it0) {
 #pragma unroll
