@@ -486,6 +486,44 @@ def projection_gemm(c, mode, M=8192, N=2048, K=2048):
                     "f32 output on pre-split rows, split not timed"}
 
 
+def qkv_projection(c, mode, B=2, S=4096, H=16, D=128, K=2048):
+    """The self-attention's q/k/v product of one block at 4096 tokens, B=2,
+    with its attention prologue: fused (anima_hip_qkv_projection_dev, the
+    prologue as the GEMM's epilogue) against anima_hip_linear_dev into
+    [M][3HD] followed by anima_hip_qkv_prologue_dev (the same bits)."""
+    torch, lib, _lib = c.torch, c.lib, c._lib
+    from anima_hip.rope import generate_rope_freqs
+    M, HD = B * S, H * D
+    N = 3 * HD
+    x = c.randn((M, K), 7101)
+    w = c.bf16_bits(c.randn((N, K), 7102, 0.02))
+    qw, kw = (1.0 + 0.1 * c.randn((D,), 7103 + i) for i in range(2))
+    freqs = torch.from_numpy(generate_rope_freqs(64, 64)).to(c.dev)
+    y = torch.empty((M, N), device=c.dev)
+    q, k, v = (torch.empty((M * HD,), device=c.dev) for _ in range(3))
+    lin = Linear(c, mode, M, K)
+    eps = ct.c_float(1e-6)
+
+    def fused():
+        _lib.check(lib.anima_hip_qkv_projection_dev(
+            x.data_ptr(), K, w.data_ptr(), K, K, qw.data_ptr(), kw.data_ptr(), freqs.data_ptr(),
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), B, S, H, eps, mode, c.stp),
+            "qkv_projection_dev")
+
+    def separate():
+        lin(x, w, y)
+        _lib.check(lib.anima_hip_qkv_prologue_dev(
+            y.data_ptr(), y.data_ptr() + HD * 4, y.data_ptr() + 2 * HD * 4, N, qw.data_ptr(),
+            kw.data_ptr(), freqs.data_ptr(), q.data_ptr(), k.data_ptr(),
+            v.data_ptr() if mode != MODE["f32"] else None, B, S, H, D, eps, mode, c.stp),
+            "qkv_prologue_dev")
+
+    ms_f = c.time(fused, 20, 3)
+    ms_s = c.time(separate, 20, 3)
+    return {"fused_ms": round(ms_f, 4), "linear_plus_prologue_ms": round(ms_s, 4),
+            "note": f"{M}x{N}x{K} two-term product; its RMSNorm + RoPE rows and (f32x3) V^T"}
+
+
 def denoise_step_blocks(c, mode, blocks=28, B=2, S=4096, H=16, D=128, Dm=2048):
     """The attention sub-layers of one denoise step, as NumpyBlock.forward
     runs them (numpy_dit.py:236-247), on one device-resident residual stream
@@ -817,6 +855,8 @@ def main():
         for v in ("bf16", "f32x3", "f32"):
             res[v] = {f"{M}x{N}x{K}": projection_gemm(c, MODE[v], M, N, K)
                       for M, N, K in GEMM_SHAPES}
+            if v != "bf16":
+                res[v]["qkv_projection_with_prologue"] = qkv_projection(c, MODE[v])
         print(json.dumps({"config": "projection_gemm_f32_activations", "results": res}),
               flush=True)
         return
