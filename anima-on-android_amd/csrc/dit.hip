@@ -665,8 +665,8 @@ bool dit_sublayer(const anima_hip_dit *d, const BlockWeights &bw, int kind, floa
     // even in time (1024 x 1024 sampler step 67.41 / 67.49 -> 67.30 / 67.31
     // ms, interleaved): the hand-written product is slower than the library
     // by about what the prologue took.  In the f32 mode, whose prologue
-    // writes f32 rows and no V^T (52 against 75 us), it was slower, and the
-    // library product stays.
+    // writes f32 rows and no V^T (52 against 75 us), the steps measured even
+    // within noise, and the library product stays.
     float *proj = reinterpret_cast<float *>(ra), *o = reinterpret_cast<float *>(rb);
     QkvPrep qp;
     const size_t op_bytes = size_t(M) * c.heads * c.head_dim * 4;
